@@ -1,0 +1,311 @@
+#!/usr/bin/env python3
+"""GQA decode on one MI355X: us/step and achieved HBM GB/s (fraction of the 8 TB/s peak).
+
+Default workload: Llama-3-8B-shape GQA decode, batch 64, 32 query / 8 KV heads,
+head_dim 128, bf16, 8192 attended keys per sequence.  One step appends one K/V row per
+sequence (bit-exact row copy into the HBM cache) and then attends every cached row:
+split-KV decode kernel + log-sum-exp combine kernel.  Inputs are synthetic N(0, 1) bf16
+generated on the GPU and resident in HBM before the timed region; the cache (2 GiB) is
+far larger than the 256 MB Infinity Cache, so the rate is an HBM rate.
+
+Printed: ONE JSON line.  ``value`` is the whole-step algorithmic byte rate in GB/s;
+``roofline`` describes the dominant kernel (the split-KV decode kernel) from its HIP-event
+average over the timed steps; ``cpu_baseline`` times the fp32 NumPy oracle on the host on
+a bounded sample of the same workload.  Other decode workloads (C2, C3, C4) are measured
+the same way and reported under ``other_workloads``.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import re
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+METRIC = "GQA decode µs/step + achieved HBM GB/s (% of peak) at 1 MI355X"
+PROFILE_TRAFFIC = ROOT / "profiles" / "decode_ns_hbm_traffic.txt"
+WORKLOAD_NAMES = {
+    "ns": "llama3-8b-gqa-decode-b64-ctx8192",
+    "c2": "llama3-8b-gqa-decode-b1-ctx4096+1",
+    "c3": "llama3-8b-gqa-decode-b64-ragged-512..8192",
+    "c4": "long-context-gqa-decode-b4-64q8kv-ctx131072",
+    "c1": "board-shape-gqa-decode-b1-8q2kv-d64-ctx256",
+}
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+class DecodeBench:
+    """Owns one libgqa context and HBM-resident inputs for a decode workload."""
+
+    def __init__(self, w, device: int = 0, chunk: int = 0):
+        import torch
+        from lara_amd import _lib
+
+        self.torch = torch
+        self.lib = _lib.lib()
+        self._lib = _lib
+        self.w = w
+        self.lens = w.lengths()
+        L = int(self.lens.max())
+        cfg = _lib.GqaConfig(w.batch, w.n_q_heads, w.n_kv_heads, w.head_dim, L, 1, float(w.scale or 0.0), device)
+        self.ctx = ctypes.c_void_p()
+        _lib.check(self.lib.gqa_create(ctypes.byref(cfg), ctypes.byref(self.ctx)), "gqa_create")
+        if chunk:
+            _lib.check(self.lib.gqa_set_option(self.ctx, _lib.GQA_OPT_DECODE_CHUNK, chunk), "chunk")
+        dev = torch.device("cuda", device)
+        self.stream = torch.cuda.current_stream(dev)
+        sptr = ctypes.c_void_p(self.stream.cuda_stream)
+        self.sptr = sptr
+        g = torch.Generator(device=dev)
+        g.manual_seed(w.seed)
+        amp = float(w.amplitude)
+        # Fill the cache sequence by sequence from device buffers.
+        for b in range(w.batch):
+            n = int(self.lens[b])
+            k = torch.randn((w.n_kv_heads, n, w.head_dim), generator=g, device=dev) * amp
+            if w.outlier_fraction > 0:
+                rows = torch.rand((w.n_kv_heads, n), generator=g, device=dev) < w.outlier_fraction
+                k[rows] *= w.outlier_scale
+            k = k.to(torch.bfloat16)
+            v = (torch.randn((w.n_kv_heads, n, w.head_dim), generator=g, device=dev) * amp).to(torch.bfloat16)
+            _lib.check(self.lib.gqa_load_kv_device(self.ctx, b, 0, n, ctypes.c_void_p(k.data_ptr()),
+                                                   ctypes.c_void_p(v.data_ptr()), sptr), "load_kv_device")
+            del k, v
+        self.q = (torch.randn((w.batch, w.n_q_heads, w.head_dim), generator=g, device=dev) * amp).to(torch.bfloat16)
+        self.k_new = (torch.randn((w.batch, w.n_kv_heads, w.head_dim), generator=g, device=dev) * amp).to(
+            torch.bfloat16)
+        self.v_new = (torch.randn((w.batch, w.n_kv_heads, w.head_dim), generator=g, device=dev) * amp).to(
+            torch.bfloat16)
+        self.pos = torch.from_numpy((self.lens - 1).astype(np.int32)).to(dev)
+        self.lens_dev = torch.from_numpy(self.lens.astype(np.int32)).to(dev)
+        self.o = torch.empty((w.batch, w.n_q_heads, w.head_dim), dtype=torch.bfloat16, device=dev)
+        torch.cuda.synchronize(dev)
+
+    def step(self) -> None:
+        c = ctypes.c_void_p
+        rc = self.lib.gqa_append_kv_device(self.ctx, c(self.k_new.data_ptr()), c(self.v_new.data_ptr()),
+                                           c(self.pos.data_ptr()), self.sptr)
+        if rc:
+            self._lib.check(rc, "append")
+        rc = self.lib.gqa_decode_device(self.ctx, c(self.q.data_ptr()), c(self.lens_dev.data_ptr()),
+                                        c(self.o.data_ptr()), None, self.sptr)
+        if rc:
+            self._lib.check(rc, "decode")
+
+    def run(self, steps: int, warmup: int) -> dict:
+        torch = self.torch
+        _lib = self._lib
+        for _ in range(warmup):
+            self.step()
+        torch.cuda.synchronize()
+        # Per-kernel HIP events on the stream the kernels run on, over the timed steps.
+        _lib.check(self.lib.gqa_set_option(self.ctx, _lib.GQA_OPT_PROFILE, 1), "profile on")
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ev0.record(self.stream)
+        for _ in range(steps):
+            self.step()
+        ev1.record(self.stream)
+        torch.cuda.synchronize()
+        wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+        gpu_ms = ev0.elapsed_time(ev1) / steps
+        times = (ctypes.c_float * _lib.GQA_TIMER_COUNT)()
+        counts = (ctypes.c_int32 * _lib.GQA_TIMER_COUNT)()
+        _lib.check(self.lib.gqa_kernel_times(self.ctx, times, _lib.GQA_TIMER_COUNT), "kernel times")
+        _lib.check(self.lib.gqa_kernel_launch_counts(self.ctx, counts, _lib.GQA_TIMER_COUNT), "counts")
+        _lib.check(self.lib.gqa_set_option(self.ctx, _lib.GQA_OPT_PROFILE, 0), "profile off")
+        return {
+            "wall_ms_per_step": wall_ms,
+            "gpu_ms_per_step": gpu_ms,
+            "append_us": times[_lib.GQA_TIMER_APPEND],
+            "decode_us": times[_lib.GQA_TIMER_DECODE],
+            "combine_us": times[_lib.GQA_TIMER_COMBINE],
+            "decode_launches": int(counts[_lib.GQA_TIMER_DECODE]),
+        }
+
+    def close(self) -> None:
+        self.lib.gqa_destroy(self.ctx)
+        self.ctx = ctypes.c_void_p()
+
+
+def measure(name: str, steps: int, warmup: int, chunk: int = 0) -> dict:
+    from lara_amd.benchmark import WORKLOADS, decode_kernel_bytes, decode_step_bytes, HBM_PEAK_GBPS
+
+    w = WORKLOADS[name]
+    log(f"{name}: filling HBM cache")
+    bench = DecodeBench(w, chunk=chunk)
+    try:
+        log(f"{name}: warmup {warmup}, timing {steps} steps")
+        r = bench.run(steps, warmup)
+    finally:
+        bench.close()
+    lens = w.lengths()
+    step_bytes = decode_step_bytes(w.n_q_heads, w.n_kv_heads, w.head_dim, lens)
+    kern_bytes = decode_kernel_bytes(w.n_q_heads, w.n_kv_heads, w.head_dim, lens)
+    ms = r["wall_ms_per_step"]
+    r.update(
+        workload=name,
+        step_bytes=step_bytes,
+        decode_kernel_bytes=kern_bytes,
+        us_per_step=ms * 1e3,
+        step_gbps=step_bytes / (ms * 1e-3) / 1e9,
+        decode_kernel_gbps=kern_bytes / (r["decode_us"] * 1e-6) / 1e9 if r["decode_us"] > 0 else None,
+        tokens_per_s=w.batch / (ms * 1e-3),
+    )
+    r["step_frac_of_peak"] = r["step_gbps"] / HBM_PEAK_GBPS
+    if r["decode_kernel_gbps"]:
+        r["decode_kernel_frac_of_peak"] = r["decode_kernel_gbps"] / HBM_PEAK_GBPS
+    log(f"{name}: {r['us_per_step']:.1f} us/step, step {r['step_gbps']:.0f} GB/s, decode kernel "
+        f"{r['decode_us']:.1f} us = {r.get('decode_kernel_gbps') or 0:.0f} GB/s")
+    return r
+
+
+def read_traffic():
+    """HBM bytes per decode launch from the committed rocprofv3 PMC summary, if present."""
+    if not PROFILE_TRAFFIC.is_file():
+        return None
+    vals = dict(re.findall(r"^(\w+)\s*=\s*([0-9.eE+-]+)\s*$", PROFILE_TRAFFIC.read_text(), flags=re.M))
+    try:
+        return float(vals["hbm_bytes_per_launch"])
+    except (KeyError, ValueError):
+        return None
+
+
+def cpu_baseline(name: str, budget_s: float) -> dict:
+    """Time the fp32 NumPy oracle on host cores, one (sequence, kv head) unit at a time."""
+    from threadpoolctl import threadpool_limits
+
+    from lara_amd.benchmark import WORKLOADS, decode_step_bytes
+    from oracle.gqa_oracle import decode_fp32_baseline, fp32_to_bf16_u16
+
+    w = WORKLOADS[name]
+    lens = w.lengths()
+    rng = np.random.default_rng(w.seed + 1000)
+    units = [(b, h) for b in range(w.batch) for h in range(w.n_kv_heads)]
+    done_bytes = 0
+    n_units = 0
+    elapsed = 0.0
+    with threadpool_limits(limits=1):
+        for b, h in units:
+            L = int(lens[b])
+            q = fp32_to_bf16_u16(rng.standard_normal((w.group, w.head_dim), dtype=np.float32) * w.amplitude)
+            k = fp32_to_bf16_u16(rng.standard_normal((L, w.head_dim), dtype=np.float32) * w.amplitude)
+            v = fp32_to_bf16_u16(rng.standard_normal((L, w.head_dim), dtype=np.float32) * w.amplitude)
+            t0 = time.perf_counter()
+            decode_fp32_baseline(q, k, v, scale=w.scale)
+            elapsed += time.perf_counter() - t0
+            done_bytes += 2 * L * w.head_dim * 2 + 2 * w.group * w.head_dim * 2
+            n_units += 1
+            if elapsed >= budget_s:
+                break
+    gbps = done_bytes / elapsed / 1e9
+    step_bytes = decode_step_bytes(w.n_q_heads, w.n_kv_heads, w.head_dim, lens)
+    return {
+        "value": gbps,
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"{n_units} of {len(units)} (sequence, kv head) units of one step, fp32 NumPy oracle "
+                   f"(bf16 words in, stable softmax), 1 BLAS thread, {elapsed:.1f} s"),
+        "us_per_step_equivalent": step_bytes / (gbps * 1e9) * 1e6,
+        "host_cpu_count": os.cpu_count(),
+    }
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=100)
+    parser.add_argument("--warmup", type=int, default=10)
+    parser.add_argument("--workload", default="ns", choices=sorted(WORKLOAD_NAMES))
+    parser.add_argument("--chunk", type=int, default=0, help="keys per split-KV work-group (0 = auto)")
+    parser.add_argument("--others", default="c2,c3,c4", help="extra decode workloads to report ('' = none)")
+    parser.add_argument("--cpu-seconds", type=float, default=12.0)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    args = parser.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1).", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from lara_amd.benchmark import HBM_PEAK_GBPS, WORKLOADS
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU (gfx950)", file=sys.stderr)
+        return 1
+    main_r = measure(args.workload, args.steps, args.warmup, args.chunk)
+    others = {}
+    for name in [x for x in args.others.split(",") if x and x != args.workload]:
+        r = measure(name, max(10, args.steps // 2), max(2, args.warmup // 2))
+        others[name] = {k: r[k] for k in ("us_per_step", "step_gbps", "step_frac_of_peak", "decode_us",
+                                           "decode_kernel_gbps", "tokens_per_s")}
+    cpu = None
+    if not args.no_cpu_baseline:
+        log(f"cpu baseline ({args.cpu_seconds:.0f} s budget)")
+        cpu = cpu_baseline(args.workload, args.cpu_seconds)
+
+    w = WORKLOADS[args.workload]
+    achieved = main_r["decode_kernel_gbps"]
+    roofline = {
+        "bound": "hbm",
+        "kernel": "decode_split_kernel<128,4>" if w.head_dim == 128 and w.group == 4 else "decode_split_kernel",
+        "achieved": achieved,
+        "peak": HBM_PEAK_GBPS,
+        "unit": "GB/s",
+        "frac": achieved / HBM_PEAK_GBPS if achieved else None,
+        "traffic": read_traffic() if args.workload == "ns" else None,
+        "algorithmic_bytes_per_launch": main_r["decode_kernel_bytes"],
+        "avg_launch_us": main_r["decode_us"],
+        "launches_averaged": main_r["decode_launches"],
+    }
+    line = {
+        "metric": METRIC,
+        "value": main_r["step_gbps"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": main_r["wall_ms_per_step"],
+        "us_per_step": main_r["us_per_step"],
+        "frac_of_hbm_peak": main_r["step_frac_of_peak"],
+        "tokens_per_s": main_r["tokens_per_s"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic N(0,1) bf16 generated on the GPU, resident in HBM",
+        "config": {
+            "workload": WORKLOAD_NAMES[args.workload],
+            "batch": w.batch,
+            "n_q_heads": w.n_q_heads,
+            "n_kv_heads": w.n_kv_heads,
+            "head_dim": w.head_dim,
+            "attended_keys": int(w.lengths().max()),
+            "step": "append 1 K/V row per sequence + split-KV decode + LSE combine",
+            "accumulate": "fp32",
+        },
+        "kernels_us": {k: main_r[k] for k in ("append_us", "decode_us", "combine_us")},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "other_workloads": others,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

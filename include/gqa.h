@@ -1,0 +1,175 @@
+/*
+ * gqa.h -- C ABI of libgqa.so, the MI355X (gfx950) GQA streaming-attention engine.
+ *
+ * The library replaces the PS->PL hardware boundary of the LARA KV260 accelerator
+ * (CSR block + AXI-Stream K/V/Q sink + O source) with device-resident K/V caches in
+ * HBM and hand-written HIP kernels.  Every entry point below names the reference
+ * interface it stands in for (paths are relative to the reference repository).
+ *
+ * Conventions
+ *   - bf16 tensors cross the boundary as raw IEEE bf16 words (uint16_t), exactly the
+ *     words sw/attn_driver.py:88-98 (fp32_to_bf16_u16) produces.
+ *   - Host buffers are caller-owned; the library never frees or retains them.
+ *   - Every function returns a status code: 0 = OK, otherwise one of GQA_ERR_*.
+ *     Codes 0x01..0x12 keep the values of error_code_t (hw/rtl/pkg/attn_pkg.sv:279-286).
+ *   - Calls on one context are serialised by the caller (one transaction at a time,
+ *     like the reference's start_ready handshake).  Separate contexts are independent.
+ *   - K/V cache layout in HBM: [B][H_kv][L_cap][D] bf16, row stride D*2 bytes, where
+ *     L_cap = max_seq_len rounded up to a multiple of 64.  Element (b, h, t, d) lives at
+ *     ((b*H_kv + h)*L_cap + t)*D + d -- per (b, h) this is the token*HEAD_DIM + dim
+ *     addressing of hw/rtl/mem/kv_cache_ram.sv:77-83.
+ */
+#ifndef LARA_GQA_H
+#define LARA_GQA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---------------------------------------------------------- */
+#define GQA_OK                 0x00
+#define GQA_ERR_BAD_CFG        0x01 /* ERR_BAD_CFG    attn_pkg.sv:281 */
+#define GQA_ERR_BUSY_START     0x02 /* ERR_BUSY_START attn_pkg.sv:282 */
+#define GQA_ERR_STREAM_LEN     0x10 /* ERR_STREAM_LEN attn_pkg.sv:283: payload size mismatch */
+#define GQA_ERR_STREAM_DEST    0x11 /* ERR_STREAM_DEST attn_pkg.sv:284: bad destination/index */
+#define GQA_ERR_RESULT_LEN     0x12 /* ERR_RESULT_LEN attn_pkg.sv:285: output size mismatch */
+#define GQA_ERR_HIP            0x20 /* a HIP runtime call failed */
+#define GQA_ERR_OOM            0x21 /* device or pinned allocation failed */
+#define GQA_ERR_NO_DEVICE      0x22 /* no usable gfx950 device */
+#define GQA_ERR_NULL           0x23 /* required pointer argument is NULL */
+#define GQA_ERR_RANGE          0x24 /* length / position outside the configured capacity */
+#define GQA_ERR_TIMEOUT        0x25 /* gqa_wait deadline expired */
+#define GQA_ERR_NO_TRANSACTION 0x26 /* start/wait/read with nothing submitted */
+#define GQA_ERR_UNSUPPORTED    0x27 /* shape with no compiled kernel (head_dim, group) */
+
+/* STATUS word bits returned by gqa_status (CSR_STATUS, attn_driver.py:51-57). */
+#define GQA_STATUS_START_READY (1u << 0)
+#define GQA_STATUS_BUSY        (1u << 1)
+#define GQA_STATUS_DONE        (1u << 2)
+#define GQA_STATUS_ERROR       (1u << 3)
+
+/* Per-kernel timer slots reported by gqa_kernel_times. */
+#define GQA_TIMER_APPEND  0
+#define GQA_TIMER_DECODE  1
+#define GQA_TIMER_COMBINE 2
+#define GQA_TIMER_PREFILL 3
+#define GQA_TIMER_COUNT   4
+
+/* Tunables for gqa_set_option. */
+#define GQA_OPT_DECODE_CHUNK 1 /* keys per split-KV work-group (multiple of 64; 0 = auto) */
+#define GQA_OPT_PROFILE      2 /* 1 = time every kernel launch with HIP events (restarts the record) */
+
+typedef struct gqa_config {
+    int32_t batch;       /* B: sequences resident in the cache                         */
+    int32_t n_q_heads;   /* H_q  (N_Q_HEADS, attn_driver.py:65)                         */
+    int32_t n_kv_heads;  /* H_kv (N_KV_HEADS, attn_driver.py:66); H_q % H_kv == 0        */
+    int32_t head_dim;    /* D    (HEAD_DIM, attn_driver.py:63): 64 or 128               */
+    int32_t max_seq_len; /* cache rows per (b, kv head)  (MAX_SEQ_LEN generalised)      */
+    int32_t max_q_len;   /* largest prefill chunk / transaction length (>= 1)           */
+    float   scale;       /* softmax scale; 0 selects fp32(1/sqrt(D)) (attn_pkg.sv:241)   */
+    int32_t device;      /* HIP device ordinal                                          */
+} gqa_config;
+
+typedef struct gqa_ctx gqa_ctx;
+
+/* ---- lifetime ---------------------------------------------------------------
+ * gqa_create replaces AttentionAccelerator.__init__'s overlay/buffer set-up
+ * (sw/attn_driver.py:251-288): it allocates the HBM K/V cache, staging and split-KV
+ * workspace and a HIP stream.  gqa_destroy replaces close() (attn_driver.py:324-331). */
+int gqa_create(const gqa_config* cfg, gqa_ctx** out_ctx);
+int gqa_destroy(gqa_ctx* ctx);
+int gqa_get_config(const gqa_ctx* ctx, gqa_config* out_cfg);
+int gqa_set_option(gqa_ctx* ctx, int32_t option, int64_t value);
+const char* gqa_status_string(int32_t code);
+int gqa_device_count(int32_t* out_count);
+
+/* ---- K/V cache --------------------------------------------------------------
+ * gqa_load_kv replaces the KV branch of _service_request + _transfer(DEST_K_CACHE /
+ * DEST_V_CACHE) (attn_driver.py:378-422) and the cache write of kv_cache_ram.sv:77-83:
+ * k, v are host [H_kv][n][D] bf16 words written to rows start_pos..start_pos+n-1 of
+ * sequence b.  Bit-exact. */
+int gqa_load_kv(gqa_ctx* ctx, int32_t b, int32_t start_pos, int32_t n,
+                const uint16_t* k, const uint16_t* v);
+/* gqa_append_kv: one new row per sequence (no reference counterpart: the KV260 reloads
+ * the whole cache per transaction, attn_driver.py:418-422).  k_rows, v_rows are host
+ * [B][H_kv][D]; positions[b] is the row index, or -1 to leave sequence b untouched. */
+int gqa_append_kv(gqa_ctx* ctx, const uint16_t* k_rows, const uint16_t* v_rows,
+                  const int32_t* positions);
+/* gqa_read_kv: copy rows back to the host ([H_kv][n][D] each) for bit-exact checks. */
+int gqa_read_kv(gqa_ctx* ctx, int32_t b, int32_t start_pos, int32_t n,
+                uint16_t* k, uint16_t* v);
+
+/* ---- attention, synchronous host-pointer forms --------------------------------
+ * gqa_decode replaces run_attention (attn_driver.py:469-550) for one new query row per
+ * sequence: q is host [B][H_q][D]; ctx_lens[b] keys (rows 0..len-1) are attended,
+ * q_head h reads kv head h / (H_q/H_kv) (board_performance.py:182-191).  o is host
+ * [B][H_q][D] bf16 words (RNE), lse (optional) is host [B][H_q] natural-log
+ * log-sum-exp of the scaled scores.  A sequence with ctx_lens[b] == 0 outputs zeros
+ * (output_buffer.sv:276-277 semantics) and lse = -inf. */
+int gqa_decode(gqa_ctx* ctx, const uint16_t* q, const int32_t* ctx_lens,
+               uint16_t* o, float* lse);
+/* gqa_prefill replaces run_attention for a block of q_len query rows of sequence b
+ * against cache rows 0..kv_len-1: q and o are host head-major [H_q][q_len][D]
+ * (attn_driver.py:487-488, 464).  Query i sits at absolute position q_pos_base + i,
+ * key j at kv_pos_base + j; with causal != 0 key j is valid iff its position <= the
+ * query's (softmax_engine.sv:865-871).  Rows with no valid key output zeros. */
+int gqa_prefill(gqa_ctx* ctx, int32_t b, const uint16_t* q, int32_t q_len,
+                int32_t q_pos_base, int32_t kv_len, int32_t kv_pos_base, int32_t causal,
+                uint16_t* o, float* lse);
+
+/* ---- transaction protocol (configure / start / status / wait_done / readback) -----
+ * gqa_submit replaces configure() + the Q DMA (attn_driver.py:364-376, 423-432): it
+ * validates the transaction and stages q (host head-major [H_q][q_len][D]) in HBM.
+ * gqa_start replaces start() (attn_driver.py:434-437): it launches the kernels
+ * asynchronously; GQA_ERR_BUSY_START if a transaction is still running.
+ * gqa_status replaces status() (attn_driver.py:439-440) with the STATUS bits above.
+ * gqa_wait replaces wait_done (attn_driver.py:442-456): timeout_ms < 0 waits forever.
+ * gqa_read_output replaces readback_o (attn_driver.py:458-464); n_words must equal
+ * H_q*q_len*D (else GQA_ERR_RESULT_LEN, like CSR_RESULT_LEN).
+ * gqa_read_perf replaces read_perf (attn_driver.py:466-467): device-clock ticks of the
+ * last transaction (total, kernel-only, copy-only) at clock_mhz. */
+int gqa_submit(gqa_ctx* ctx, int32_t b, const uint16_t* q, int32_t q_len,
+               int32_t q_pos_base, int32_t kv_len, int32_t kv_pos_base, int32_t causal);
+int gqa_start(gqa_ctx* ctx);
+int gqa_status(gqa_ctx* ctx, uint32_t* out_status);
+int gqa_wait(gqa_ctx* ctx, int32_t timeout_ms);
+int gqa_read_output(gqa_ctx* ctx, uint16_t* o, int64_t n_words);
+int gqa_read_perf(gqa_ctx* ctx, uint64_t* total_ticks, uint64_t* kernel_ticks,
+                  uint64_t* copy_ticks, double* clock_mhz);
+
+/* ---- device-pointer forms (inputs already in HBM; stream may be NULL = ctx stream) --
+ * Same semantics as the host forms; all pointers are device pointers.  They enqueue
+ * and return without synchronising. */
+int gqa_append_kv_device(gqa_ctx* ctx, const void* k_rows, const void* v_rows,
+                         const int32_t* positions, void* stream);
+int gqa_decode_device(gqa_ctx* ctx, const void* q, const int32_t* ctx_lens,
+                      void* o, float* lse, void* stream);
+int gqa_prefill_device(gqa_ctx* ctx, int32_t b, const void* q, int32_t q_len,
+                       int32_t q_pos_base, int32_t kv_len, int32_t kv_pos_base,
+                       int32_t causal, void* o, float* lse, void* stream);
+/* gqa_load_kv_device: gqa_load_kv from device memory (k, v are [H_kv][n][D] in HBM). */
+int gqa_load_kv_device(gqa_ctx* ctx, int32_t b, int32_t start_pos, int32_t n,
+                       const void* k, const void* v, void* stream);
+/* Device addresses of the K and V caches ([B][H_kv][L_cap][D] bf16) and L_cap. */
+int gqa_cache_pointers(gqa_ctx* ctx, void** k_cache, void** v_cache, int32_t* l_cap);
+
+/* ---- timing ---------------------------------------------------------------------
+ * gqa_last_elapsed_us: elapsed time of the last synchronous call (HIP events on the ctx
+ * stream).  With GQA_OPT_PROFILE on, every kernel launch is bracketed by HIP events on
+ * the stream it runs on (up to 512 launches per kernel; setting the option again
+ * restarts the record); gqa_kernel_times returns each kernel's AVERAGE duration in
+ * microseconds, indexed by GQA_TIMER_* (0 when it did not run), and
+ * gqa_kernel_launch_counts the number of launches averaged.  These replace the PL cycle
+ * counters CSR_PERF_* (attn_pkg.sv:274-277) as the source of RunProfile timings. */
+int gqa_last_elapsed_us(gqa_ctx* ctx, float* out_us);
+int gqa_kernel_times(gqa_ctx* ctx, float* out_us, int32_t n);
+int gqa_kernel_launch_counts(gqa_ctx* ctx, int32_t* out_counts, int32_t n);
+int gqa_synchronize(gqa_ctx* ctx);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LARA_GQA_H */

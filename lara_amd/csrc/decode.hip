@@ -1,0 +1,383 @@
+// Split-KV GQA decode (flash-decoding) for CDNA4 / gfx950.
+//
+// Arithmetic contract (what the KV260 datapath computes, restated for one query row):
+//   s_k   = scale * sum_d q[d] * k_k[d]          (attn_tile.sv:176-248, attn_pkg.sv:241)
+//   p_k   = exp(s_k - m),  m = running max         (softmax_engine.sv:858-1073)
+//   O     = sum_k p_k v_k,  l = sum_k p_k            (attn_top.sv:462-625, output_buffer.sv:226-269)
+//   out   = bf16_rne(O / l), 0 when no key is valid (output_buffer.sv:271-286, attn_pkg.sv:618-626)
+// The KV260 works on 16-key sub-blocks of one Q tile at a time; here one work-group of
+// NW waves owns a contiguous chunk of keys of one (sequence, kv head) -- a "split" --
+// for all G query heads of the GQA group, so every K/V byte is read from HBM once.
+//
+// Work decomposition inside a work-group: keys are taken in rounds of RK rows; wave w
+// owns rounds w, w+NW, ...  Per round a wave
+//   1. has the round's K and V rows in registers (coalesced 16-byte loads, 1 KiB per
+//      wave instruction) and prefetches the next round's rows behind the math;
+//   2. writes K to a wave-private, XOR-swizzled LDS tile and reads it back transposed so
+//      that lane (g, k) owns the full dot product of head g with key k (v_dot2_f32_bf16,
+//      exact bf16 products, fp32 accumulation; no cross-lane reduction);
+//   3. updates the online softmax in the log2 domain (v_exp_f32) with a DPP max over the
+//      lanes of a head;
+//   4. hands p to the PV layout through LDS and accumulates O in fp32 registers, lane
+//      (r, c) owning dims 8c..8c+7 of every head for rows r, r+RPL, ...
+// At the end the waves merge in LDS.  A sequence that fits in one split writes the
+// bf16 output directly; otherwise each split writes an fp32 partial (O, m, l) and
+// decode_combine_kernel merges the splits with log-sum-exp weights.
+#include "gqa_internal.h"
+
+#include <math.h>
+
+namespace lara {
+namespace {
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+constexpr float kLn2 = 0.693147180559945309f;
+
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                           __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+    return __builtin_amdgcn_update_dpp(0.0f, x, CTRL, 0xF, 0xF, false);
+}
+
+// All-reduce over aligned groups of W consecutive lanes, W in {4, 8, 16, 32}.
+template <int W>
+__device__ __forceinline__ float group_max(float x) {
+    static_assert(W == 4 || W == 8 || W == 16 || W == 32, "group width");
+    x = fmaxf(x, dpp<0xB1>(x));                       // quad_perm [1,0,3,2]
+    x = fmaxf(x, dpp<0x4E>(x));                       // quad_perm [2,3,0,1]
+    if constexpr (W >= 8) x = fmaxf(x, dpp<0x141>(x)); // row_half_mirror
+    if constexpr (W >= 16) x = fmaxf(x, dpp<0x140>(x)); // row_mirror
+    if constexpr (W >= 32)
+        x = fmaxf(x, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x401F)));
+    return x;
+}
+
+template <int W>
+__device__ __forceinline__ float group_sum(float x) {
+    static_assert(W == 4 || W == 8 || W == 16 || W == 32, "group width");
+    x += dpp<0xB1>(x);
+    x += dpp<0x4E>(x);
+    if constexpr (W >= 8) x += dpp<0x141>(x);
+    if constexpr (W >= 16) x += dpp<0x140>(x);
+    if constexpr (W >= 32) x += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x401F));
+    return x;
+}
+
+// Orders a wave's LDS writes before its subsequent LDS reads of other lanes' data.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ void unpack_bf16x8(const u32x4& w, float* v) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        v[2 * i] = __uint_as_float(w[i] << 16);
+        v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+    }
+}
+
+__device__ __forceinline__ int clamp_len(int len, int l_max) {
+    return len < 0 ? 0 : (len > l_max ? l_max : len);
+}
+
+template <int D, int G, int NW>
+__global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
+    constexpr int NCH = D / 8;               // 16-byte words per K/V row
+    constexpr int QKG = 64 / G;              // lanes (keys) per head in the QK layout
+    constexpr int RK = QKG > 16 ? QKG : 16;  // keys per wave round
+    constexpr int NSUB = RK / QKG;           // QK sub-rounds per round
+    constexpr int RPL = 64 / NCH;            // rows covered by one wave-wide 1 KiB load
+    constexpr int NLD = RK / RPL;            // wave loads per round, for K and for V
+    constexpr int ROWS_PER_PERIOD = (2 * D >= 256) ? 1 : 256 / (2 * D);
+    static_assert(NLD >= 1 && NSUB >= 1, "tile shape");
+
+    const int split = blockIdx.x;
+    const int unit = blockIdx.y;  // b * H_kv + h
+    const int b = unit / a.n_kv_heads;
+    const int h = unit - b * a.n_kv_heads;
+    const int H_q = a.n_kv_heads * G;
+    const int L = clamp_len(a.lens[b], a.l_max);
+    const int n_splits = L > 0 ? (L + a.chunk - 1) / a.chunk : 1;
+    if (split >= n_splits) return;  // uniform across the work-group
+    const int k_begin = split * a.chunk;
+    const int k_end = min(L, k_begin + a.chunk);
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+
+    __shared__ __attribute__((aligned(16))) u32x4 lds_k[NW][RK * NCH];
+    __shared__ __attribute__((aligned(16))) float lds_p[NW][RK * G];
+    __shared__ float lds_o[NW][G][D];
+    __shared__ float lds_m[NW][G];
+    __shared__ float lds_l[NW][G];
+
+    // QK layout: lane = gq * QKG + kk holds all of q[head gq] as bf16 pairs.
+    const int gq = lane / QKG;
+    const int kk = lane - gq * QKG;
+    uint32_t qw[D / 2];
+    {
+        const u32x4* qp = reinterpret_cast<const u32x4*>(a.q + ((size_t)b * H_q + h * G + gq) * D);
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            const u32x4 t = qp[c];
+            qw[4 * c + 0] = t[0];
+            qw[4 * c + 1] = t[1];
+            qw[4 * c + 2] = t[2];
+            qw[4 * c + 3] = t[3];
+        }
+    }
+
+    // PV layout: lane = rpv * NCH + cpv holds dims 8*cpv..8*cpv+7 of rows rpv + RPL*j.
+    const int rpv = lane / NCH;
+    const int cpv = lane - rpv * NCH;
+    float acc[G][8];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[g][i] = 0.f;
+    float m_run = -INFINITY;  // running max (log2 units) of head gq, uniform over its lanes
+    float l_lane = 0.f;       // this lane's share of the running sum of head gq
+
+    const size_t row0 = (size_t)unit * a.l_cap;
+    const u32x4* kbase = reinterpret_cast<const u32x4*>(a.kc) + row0 * NCH;
+    const u32x4* vbase = reinterpret_cast<const u32x4*>(a.vc) + row0 * NCH;
+
+    // Rounds start at multiples of RK and l_cap is a multiple of 64, so every row a round
+    // touches lies inside the sequence's cache region; rows >= k_end are masked below.
+    const int n_rounds = (k_end - k_begin + RK - 1) / RK;
+    u32x4 kr[NLD], vr[NLD];
+    int r = wave;
+    if (r < n_rounds) {
+        const int key0 = k_begin + r * RK;
+#pragma unroll
+        for (int j = 0; j < NLD; ++j) {
+            const size_t off = (size_t)(key0 + j * RPL + rpv) * NCH + cpv;
+            kr[j] = kbase[off];
+            vr[j] = vbase[off];
+        }
+    }
+    for (; r < n_rounds; r += NW) {
+        const int key0 = k_begin + r * RK;
+        // 1. K -> LDS, swizzled so that the transposed reads below are conflict-free.
+#pragma unroll
+        for (int j = 0; j < NLD; ++j) {
+            const int row = j * RPL + rpv;
+            lds_k[wave][row * NCH + (cpv ^ ((row / ROWS_PER_PERIOD) % NCH))] = kr[j];
+        }
+        u32x4 vcur[NLD];
+#pragma unroll
+        for (int j = 0; j < NLD; ++j) vcur[j] = vr[j];
+        if (key0 + RK > k_end) {
+            // Partial last round: rows past the sequence may hold stale words.
+#pragma unroll
+            for (int j = 0; j < NLD; ++j)
+                if (key0 + j * RPL + rpv >= k_end) vcur[j] = u32x4{0u, 0u, 0u, 0u};
+        }
+        // Prefetch the next round of this wave.
+        if (r + NW < n_rounds) {
+            const int key1 = key0 + NW * RK;
+#pragma unroll
+            for (int j = 0; j < NLD; ++j) {
+                const size_t off = (size_t)(key1 + j * RPL + rpv) * NCH + cpv;
+                kr[j] = kbase[off];
+                vr[j] = vbase[off];
+            }
+        }
+        wave_lds_sync();
+
+        // 2. Scores: lane (gq, kk) dots q[gq] with key row sub*QKG + kk.
+        float s[NSUB];
+#pragma unroll
+        for (int sub = 0; sub < NSUB; ++sub) {
+            const int row = sub * QKG + kk;
+            const int swz = (row / ROWS_PER_PERIOD) % NCH;
+            float dot = 0.f;
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) {
+                const u32x4 kw = lds_k[wave][row * NCH + (c ^ swz)];
+                dot = dot2_bf16(qw[4 * c + 0], kw[0], dot);
+                dot = dot2_bf16(qw[4 * c + 1], kw[1], dot);
+                dot = dot2_bf16(qw[4 * c + 2], kw[2], dot);
+                dot = dot2_bf16(qw[4 * c + 3], kw[3], dot);
+            }
+            s[sub] = (key0 + row < k_end) ? dot * a.scale_log2 : -INFINITY;
+        }
+
+        // 3. Online softmax for head gq.
+        float mx = s[0];
+#pragma unroll
+        for (int sub = 1; sub < NSUB; ++sub) mx = fmaxf(mx, s[sub]);
+        mx = group_max<QKG>(mx);
+        const float m_new = fmaxf(m_run, mx);
+        const bool none = (m_new == -INFINITY);  // every key so far is masked
+        const float corr = none ? 1.f : fast_exp2(m_run - m_new);
+        float psum = 0.f;
+#pragma unroll
+        for (int sub = 0; sub < NSUB; ++sub) {
+            const float p = (s[sub] == -INFINITY) ? 0.f : fast_exp2(s[sub] - m_new);
+            lds_p[wave][(sub * QKG + kk) * G + gq] = p;
+            psum += p;
+        }
+        l_lane = l_lane * corr + psum;
+        m_run = m_new;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float cg = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(corr), g * QKG));
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[g][i] *= cg;
+        }
+        wave_lds_sync();
+
+        // 4. O += p * V in the PV layout.
+#pragma unroll
+        for (int j = 0; j < NLD; ++j) {
+            const int row = j * RPL + rpv;
+            float p[G];
+#pragma unroll
+            for (int g = 0; g < G; ++g) p[g] = lds_p[wave][row * G + g];
+            float v[8];
+            unpack_bf16x8(vcur[j], v);
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) acc[g][i] = fmaf(p[g], v[i], acc[g][i]);
+        }
+    }
+
+    // ---- merge the waves of this work-group ----
+    const float l_head = group_sum<QKG>(l_lane);
+#pragma unroll
+    for (int off = NCH; off < 64; off <<= 1)
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[g][i] += __shfl_xor(acc[g][i], off);
+    if (rpv == 0) {
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) lds_o[wave][g][cpv * 8 + i] = acc[g][i];
+    }
+    if (kk == 0) {
+        lds_m[wave][gq] = m_run;
+        lds_l[wave][gq] = l_head;
+    }
+    __syncthreads();
+
+    const bool single = (n_splits == 1);
+    for (int idx = threadIdx.x; idx < G * D; idx += NW * 64) {
+        const int g = idx / D;
+        const int d = idx - g * D;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) M = fmaxf(M, lds_m[w][g]);
+        float O = 0.f, Ls = 0.f;
+        if (M != -INFINITY) {
+#pragma unroll
+            for (int w = 0; w < NW; ++w) {
+                const float sc = fast_exp2(lds_m[w][g] - M);
+                O = fmaf(sc, lds_o[w][g][d], O);
+                Ls = fmaf(sc, lds_l[w][g], Ls);
+            }
+        }
+        if (single) {
+            const size_t row = (size_t)b * H_q + h * G + g;
+            a.out[row * D + d] = f32_to_bf16_rne(Ls > 0.f ? O / Ls : 0.f);
+            if (d == 0 && a.lse != nullptr) a.lse[row] = Ls > 0.f ? (M + log2f(Ls)) * kLn2 : -INFINITY;
+        } else {
+            const size_t pidx = ((size_t)unit * a.max_splits + split) * G + g;
+            a.part_o[pidx * D + d] = O;
+            if (d == 0) {
+                a.part_ml[pidx * 2] = M;
+                a.part_ml[pidx * 2 + 1] = Ls;
+            }
+        }
+    }
+}
+
+// Log-sum-exp merge of the split partials of one (sequence, kv head).
+template <int D, int G>
+__global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
+    const int unit = blockIdx.x;
+    const int b = unit / a.n_kv_heads;
+    const int h = unit - b * a.n_kv_heads;
+    const int L = clamp_len(a.lens[b], a.l_max);
+    const int n_splits = L > 0 ? (L + a.chunk - 1) / a.chunk : 1;
+    if (n_splits <= 1) return;
+    const int H_q = a.n_kv_heads * G;
+    for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
+        const int g = idx / D;
+        const int d = idx - g * D;
+        const size_t base = (size_t)unit * a.max_splits * G + g;  // partial index of split 0
+        float M = -INFINITY;
+        for (int sp = 0; sp < n_splits; ++sp) M = fmaxf(M, a.part_ml[(base + (size_t)sp * G) * 2]);
+        float O = 0.f, Ls = 0.f;
+        if (M != -INFINITY) {
+            for (int sp = 0; sp < n_splits; ++sp) {
+                const size_t pidx = base + (size_t)sp * G;
+                const float sc = fast_exp2(a.part_ml[pidx * 2] - M);
+                O = fmaf(sc, a.part_o[pidx * D + d], O);
+                Ls = fmaf(sc, a.part_ml[pidx * 2 + 1], Ls);
+            }
+        }
+        const size_t row = (size_t)b * H_q + h * G + g;
+        a.out[row * D + d] = f32_to_bf16_rne(Ls > 0.f ? O / Ls : 0.f);
+        if (d == 0 && a.lse != nullptr) a.lse[row] = Ls > 0.f ? (M + log2f(Ls)) * kLn2 : -INFINITY;
+    }
+}
+
+constexpr int kDecodeWaves = 4;
+
+template <int D, int G>
+hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t s) {
+    dim3 grid(a.max_splits, a.batch * a.n_kv_heads);
+    hipLaunchKernelGGL((decode_split_kernel<D, G, kDecodeWaves>), grid, dim3(kDecodeWaves * 64), 0, s, a);
+    return hipGetLastError();
+}
+
+template <int D, int G>
+hipError_t launch_combine_t(const DecodeArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL((decode_combine_kernel<D, G>), dim3(a.batch * a.n_kv_heads), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool decode_supported(int head_dim, int group) {
+    return (head_dim == 64 || head_dim == 128) && (group == 2 || group == 4 || group == 8 || group == 16);
+}
+
+#define LARA_DISPATCH_DG(FN, D_, G_, ...)                              \
+    do {                                                               \
+        if ((D_) == 128) {                                             \
+            if ((G_) == 4) return FN<128, 4>(__VA_ARGS__);             \
+            if ((G_) == 8) return FN<128, 8>(__VA_ARGS__);             \
+            if ((G_) == 2) return FN<128, 2>(__VA_ARGS__);             \
+            if ((G_) == 16) return FN<128, 16>(__VA_ARGS__);           \
+        } else if ((D_) == 64) {                                       \
+            if ((G_) == 4) return FN<64, 4>(__VA_ARGS__);              \
+            if ((G_) == 8) return FN<64, 8>(__VA_ARGS__);              \
+            if ((G_) == 2) return FN<64, 2>(__VA_ARGS__);              \
+            if ((G_) == 16) return FN<64, 16>(__VA_ARGS__);            \
+        }                                                              \
+        return hipErrorInvalidValue;                                   \
+    } while (0)
+
+hipError_t launch_decode(int head_dim, int group, const DecodeArgs& a, hipStream_t s) {
+    LARA_DISPATCH_DG(launch_decode_t, head_dim, group, a, s);
+}
+
+hipError_t launch_combine(int head_dim, int group, const DecodeArgs& a, hipStream_t s) {
+    LARA_DISPATCH_DG(launch_combine_t, head_dim, group, a, s);
+}
+
+}  // namespace lara

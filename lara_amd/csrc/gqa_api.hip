@@ -1,0 +1,667 @@
+// C ABI of libgqa.so: context lifetime, validation, staging and the transaction protocol.
+// Declarations and the reference interface each entry point replaces are in include/gqa.h.
+#include "../../include/gqa.h"
+#include "gqa_internal.h"
+
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <time.h>
+
+using namespace lara;
+
+namespace {
+
+constexpr int kMinChunk = 256;     // smallest split (keys); multiple of every decode round size
+constexpr int kTargetDecodeWgs = 2048;
+
+struct Txn {
+    int valid = 0;     // a transaction has been submitted (configure + Q staged)
+    int running = 0;   // launched, completion not yet observed
+    int32_t b = 0, q_len = 0, q_pos_base = 0, kv_len = 0, kv_pos_base = 0, causal = 1;
+    float kernel_us = 0.f, total_us = 0.f, copy_us = 0.f;
+};
+
+}  // namespace
+
+struct gqa_ctx {
+    gqa_config cfg{};
+    int group = 1;
+    int l_cap = 0;
+    int max_splits_cap = 0;
+    float scale = 0.f;
+    hipStream_t stream = nullptr;
+    uint16_t* k_cache = nullptr;
+    uint16_t* v_cache = nullptr;
+    float* part_o = nullptr;
+    float* part_ml = nullptr;
+    uint16_t* q_dev = nullptr;   // staging: max(B*H_q*D, H_q*max_q_len*D) words
+    uint16_t* o_dev = nullptr;   // same size as q_dev
+    float* lse_dev = nullptr;    // max(B*H_q, H_q*max_q_len)
+    int32_t* lens_dev = nullptr; // [B]
+    uint16_t* rows_dev = nullptr;  // [2][B][H_kv][D] append staging
+    uint16_t* o_pinned = nullptr;  // transaction output (host, pinned)
+    size_t stage_words = 0;
+    size_t lse_words = 0;
+    int chunk_opt = 0;
+    int profile = 0;
+    hipEvent_t ev_begin = nullptr, ev_end = nullptr;
+    // Profiling: a pool of event pairs per timer slot, filled launch by launch.
+    hipEvent_t* ev_pool[GQA_TIMER_COUNT] = {};
+    int ev_count[GQA_TIMER_COUNT] = {};
+    hipEvent_t ev_t[4] = {};     // transaction: copy-in start, kernel start, kernel end, done
+    float last_us = 0.f;
+    double clock_mhz = 0.0;
+    Txn txn;
+};
+
+namespace {
+
+#define HIP_TRY(expr)                          \
+    do {                                       \
+        hipError_t err__ = (expr);             \
+        if (err__ != hipSuccess) {             \
+            last_hip_error(err__, #expr);      \
+            return GQA_ERR_HIP;                \
+        }                                      \
+    } while (0)
+
+thread_local char g_last_error[256];
+
+void last_hip_error(hipError_t e, const char* what) {
+    snprintf(g_last_error, sizeof(g_last_error), "%s: %s", what, hipGetErrorString(e));
+}
+
+inline size_t kv_words(const gqa_ctx* c) {
+    return (size_t)c->cfg.batch * c->cfg.n_kv_heads * c->l_cap * c->cfg.head_dim;
+}
+
+hipStream_t pick_stream(gqa_ctx* c, void* s) { return s ? (hipStream_t)s : c->stream; }
+
+int choose_chunk(const gqa_ctx* c, int max_len) {
+    if (c->chunk_opt > 0) return c->chunk_opt;
+    const int units = c->cfg.batch * c->cfg.n_kv_heads;
+    int splits = (kTargetDecodeWgs + units - 1) / units;
+    if (splits < 1) splits = 1;
+    int chunk = (max_len + splits - 1) / splits;
+    chunk = ((chunk + kMinChunk - 1) / kMinChunk) * kMinChunk;
+    if (chunk < kMinChunk) chunk = kMinChunk;
+    return chunk;
+}
+
+constexpr int kProfileLaunches = 512;  // event pairs kept per timer slot
+
+void timer_begin(gqa_ctx* c, int slot, hipStream_t s) {
+    if (c->profile && c->ev_count[slot] < kProfileLaunches)
+        (void)hipEventRecord(c->ev_pool[slot][2 * c->ev_count[slot]], s);
+}
+
+void timer_end(gqa_ctx* c, int slot, hipStream_t s) {
+    if (c->profile && c->ev_count[slot] < kProfileLaunches) {
+        (void)hipEventRecord(c->ev_pool[slot][2 * c->ev_count[slot] + 1], s);
+        c->ev_count[slot] += 1;
+    }
+}
+
+void timers_reset(gqa_ctx* c) {
+    for (int i = 0; i < GQA_TIMER_COUNT; ++i) c->ev_count[i] = 0;
+}
+
+int profile_enable(gqa_ctx* c, int on) {
+    if (on) {
+        for (int i = 0; i < GQA_TIMER_COUNT; ++i) {
+            if (c->ev_pool[i]) continue;
+            c->ev_pool[i] = (hipEvent_t*)calloc(2 * kProfileLaunches, sizeof(hipEvent_t));
+            if (!c->ev_pool[i]) return GQA_ERR_OOM;
+            for (int e = 0; e < 2 * kProfileLaunches; ++e) HIP_TRY(hipEventCreate(&c->ev_pool[i][e]));
+        }
+    }
+    c->profile = on ? 1 : 0;
+    return GQA_OK;
+}
+
+int run_decode(gqa_ctx* c, const void* q, const int32_t* lens, void* o, float* lse, hipStream_t s,
+               int max_len) {
+    const int chunk = choose_chunk(c, max_len);
+    int max_splits = max_len > 0 ? (max_len + chunk - 1) / chunk : 1;
+    if (max_splits > c->max_splits_cap) return GQA_ERR_RANGE;
+    DecodeArgs a{};
+    a.q = (const uint16_t*)q;
+    a.kc = c->k_cache;
+    a.vc = c->v_cache;
+    a.lens = lens;
+    a.batch = c->cfg.batch;
+    a.n_kv_heads = c->cfg.n_kv_heads;
+    a.l_cap = c->l_cap;
+    a.l_max = c->cfg.max_seq_len;
+    a.chunk = chunk;
+    a.max_splits = max_splits;
+    a.scale_log2 = c->scale * 1.4426950408889634f;
+    a.part_o = c->part_o;
+    a.part_ml = c->part_ml;
+    a.out = (uint16_t*)o;
+    a.lse = lse;
+    timer_begin(c, GQA_TIMER_DECODE, s);
+    HIP_TRY(launch_decode(c->cfg.head_dim, c->group, a, s));
+    timer_end(c, GQA_TIMER_DECODE, s);
+    if (max_splits > 1) {
+        timer_begin(c, GQA_TIMER_COMBINE, s);
+        HIP_TRY(launch_combine(c->cfg.head_dim, c->group, a, s));
+        timer_end(c, GQA_TIMER_COMBINE, s);
+    }
+    return GQA_OK;
+}
+
+int check_prefill_args(const gqa_ctx* c, int32_t b, int32_t q_len, int32_t q_pos_base, int32_t kv_len,
+                       int32_t kv_pos_base) {
+    if (b < 0 || b >= c->cfg.batch) return GQA_ERR_STREAM_DEST;
+    if (q_len < 1 || q_len > c->cfg.max_q_len) return GQA_ERR_RANGE;
+    if (kv_len < 0 || kv_len > c->cfg.max_seq_len) return GQA_ERR_RANGE;
+    if (q_pos_base < 0 || kv_pos_base < 0) return GQA_ERR_RANGE;
+    if ((int64_t)q_pos_base + q_len > INT32_MAX || (int64_t)kv_pos_base + kv_len > INT32_MAX)
+        return GQA_ERR_RANGE;
+    return GQA_OK;
+}
+
+int run_prefill(gqa_ctx* c, int32_t b, const void* q, int32_t q_len, int32_t q_pos_base, int32_t kv_len,
+                int32_t kv_pos_base, int32_t causal, void* o, float* lse, hipStream_t s) {
+    if (!prefill_supported(c->cfg.head_dim, c->group)) return GQA_ERR_UNSUPPORTED;
+    PrefillArgs a{};
+    const size_t seq_off = (size_t)b * c->cfg.n_kv_heads * c->l_cap * c->cfg.head_dim;
+    a.q = (const uint16_t*)q;
+    a.kc = c->k_cache + seq_off;
+    a.vc = c->v_cache + seq_off;
+    a.n_q_heads = c->cfg.n_q_heads;
+    a.n_kv_heads = c->cfg.n_kv_heads;
+    a.l_cap = c->l_cap;
+    a.q_len = q_len;
+    a.kv_len = kv_len;
+    a.q_pos_base = q_pos_base;
+    a.kv_pos_base = kv_pos_base;
+    a.causal = causal ? 1 : 0;
+    a.scale_log2 = c->scale * 1.4426950408889634f;
+    a.out = (uint16_t*)o;
+    a.lse = lse;
+    timer_begin(c, GQA_TIMER_PREFILL, s);
+    HIP_TRY(launch_prefill(c->cfg.head_dim, c->group, a, s));
+    timer_end(c, GQA_TIMER_PREFILL, s);
+    return GQA_OK;
+}
+
+int finish_sync(gqa_ctx* c) {
+    HIP_TRY(hipEventRecord(c->ev_end, c->stream));
+    HIP_TRY(hipEventSynchronize(c->ev_end));
+    float ms = 0.f;
+    HIP_TRY(hipEventElapsedTime(&ms, c->ev_begin, c->ev_end));
+    c->last_us = ms * 1000.f;
+    return GQA_OK;
+}
+
+int txn_idle(gqa_ctx* c) {
+    // A transaction in flight blocks every other use of the context's staging buffers.
+    if (!c->txn.running) return GQA_OK;
+    hipError_t e = hipEventQuery(c->ev_t[3]);
+    if (e == hipErrorNotReady) return GQA_ERR_BUSY_START;
+    if (e != hipSuccess) {
+        last_hip_error(e, "hipEventQuery");
+        return GQA_ERR_HIP;
+    }
+    return GQA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* gqa_status_string(int32_t code) {
+    switch (code) {
+        case GQA_OK: return "ok";
+        case GQA_ERR_BAD_CFG: return "bad configuration";
+        case GQA_ERR_BUSY_START: return "start while a transaction is running";
+        case GQA_ERR_STREAM_LEN: return "payload length does not match the configured shape";
+        case GQA_ERR_STREAM_DEST: return "bad destination (sequence index)";
+        case GQA_ERR_RESULT_LEN: return "result length does not match the transaction";
+        case GQA_ERR_HIP: return g_last_error[0] ? g_last_error : "HIP runtime error";
+        case GQA_ERR_OOM: return "out of device or pinned host memory";
+        case GQA_ERR_NO_DEVICE: return "no usable gfx950 device";
+        case GQA_ERR_NULL: return "required pointer is NULL";
+        case GQA_ERR_RANGE: return "length or position outside the configured capacity";
+        case GQA_ERR_TIMEOUT: return "timed out waiting for the transaction";
+        case GQA_ERR_NO_TRANSACTION: return "no transaction has been submitted";
+        case GQA_ERR_UNSUPPORTED: return "no kernel compiled for this head_dim / group size";
+        default: return "unknown status";
+    }
+}
+
+int gqa_device_count(int32_t* out_count) {
+    if (!out_count) return GQA_ERR_NULL;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    *out_count = (e == hipSuccess) ? n : 0;
+    return GQA_OK;
+}
+
+int gqa_create(const gqa_config* cfg, gqa_ctx** out_ctx) {
+    if (!cfg || !out_ctx) return GQA_ERR_NULL;
+    *out_ctx = nullptr;
+    const gqa_config& k = *cfg;
+    if (k.batch < 1 || k.n_q_heads < 1 || k.n_kv_heads < 1 || k.n_q_heads % k.n_kv_heads != 0 ||
+        k.max_seq_len < 1 || k.max_q_len < 1 || !(k.scale >= 0.f) || !isfinite(k.scale))
+        return GQA_ERR_BAD_CFG;
+    const int group = k.n_q_heads / k.n_kv_heads;
+    if (!decode_supported(k.head_dim, group)) return GQA_ERR_UNSUPPORTED;
+
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n < 1) return GQA_ERR_NO_DEVICE;
+    if (k.device < 0 || k.device >= n) return GQA_ERR_NO_DEVICE;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, k.device) != hipSuccess) return GQA_ERR_NO_DEVICE;
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) return GQA_ERR_NO_DEVICE;
+    HIP_TRY(hipSetDevice(k.device));
+
+    gqa_ctx* c = new gqa_ctx();
+    c->cfg = k;
+    c->group = group;
+    c->l_cap = ((k.max_seq_len + 63) / 64) * 64;
+    c->max_splits_cap = (c->l_cap + kMinChunk - 1) / kMinChunk;
+    c->scale = k.scale > 0.f ? k.scale : (float)(1.0 / sqrt((double)k.head_dim));
+    c->cfg.scale = c->scale;
+    c->clock_mhz = prop.clockRate / 1000.0;
+    const size_t D = (size_t)k.head_dim;
+    const size_t units = (size_t)k.batch * k.n_kv_heads;
+    c->stage_words = (size_t)k.n_q_heads * D * (size_t)(k.batch > k.max_q_len ? k.batch : k.max_q_len);
+    c->lse_words = (size_t)k.n_q_heads * (size_t)(k.batch > k.max_q_len ? k.batch : k.max_q_len);
+
+    int rc = GQA_OK;
+    auto alloc = [&](void** p, size_t bytes) {
+        if (rc != GQA_OK) return;
+        if (hipMalloc(p, bytes) != hipSuccess) rc = GQA_ERR_OOM;
+    };
+    alloc((void**)&c->k_cache, kv_words(c) * 2);
+    alloc((void**)&c->v_cache, kv_words(c) * 2);
+    alloc((void**)&c->part_o, units * c->max_splits_cap * group * D * sizeof(float));
+    alloc((void**)&c->part_ml, units * c->max_splits_cap * group * 2 * sizeof(float));
+    alloc((void**)&c->q_dev, c->stage_words * 2);
+    alloc((void**)&c->o_dev, c->stage_words * 2);
+    alloc((void**)&c->lse_dev, c->lse_words * sizeof(float));
+    alloc((void**)&c->lens_dev, (size_t)k.batch * sizeof(int32_t));
+    alloc((void**)&c->rows_dev, 2 * units * D * 2);
+    if (rc == GQA_OK && hipHostMalloc((void**)&c->o_pinned, c->stage_words * 2, 0) != hipSuccess) rc = GQA_ERR_OOM;
+    if (rc == GQA_OK && hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) rc = GQA_ERR_HIP;
+    if (rc == GQA_OK) {
+        bool ok = hipEventCreate(&c->ev_begin) == hipSuccess && hipEventCreate(&c->ev_end) == hipSuccess;
+        for (int i = 0; i < 4 && ok; ++i) ok = hipEventCreate(&c->ev_t[i]) == hipSuccess;
+        if (!ok) rc = GQA_ERR_HIP;
+    }
+    // Zero the caches once so rows beyond every sequence's length hold finite words.
+    if (rc == GQA_OK && (hipMemsetAsync(c->k_cache, 0, kv_words(c) * 2, c->stream) != hipSuccess ||
+                         hipMemsetAsync(c->v_cache, 0, kv_words(c) * 2, c->stream) != hipSuccess ||
+                         hipStreamSynchronize(c->stream) != hipSuccess))
+        rc = GQA_ERR_HIP;
+    if (rc != GQA_OK) {
+        gqa_destroy(c);
+        return rc;
+    }
+    *out_ctx = c;
+    return GQA_OK;
+}
+
+int gqa_destroy(gqa_ctx* c) {
+    if (!c) return GQA_ERR_NULL;
+    (void)hipSetDevice(c->cfg.device);
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    (void)hipFree(c->k_cache);
+    (void)hipFree(c->v_cache);
+    (void)hipFree(c->part_o);
+    (void)hipFree(c->part_ml);
+    (void)hipFree(c->q_dev);
+    (void)hipFree(c->o_dev);
+    (void)hipFree(c->lse_dev);
+    (void)hipFree(c->lens_dev);
+    (void)hipFree(c->rows_dev);
+    if (c->o_pinned) (void)hipHostFree(c->o_pinned);
+    if (c->ev_begin) (void)hipEventDestroy(c->ev_begin);
+    if (c->ev_end) (void)hipEventDestroy(c->ev_end);
+    for (int i = 0; i < GQA_TIMER_COUNT; ++i) {
+        if (!c->ev_pool[i]) continue;
+        for (int e = 0; e < 2 * kProfileLaunches; ++e)
+            if (c->ev_pool[i][e]) (void)hipEventDestroy(c->ev_pool[i][e]);
+        free(c->ev_pool[i]);
+    }
+    for (int i = 0; i < 4; ++i)
+        if (c->ev_t[i]) (void)hipEventDestroy(c->ev_t[i]);
+    if (c->stream) (void)hipStreamDestroy(c->stream);
+    delete c;
+    return GQA_OK;
+}
+
+int gqa_get_config(const gqa_ctx* c, gqa_config* out) {
+    if (!c || !out) return GQA_ERR_NULL;
+    *out = c->cfg;
+    return GQA_OK;
+}
+
+int gqa_set_option(gqa_ctx* c, int32_t option, int64_t value) {
+    if (!c) return GQA_ERR_NULL;
+    switch (option) {
+        case GQA_OPT_DECODE_CHUNK:
+            if (value < 0 || (value > 0 && (value % kMinChunk != 0 || value > c->l_cap + kMinChunk)))
+                return GQA_ERR_RANGE;
+            c->chunk_opt = (int)value;
+            return GQA_OK;
+        case GQA_OPT_PROFILE:
+            return profile_enable(c, value ? 1 : 0);
+        default:
+            return GQA_ERR_BAD_CFG;
+    }
+}
+
+int gqa_cache_pointers(gqa_ctx* c, void** k, void** v, int32_t* l_cap) {
+    if (!c) return GQA_ERR_NULL;
+    if (k) *k = c->k_cache;
+    if (v) *v = c->v_cache;
+    if (l_cap) *l_cap = c->l_cap;
+    return GQA_OK;
+}
+
+int gqa_load_kv(gqa_ctx* c, int32_t b, int32_t start_pos, int32_t n, const uint16_t* k, const uint16_t* v) {
+    if (!c || !k || !v) return GQA_ERR_NULL;
+    if (b < 0 || b >= c->cfg.batch) return GQA_ERR_STREAM_DEST;
+    if (n < 0 || start_pos < 0 || (int64_t)start_pos + n > c->cfg.max_seq_len) return GQA_ERR_RANGE;
+    int rc = txn_idle(c);
+    if (rc != GQA_OK) return rc;
+    if (n == 0) return GQA_OK;
+    HIP_TRY(hipSetDevice(c->cfg.device));
+    const size_t D = c->cfg.head_dim;
+    const size_t row_bytes = D * 2;
+    HIP_TRY(hipEventRecord(c->ev_begin, c->stream));
+    for (int h = 0; h < c->cfg.n_kv_heads; ++h) {
+        const size_t dst = (((size_t)b * c->cfg.n_kv_heads + h) * c->l_cap + start_pos) * D;
+        const size_t src = (size_t)h * n * D;
+        HIP_TRY(hipMemcpyAsync(c->k_cache + dst, k + src, n * row_bytes, hipMemcpyHostToDevice, c->stream));
+        HIP_TRY(hipMemcpyAsync(c->v_cache + dst, v + src, n * row_bytes, hipMemcpyHostToDevice, c->stream));
+    }
+    return finish_sync(c);
+}
+
+int gqa_load_kv_device(gqa_ctx* c, int32_t b, int32_t start_pos, int32_t n, const void* k, const void* v,
+                       void* stream) {
+    if (!c || !k || !v) return GQA_ERR_NULL;
+    if (b < 0 || b >= c->cfg.batch) return GQA_ERR_STREAM_DEST;
+    if (n < 0 || start_pos < 0 || (int64_t)start_pos + n > c->cfg.max_seq_len) return GQA_ERR_RANGE;
+    if (n == 0) return GQA_OK;
+    hipStream_t s = pick_stream(c, stream);
+    const size_t D = c->cfg.head_dim;
+    const size_t pitch_dst = (size_t)c->l_cap * D * 2;   // bytes between kv heads in the cache
+    const size_t pitch_src = (size_t)n * D * 2;          // bytes between kv heads in the source
+    const size_t dst = ((size_t)b * c->cfg.n_kv_heads * c->l_cap + start_pos) * D;
+    HIP_TRY(hipMemcpy2DAsync(c->k_cache + dst, pitch_dst, k, pitch_src, pitch_src, c->cfg.n_kv_heads,
+                             hipMemcpyDeviceToDevice, s));
+    HIP_TRY(hipMemcpy2DAsync(c->v_cache + dst, pitch_dst, v, pitch_src, pitch_src, c->cfg.n_kv_heads,
+                             hipMemcpyDeviceToDevice, s));
+    return GQA_OK;
+}
+
+int gqa_read_kv(gqa_ctx* c, int32_t b, int32_t start_pos, int32_t n, uint16_t* k, uint16_t* v) {
+    if (!c || !k || !v) return GQA_ERR_NULL;
+    if (b < 0 || b >= c->cfg.batch) return GQA_ERR_STREAM_DEST;
+    if (n < 0 || start_pos < 0 || (int64_t)start_pos + n > c->cfg.max_seq_len) return GQA_ERR_RANGE;
+    int rc = txn_idle(c);
+    if (rc != GQA_OK) return rc;
+    if (n == 0) return GQA_OK;
+    HIP_TRY(hipSetDevice(c->cfg.device));
+    const size_t D = c->cfg.head_dim;
+    for (int h = 0; h < c->cfg.n_kv_heads; ++h) {
+        const size_t src = (((size_t)b * c->cfg.n_kv_heads + h) * c->l_cap + start_pos) * D;
+        const size_t dst = (size_t)h * n * D;
+        HIP_TRY(hipMemcpyAsync(k + dst, c->k_cache + src, n * D * 2, hipMemcpyDeviceToHost, c->stream));
+        HIP_TRY(hipMemcpyAsync(v + dst, c->v_cache + src, n * D * 2, hipMemcpyDeviceToHost, c->stream));
+    }
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    return GQA_OK;
+}
+
+int gqa_append_kv(gqa_ctx* c, const uint16_t* k_rows, const uint16_t* v_rows, const int32_t* positions) {
+    if (!c || !k_rows || !v_rows || !positions) return GQA_ERR_NULL;
+    for (int b = 0; b < c->cfg.batch; ++b)
+        if (positions[b] < -1 || positions[b] >= c->cfg.max_seq_len) return GQA_ERR_RANGE;
+    int rc = txn_idle(c);
+    if (rc != GQA_OK) return rc;
+    HIP_TRY(hipSetDevice(c->cfg.device));
+    const size_t row_words = (size_t)c->cfg.batch * c->cfg.n_kv_heads * c->cfg.head_dim;
+    HIP_TRY(hipEventRecord(c->ev_begin, c->stream));
+    HIP_TRY(hipMemcpyAsync(c->rows_dev, k_rows, row_words * 2, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(hipMemcpyAsync(c->rows_dev + row_words, v_rows, row_words * 2, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(hipMemcpyAsync(c->lens_dev, positions, c->cfg.batch * sizeof(int32_t), hipMemcpyHostToDevice,
+                           c->stream));
+    rc = gqa_append_kv_device(c, c->rows_dev, c->rows_dev + row_words, c->lens_dev, nullptr);
+    if (rc != GQA_OK) return rc;
+    return finish_sync(c);
+}
+
+int gqa_append_kv_device(gqa_ctx* c, const void* k_rows, const void* v_rows, const int32_t* positions,
+                         void* stream) {
+    if (!c || !k_rows || !v_rows || !positions) return GQA_ERR_NULL;
+    hipStream_t s = pick_stream(c, stream);
+    timer_begin(c, GQA_TIMER_APPEND, s);
+    HIP_TRY(launch_append((const uint16_t*)k_rows, (const uint16_t*)v_rows, positions, c->k_cache, c->v_cache,
+                          c->cfg.batch, c->cfg.n_kv_heads, c->cfg.head_dim, c->l_cap, c->cfg.max_seq_len, s));
+    timer_end(c, GQA_TIMER_APPEND, s);
+    return GQA_OK;
+}
+
+int gqa_decode(gqa_ctx* c, const uint16_t* q, const int32_t* ctx_lens, uint16_t* o, float* lse) {
+    if (!c || !q || !ctx_lens || !o) return GQA_ERR_NULL;
+    int max_len = 0;
+    for (int b = 0; b < c->cfg.batch; ++b) {
+        if (ctx_lens[b] < 0 || ctx_lens[b] > c->cfg.max_seq_len) return GQA_ERR_RANGE;
+        if (ctx_lens[b] > max_len) max_len = ctx_lens[b];
+    }
+    int rc = txn_idle(c);
+    if (rc != GQA_OK) return rc;
+    HIP_TRY(hipSetDevice(c->cfg.device));
+    const size_t qwords = (size_t)c->cfg.batch * c->cfg.n_q_heads * c->cfg.head_dim;
+    HIP_TRY(hipEventRecord(c->ev_begin, c->stream));
+    HIP_TRY(hipMemcpyAsync(c->q_dev, q, qwords * 2, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(hipMemcpyAsync(c->lens_dev, ctx_lens, c->cfg.batch * sizeof(int32_t), hipMemcpyHostToDevice, c->stream));
+    rc = run_decode(c, c->q_dev, c->lens_dev, c->o_dev, lse ? c->lse_dev : nullptr, c->stream, max_len);
+    if (rc != GQA_OK) return rc;
+    HIP_TRY(hipMemcpyAsync(o, c->o_dev, qwords * 2, hipMemcpyDeviceToHost, c->stream));
+    if (lse)
+        HIP_TRY(hipMemcpyAsync(lse, c->lse_dev, (size_t)c->cfg.batch * c->cfg.n_q_heads * sizeof(float),
+                               hipMemcpyDeviceToHost, c->stream));
+    return finish_sync(c);
+}
+
+int gqa_decode_device(gqa_ctx* c, const void* q, const int32_t* ctx_lens, void* o, float* lse, void* stream) {
+    if (!c || !q || !ctx_lens || !o) return GQA_ERR_NULL;
+    return run_decode(c, q, ctx_lens, o, lse, pick_stream(c, stream), c->cfg.max_seq_len);
+}
+
+int gqa_prefill(gqa_ctx* c, int32_t b, const uint16_t* q, int32_t q_len, int32_t q_pos_base, int32_t kv_len,
+                int32_t kv_pos_base, int32_t causal, uint16_t* o, float* lse) {
+    if (!c || !q || !o) return GQA_ERR_NULL;
+    int rc = check_prefill_args(c, b, q_len, q_pos_base, kv_len, kv_pos_base);
+    if (rc != GQA_OK) return rc;
+    rc = txn_idle(c);
+    if (rc != GQA_OK) return rc;
+    HIP_TRY(hipSetDevice(c->cfg.device));
+    const size_t qwords = (size_t)c->cfg.n_q_heads * q_len * c->cfg.head_dim;
+    HIP_TRY(hipEventRecord(c->ev_begin, c->stream));
+    HIP_TRY(hipMemcpyAsync(c->q_dev, q, qwords * 2, hipMemcpyHostToDevice, c->stream));
+    rc = run_prefill(c, b, c->q_dev, q_len, q_pos_base, kv_len, kv_pos_base, causal, c->o_dev,
+                     lse ? c->lse_dev : nullptr, c->stream);
+    if (rc != GQA_OK) return rc;
+    HIP_TRY(hipMemcpyAsync(o, c->o_dev, qwords * 2, hipMemcpyDeviceToHost, c->stream));
+    if (lse)
+        HIP_TRY(hipMemcpyAsync(lse, c->lse_dev, (size_t)c->cfg.n_q_heads * q_len * sizeof(float),
+                               hipMemcpyDeviceToHost, c->stream));
+    return finish_sync(c);
+}
+
+int gqa_prefill_device(gqa_ctx* c, int32_t b, const void* q, int32_t q_len, int32_t q_pos_base, int32_t kv_len,
+                       int32_t kv_pos_base, int32_t causal, void* o, float* lse, void* stream) {
+    if (!c || !q || !o) return GQA_ERR_NULL;
+    int rc = check_prefill_args(c, b, q_len, q_pos_base, kv_len, kv_pos_base);
+    if (rc != GQA_OK) return rc;
+    return run_prefill(c, b, q, q_len, q_pos_base, kv_len, kv_pos_base, causal, o, lse, pick_stream(c, stream));
+}
+
+// ---- transaction protocol ----------------------------------------------------------
+
+int gqa_submit(gqa_ctx* c, int32_t b, const uint16_t* q, int32_t q_len, int32_t q_pos_base, int32_t kv_len,
+               int32_t kv_pos_base, int32_t causal) {
+    if (!c || !q) return GQA_ERR_NULL;
+    int rc = txn_idle(c);
+    if (rc != GQA_OK) return rc;
+    rc = check_prefill_args(c, b, q_len, q_pos_base, kv_len, kv_pos_base);
+    if (rc != GQA_OK) return rc;
+    if (!prefill_supported(c->cfg.head_dim, c->group)) return GQA_ERR_UNSUPPORTED;
+    HIP_TRY(hipSetDevice(c->cfg.device));
+    c->txn = Txn();
+    c->txn.b = b;
+    c->txn.q_len = q_len;
+    c->txn.q_pos_base = q_pos_base;
+    c->txn.kv_len = kv_len;
+    c->txn.kv_pos_base = kv_pos_base;
+    c->txn.causal = causal ? 1 : 0;
+    const size_t qwords = (size_t)c->cfg.n_q_heads * q_len * c->cfg.head_dim;
+    HIP_TRY(hipEventRecord(c->ev_t[0], c->stream));
+    HIP_TRY(hipMemcpyAsync(c->q_dev, q, qwords * 2, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    c->txn.valid = 1;
+    return GQA_OK;
+}
+
+int gqa_start(gqa_ctx* c) {
+    if (!c) return GQA_ERR_NULL;
+    if (c->txn.running && txn_idle(c) != GQA_OK) return GQA_ERR_BUSY_START;
+    if (!c->txn.valid) return GQA_ERR_NO_TRANSACTION;
+    HIP_TRY(hipSetDevice(c->cfg.device));
+    const Txn& t = c->txn;
+    HIP_TRY(hipEventRecord(c->ev_t[1], c->stream));
+    int rc = run_prefill(c, t.b, c->q_dev, t.q_len, t.q_pos_base, t.kv_len, t.kv_pos_base, t.causal, c->o_dev,
+                         nullptr, c->stream);
+    if (rc != GQA_OK) return rc;
+    HIP_TRY(hipEventRecord(c->ev_t[2], c->stream));
+    const size_t owords = (size_t)c->cfg.n_q_heads * t.q_len * c->cfg.head_dim;
+    HIP_TRY(hipMemcpyAsync(c->o_pinned, c->o_dev, owords * 2, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipEventRecord(c->ev_t[3], c->stream));
+    c->txn.running = 1;
+    return GQA_OK;
+}
+
+int gqa_status(gqa_ctx* c, uint32_t* out_status) {
+    if (!c || !out_status) return GQA_ERR_NULL;
+    if (!c->txn.running) {
+        *out_status = GQA_STATUS_START_READY;
+        return GQA_OK;
+    }
+    hipError_t e = hipEventQuery(c->ev_t[3]);
+    if (e == hipErrorNotReady) {
+        *out_status = GQA_STATUS_BUSY;
+        return GQA_OK;
+    }
+    if (e != hipSuccess) {
+        last_hip_error(e, "hipEventQuery");
+        *out_status = GQA_STATUS_ERROR;
+        return GQA_ERR_HIP;
+    }
+    *out_status = GQA_STATUS_DONE | GQA_STATUS_START_READY;
+    return GQA_OK;
+}
+
+int gqa_wait(gqa_ctx* c, int32_t timeout_ms) {
+    if (!c) return GQA_ERR_NULL;
+    if (!c->txn.running) return c->txn.valid ? GQA_ERR_NO_TRANSACTION : GQA_ERR_NO_TRANSACTION;
+    struct timespec t0;
+    clock_gettime(CLOCK_MONOTONIC, &t0);
+    for (;;) {
+        hipError_t e = hipEventQuery(c->ev_t[3]);
+        if (e == hipSuccess) break;
+        if (e != hipErrorNotReady) {
+            last_hip_error(e, "hipEventQuery");
+            return GQA_ERR_HIP;
+        }
+        if (timeout_ms >= 0) {
+            struct timespec t1;
+            clock_gettime(CLOCK_MONOTONIC, &t1);
+            const double ms = (t1.tv_sec - t0.tv_sec) * 1e3 + (t1.tv_nsec - t0.tv_nsec) * 1e-6;
+            if (ms > timeout_ms) return GQA_ERR_TIMEOUT;
+        }
+        struct timespec nap = {0, 20000};
+        nanosleep(&nap, nullptr);
+    }
+    float k_ms = 0.f, tot_ms = 0.f, copy_ms = 0.f;
+    HIP_TRY(hipEventElapsedTime(&k_ms, c->ev_t[1], c->ev_t[2]));
+    HIP_TRY(hipEventElapsedTime(&tot_ms, c->ev_t[0], c->ev_t[3]));
+    HIP_TRY(hipEventElapsedTime(&copy_ms, c->ev_t[2], c->ev_t[3]));
+    c->txn.kernel_us = k_ms * 1000.f;
+    c->txn.total_us = tot_ms * 1000.f;
+    c->txn.copy_us = copy_ms * 1000.f;
+    c->last_us = c->txn.total_us;
+    return GQA_OK;
+}
+
+int gqa_read_output(gqa_ctx* c, uint16_t* o, int64_t n_words) {
+    if (!c || !o) return GQA_ERR_NULL;
+    if (!c->txn.running) return GQA_ERR_NO_TRANSACTION;
+    const int64_t expect = (int64_t)c->cfg.n_q_heads * c->txn.q_len * c->cfg.head_dim;
+    if (n_words != expect) return GQA_ERR_RESULT_LEN;
+    int rc = gqa_wait(c, -1);
+    if (rc != GQA_OK) return rc;
+    memcpy(o, c->o_pinned, (size_t)expect * 2);
+    return GQA_OK;
+}
+
+int gqa_read_perf(gqa_ctx* c, uint64_t* total_ticks, uint64_t* kernel_ticks, uint64_t* copy_ticks,
+                  double* clock_mhz) {
+    if (!c) return GQA_ERR_NULL;
+    const double mhz = c->clock_mhz;
+    if (total_ticks) *total_ticks = (uint64_t)llround(c->txn.total_us * mhz);
+    if (kernel_ticks) *kernel_ticks = (uint64_t)llround(c->txn.kernel_us * mhz);
+    if (copy_ticks) *copy_ticks = (uint64_t)llround(c->txn.copy_us * mhz);
+    if (clock_mhz) *clock_mhz = mhz;
+    return GQA_OK;
+}
+
+// ---- timing -------------------------------------------------------------------------
+
+int gqa_last_elapsed_us(gqa_ctx* c, float* out_us) {
+    if (!c || !out_us) return GQA_ERR_NULL;
+    *out_us = c->last_us;
+    return GQA_OK;
+}
+
+int gqa_kernel_times(gqa_ctx* c, float* out_us, int32_t n) {
+    if (!c || !out_us) return GQA_ERR_NULL;
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    for (int i = 0; i < n; ++i) out_us[i] = 0.f;
+    for (int i = 0; i < n && i < GQA_TIMER_COUNT; ++i) {
+        if (!c->profile || c->ev_count[i] == 0) continue;
+        double total = 0.0;
+        for (int k = 0; k < c->ev_count[i]; ++k) {
+            HIP_TRY(hipEventSynchronize(c->ev_pool[i][2 * k + 1]));
+            float ms = 0.f;
+            HIP_TRY(hipEventElapsedTime(&ms, c->ev_pool[i][2 * k], c->ev_pool[i][2 * k + 1]));
+            total += ms;
+        }
+        out_us[i] = (float)(total * 1000.0 / c->ev_count[i]);
+    }
+    return GQA_OK;
+}
+
+int gqa_kernel_launch_counts(gqa_ctx* c, int32_t* out_counts, int32_t n) {
+    if (!c || !out_counts) return GQA_ERR_NULL;
+    for (int i = 0; i < n; ++i) out_counts[i] = (i < GQA_TIMER_COUNT && c->profile) ? c->ev_count[i] : 0;
+    return GQA_OK;
+}
+
+int gqa_synchronize(gqa_ctx* c) {
+    if (!c) return GQA_ERR_NULL;
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    return GQA_OK;
+}
+
+}  // extern "C"

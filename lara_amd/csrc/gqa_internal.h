@@ -1,0 +1,68 @@
+// Internal declarations shared by the libgqa translation units (not part of the ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace lara {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Split-KV decode launch description.  All pointers are device pointers.
+struct DecodeArgs {
+    const uint16_t* q;      // [B][H_q][D] bf16
+    const uint16_t* kc;     // [B][H_kv][L_cap][D] bf16
+    const uint16_t* vc;     // same layout as kc
+    const int32_t* lens;    // [B] keys attended per sequence
+    int32_t batch;
+    int32_t n_kv_heads;
+    int32_t l_cap;          // cache rows per (b, kv head), multiple of 64
+    int32_t l_max;          // configured maximum (lens are clamped to it)
+    int32_t chunk;          // keys per split work-group, multiple of 256
+    int32_t max_splits;     // grid x extent; splits beyond a sequence's length exit
+    float scale_log2;       // softmax scale * log2(e)
+    float* part_o;          // [B*H_kv][max_splits][G][D] fp32 un-normalised partial O
+    float* part_ml;         // [B*H_kv][max_splits][G][2] (running max in log2 units, sum)
+    uint16_t* out;          // [B][H_q][D] bf16
+    float* lse;             // [B][H_q] natural-log LSE, or nullptr
+};
+
+// Chunked prefill / full-transaction launch description (one sequence b).
+struct PrefillArgs {
+    const uint16_t* q;      // [H_q][q_len][D] bf16, head-major
+    const uint16_t* kc;     // cache base of sequence b: [H_kv][L_cap][D]
+    const uint16_t* vc;
+    int32_t n_q_heads;
+    int32_t n_kv_heads;
+    int32_t l_cap;
+    int32_t q_len;
+    int32_t kv_len;
+    int32_t q_pos_base;
+    int32_t kv_pos_base;
+    int32_t causal;
+    float scale_log2;
+    uint16_t* out;          // [H_q][q_len][D] bf16
+    float* lse;             // [H_q][q_len] or nullptr
+};
+
+bool decode_supported(int head_dim, int group);
+hipError_t launch_decode(int head_dim, int group, const DecodeArgs& a, hipStream_t s);
+hipError_t launch_combine(int head_dim, int group, const DecodeArgs& a, hipStream_t s);
+
+bool prefill_supported(int head_dim, int group);
+hipError_t launch_prefill(int head_dim, int group, const PrefillArgs& a, hipStream_t s);
+
+// K/V row append: rows [B][H_kv][D] -> cache row positions[b] (skipped if < 0 or >= l_max).
+hipError_t launch_append(const uint16_t* k_rows, const uint16_t* v_rows, const int32_t* positions,
+                         uint16_t* kc, uint16_t* vc, int batch, int n_kv_heads, int head_dim,
+                         int l_cap, int l_max, hipStream_t s);
+
+// fp32 -> bf16 word, round to nearest even on the upper half (sw/attn_driver.py:88-98).
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float x) {
+    uint32_t bits = __float_as_uint(x);
+    uint32_t lsb = (bits >> 16) & 1u;
+    bits += 0x7FFFu + lsb;
+    return (uint16_t)(bits >> 16);
+}
+
+}  // namespace lara

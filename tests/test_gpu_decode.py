@@ -1,0 +1,199 @@
+"""GPU parity of K/V append and split-KV decode against the CPU oracle.
+
+Tolerance (stated once, used everywhere): for every output row (one query head of one
+sequence) the max abs error against the float64 oracle is <= 2 bf16 ulp of the row's
+largest |output| ("2 bf16 ulp of output magnitude"); the softmax sum l, recovered from
+the returned log-sum-exp, is within rtol 1e-2; K/V append and read-back are bit-exact.
+"""
+import numpy as np
+import pytest
+
+from lara_amd import _lib
+from lara_amd.attn_driver import AttentionAccelerator
+from oracle import gqa_oracle as orc
+from tests._gen import bf16_normal, kv_with_outliers
+
+pytestmark = pytest.mark.gpu
+
+ULP_TOL = 2.0
+L_RTOL = 1e-2
+
+
+def make_engine(B, hq, hkv, d, max_len, **kw):
+    print(f"[engine] B={B} Hq={hq} Hkv={hkv} D={d} L={max_len}", flush=True)
+    return AttentionAccelerator(batch=B, n_q_heads=hq, n_kv_heads=hkv, head_dim=d, max_seq_len=max_len,
+                                max_q_len=kw.pop("max_q_len", min(max_len, 512)), **kw)
+
+
+def check_decode(out, lse, q, kc, vc, lens, scale):
+    ref, ref_lse = orc.decode(q, kc, vc, lens, scale=scale)
+    err = orc.row_ulp_error(out, ref)
+    worst = float(np.max(err))
+    assert worst <= ULP_TOL, f"max row error {worst:.3f} bf16 ulp > {ULP_TOL}"
+    if lse is not None:
+        live = np.isfinite(ref_lse)
+        assert np.array_equal(np.isneginf(lse), ~live)
+        # l = exp(lse - m): compare the sums relative to a common max via the lse difference
+        rel = np.abs(np.expm1(lse[live].astype(np.float64) - ref_lse[live]))
+        assert float(rel.max(initial=0.0)) <= L_RTOL
+    return worst
+
+
+def fill_cache(eng, rng, B, hkv, d, lens, amp=1.0, outliers=(0.0, 1.0), lcap=None):
+    lcap = lcap or int(max(lens.max(), 1))
+    kc = np.zeros((B, hkv, lcap, d), np.uint16)
+    vc = np.zeros((B, hkv, lcap, d), np.uint16)
+    for b in range(B):
+        n = int(lens[b])
+        if n == 0:
+            continue
+        kc[b, :, :n] = kv_with_outliers(rng, (hkv, n, d), amp, *outliers)
+        vc[b, :, :n] = bf16_normal(rng, (hkv, n, d), amp)
+        eng.load_kv(kc[b, :, :n], vc[b, :, :n], b=b)
+    return kc, vc
+
+
+def test_append_and_load_bit_exact():
+    rng = np.random.default_rng(100)
+    B, hq, hkv, d, L = 3, 32, 8, 128, 300
+    with make_engine(B, hq, hkv, d, L) as eng:
+        k = rng.integers(0, 1 << 16, (hkv, 200, d), dtype=np.uint16)  # arbitrary words, NaN patterns included
+        v = rng.integers(0, 1 << 16, (hkv, 200, d), dtype=np.uint16)
+        eng.load_kv(k, v, b=1, start_pos=50)
+        kr, vr = eng.read_kv(1, 50, 200)
+        assert np.array_equal(kr, k) and np.array_equal(vr, v)
+        rows_k = rng.integers(0, 1 << 16, (B, hkv, d), dtype=np.uint16)
+        rows_v = rng.integers(0, 1 << 16, (B, hkv, d), dtype=np.uint16)
+        eng.append_kv(rows_k, rows_v, np.array([7, 299, -1], np.int32))
+        k0, v0 = eng.read_kv(0, 7, 1)
+        assert np.array_equal(k0[:, 0], rows_k[0]) and np.array_equal(v0[:, 0], rows_v[0])
+        k1, v1 = eng.read_kv(1, 299, 1)
+        assert np.array_equal(k1[:, 0], rows_k[1]) and np.array_equal(v1[:, 0], rows_v[1])
+        # untouched rows unchanged, skipped sequence unchanged
+        kr, vr = eng.read_kv(1, 50, 200)
+        assert np.array_equal(kr, k) and np.array_equal(vr, v)
+        k2, v2 = eng.read_kv(2, 0, 300)
+        assert not k2.any() and not v2.any()
+        with pytest.raises(ValueError):
+            eng.append_kv(rows_k, rows_v, np.array([0, 300, 0], np.int32))
+
+
+def test_decode_c1_board_shape():
+    # B1, 8q/2kv, D64, ctx 256, scale 1/8, no mask
+    rng = np.random.default_rng(101)
+    B, hq, hkv, d, L = 1, 8, 2, 64, 256
+    with make_engine(B, hq, hkv, d, L, scale=0.125) as eng:
+        lens = np.array([L], np.int32)
+        kc, vc = fill_cache(eng, rng, B, hkv, d, lens)
+        q = bf16_normal(rng, (B, hq, d))
+        out, lse = eng.decode_step(q, lens, return_lse=True)
+        check_decode(out, lse, q, kc, vc, lens, 0.125)
+
+
+def test_decode_c2_append_then_attend():
+    # B1, 32q/8kv, D128: 4096 cached rows, each step appends one and attends 4097.
+    rng = np.random.default_rng(102)
+    B, hq, hkv, d = 1, 32, 8, 128
+    with make_engine(B, hq, hkv, d, 4200) as eng:
+        lens = np.array([4096], np.int32)
+        kc, vc = fill_cache(eng, rng, B, hkv, d, lens, amp=0.5, lcap=4200)
+        for step in range(3):
+            pos = 4096 + step
+            nk = bf16_normal(rng, (B, hkv, d), 0.5)
+            nv = bf16_normal(rng, (B, hkv, d), 0.5)
+            eng.append_kv(nk, nv, np.array([pos], np.int32))
+            kc[:, :, pos], vc[:, :, pos] = nk, nv
+            q = bf16_normal(rng, (B, hq, d), 0.5)
+            cur = np.array([pos + 1], np.int32)
+            out, lse = eng.decode_step(q, cur, return_lse=True)
+            check_decode(out, lse, q, kc, vc, cur, None)
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (16, 8, 128), (64, 4, 128), (16, 4, 64), (32, 4, 64)])
+def test_decode_ragged_edges(hq, hkv, d):
+    # lengths at round (16), chunk (256) and empty boundaries
+    rng = np.random.default_rng(hq + hkv + d)
+    lens = np.array([0, 1, 15, 16, 17, 255, 256, 257, 1000, 2049], np.int32)
+    B = len(lens)
+    with make_engine(B, hq, hkv, d, 2100) as eng:
+        kc, vc = fill_cache(eng, rng, B, hkv, d, lens, lcap=2100)
+        q = bf16_normal(rng, (B, hq, d))
+        out, lse = eng.decode_step(q, lens, return_lse=True)
+        check_decode(out, lse, q, kc, vc, lens, None)
+        assert not out[0].any()
+
+
+def test_decode_split_invariance():
+    rng = np.random.default_rng(103)
+    B, hq, hkv, d = 2, 32, 8, 128
+    lens = np.array([3000, 1777], np.int32)
+    with make_engine(B, hq, hkv, d, 3072) as eng:
+        kc, vc = fill_cache(eng, rng, B, hkv, d, lens, lcap=3072)
+        q = bf16_normal(rng, (B, hq, d))
+        outs = []
+        for chunk in (256, 512, 1024, 3072, 0):
+            _lib.check(eng._lib.gqa_set_option(eng._ctx, _lib.GQA_OPT_DECODE_CHUNK, chunk), "set chunk")
+            out, lse = eng.decode_step(q, lens, return_lse=True)
+            check_decode(out, lse, q, kc, vc, lens, None)
+            outs.append(out)
+        # different split counts differ by at most the rounding of the final bf16
+        for o in outs[1:]:
+            diff = np.abs(orc.bf16_u16_to_fp32(o).astype(np.float64) - orc.bf16_u16_to_fp32(outs[0]))
+            assert float(diff.max()) <= float(orc.bf16_ulp(np.abs(orc.bf16_u16_to_fp32(outs[0])).max()))
+
+
+def test_decode_group8_outliers():
+    # C4-shaped (64q/8kv, 1% of K rows x8) at a length the oracle checks in seconds
+    rng = np.random.default_rng(104)
+    B, hq, hkv, d, L = 2, 64, 8, 128, 20000
+    with make_engine(B, hq, hkv, d, L) as eng:
+        lens = np.array([L, 12345], np.int32)
+        kc, vc = fill_cache(eng, rng, B, hkv, d, lens, outliers=(0.01, 8.0), lcap=L)
+        q = bf16_normal(rng, (B, hq, d))
+        out, lse = eng.decode_step(q, lens, return_lse=True)
+        check_decode(out, lse, q, kc, vc, lens, None)
+
+
+def test_decode_constant_v_is_exact():
+    # softmax weights sum to 1: a constant V row must come back exactly
+    rng = np.random.default_rng(105)
+    B, hq, hkv, d, L = 2, 32, 8, 128, 5000
+    with make_engine(B, hq, hkv, d, L) as eng:
+        for b in range(B):
+            k = bf16_normal(rng, (hkv, L, d))
+            v = np.broadcast_to(bf16_normal(rng, (hkv, 1, d)), (hkv, L, d)).copy()
+            eng.load_kv(k, v, b=b)
+            if b == 0:
+                v0 = v[:, 0]
+        q = bf16_normal(rng, (B, hq, d))
+        out = eng.decode_step(q, np.array([L, L], np.int32))
+        assert np.array_equal(out[0], np.repeat(v0, hq // hkv, axis=0))
+
+
+def _full_size(name):
+    from lara_amd.benchmark import WORKLOADS
+    w = WORKLOADS[name]
+    rng = np.random.default_rng(w.seed)
+    lens = w.lengths()
+    with make_engine(w.batch, w.n_q_heads, w.n_kv_heads, w.head_dim, int(lens.max()), max_q_len=1,
+                     scale=w.scale) as eng:
+        kc, vc = fill_cache(eng, rng, w.batch, w.n_kv_heads, w.head_dim, lens, w.amplitude,
+                            (w.outlier_fraction, w.outlier_scale))
+        q = bf16_normal(rng, (w.batch, w.n_q_heads, w.head_dim), w.amplitude)
+        print(f"[{name}] decode", flush=True)
+        out, lse = eng.decode_step(q, lens, return_lse=True)
+        print(f"[{name}] oracle check", flush=True)
+        worst = check_decode(out, lse, q, kc, vc, lens, w.scale)
+        print(f"[{name}] worst row error {worst:.3f} ulp", flush=True)
+
+
+def test_decode_full_size_ns():
+    _full_size("ns")
+
+
+def test_decode_full_size_c3_ragged():
+    _full_size("c3")
+
+
+def test_decode_full_size_c4_long_context():
+    _full_size("c4")
