@@ -224,6 +224,21 @@ def cpu_baseline(name: str, budget_s: float) -> dict:
     }
 
 
+def copy_calibration(mib: int) -> int:
+    """A plain copy kernel of known size: reads and writes ``mib`` MiB per launch."""
+    import torch
+
+    n = mib * 2**20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").random_(0, 255)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_per_launch": n, "launches": 5}), flush=True)
+    return 0
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -234,6 +249,9 @@ def main() -> int:
     parser.add_argument("--others", default="c2,c3,c4", help="extra decode workloads to report ('' = none)")
     parser.add_argument("--cpu-seconds", type=float, default=12.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--calibrate-copy-mib", type=int, default=0,
+                        help="only run a plain device-to-device copy of this many MiB (5 times) and exit; "
+                             "used to scale the FETCH_SIZE / WRITE_SIZE counters")
     args = parser.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -247,6 +265,8 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a GPU (gfx950)", file=sys.stderr)
         return 1
+    if args.calibrate_copy_mib:
+        return copy_calibration(args.calibrate_copy_mib)
     main_r = measure(args.workload, args.steps, args.warmup, args.chunk)
     others = {}
     for name in [x for x in args.others.split(",") if x and x != args.workload]:
