@@ -117,12 +117,14 @@ int profile_enable(gqa_ctx* c, int on) {
             for (int e = 0; e < 2 * kProfileLaunches; ++e) HIP_TRY(hipEventCreate(&c->ev_pool[i][e]));
         }
     }
+    timers_reset(c);
     c->profile = on ? 1 : 0;
     return GQA_OK;
 }
 
 int run_decode(gqa_ctx* c, const void* q, const int32_t* lens, void* o, float* lse, hipStream_t s,
                int max_len) {
+    if (!decode_supported(c->cfg.head_dim, c->group)) return GQA_ERR_UNSUPPORTED;
     const int chunk = choose_chunk(c, max_len);
     int max_splits = max_len > 0 ? (max_len + chunk - 1) / chunk : 1;
     if (max_splits > c->max_splits_cap) return GQA_ERR_RANGE;
@@ -250,7 +252,7 @@ int gqa_create(const gqa_config* cfg, gqa_ctx** out_ctx) {
         k.max_seq_len < 1 || k.max_q_len < 1 || !(k.scale >= 0.f) || !isfinite(k.scale))
         return GQA_ERR_BAD_CFG;
     const int group = k.n_q_heads / k.n_kv_heads;
-    if (!decode_supported(k.head_dim, group)) return GQA_ERR_UNSUPPORTED;
+    if (!decode_supported(k.head_dim, group) && !prefill_supported(k.head_dim, group)) return GQA_ERR_UNSUPPORTED;
 
     int n = 0;
     if (hipGetDeviceCount(&n) != hipSuccess || n < 1) return GQA_ERR_NO_DEVICE;

@@ -1,0 +1,180 @@
+"""GPU parity of the MFMA prefill path (run_attention transactions and chunked prefill).
+
+Tolerance, as for decode: every output row (one query head, one query position) is within
+2 bf16 ulp of the row's largest |output| of the float64 oracle; the softmax sum l, recovered
+from the returned log-sum-exp, is within rtol 1e-2; rows with no valid key are exactly zero.
+"""
+import numpy as np
+import pytest
+
+from lara_amd import attn_driver as drv
+from lara_amd.attn_driver import AttentionAccelerator
+from oracle import gqa_oracle as orc
+from tests._gen import bf16_normal
+
+pytestmark = pytest.mark.gpu
+
+ULP_TOL = 2.0
+L_RTOL = 1e-2
+
+
+def check_rows(out_words, lse, ref, ref_lse):
+    err = orc.row_ulp_error(out_words, ref)
+    worst = float(np.max(err)) if err.size else 0.0
+    assert worst <= ULP_TOL, f"max row error {worst:.3f} bf16 ulp > {ULP_TOL}"
+    if lse is not None:
+        live = np.isfinite(ref_lse)
+        assert np.array_equal(np.isneginf(lse), ~live)
+        rel = np.abs(np.expm1(lse[live].astype(np.float64) - ref_lse[live]))
+        assert float(rel.max(initial=0.0)) <= L_RTOL
+    return worst
+
+
+def oracle_for(q, k, v, **kw):
+    return orc.attention(orc.bf16_u16_to_fp32(q), orc.bf16_u16_to_fp32(k), orc.bf16_u16_to_fp32(v), **kw)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("L,qb,kb", [(1, 0, 0), (16, 0, 0), (32, 3, 3), (64, 31, 7), (128, 0, 0), (200, 5, 9),
+                                     (512, 0, 0)])
+def test_run_attention_board_contract(L, qb, kb, causal):
+    """sw/attn_driver.py:469-550 at the KV260 shape: Q [32, L, 128], K/V [8, L, 128]."""
+    print(f"[run_attention] L={L} q_pos_base={qb} kv_pos_base={kb} causal={causal}", flush=True)
+    rng = np.random.default_rng(1000 + L + qb + kb + causal)
+    q = bf16_normal(rng, (32, L, 128))
+    k = bf16_normal(rng, (8, L, 128))
+    v = bf16_normal(rng, (8, L, 128))
+    with AttentionAccelerator() as acc:
+        out = acc.run_attention(q, k, v, seq_len=L, q_pos_base=qb, kv_pos_base=kb, causal=causal)
+        assert out.dtype == np.uint16 and out.shape == (32, L, 128)
+        prof = acc.last_profile.to_dict()
+        assert prof["seq_len"] == L and prof["attention_total_ms"] > 0
+    ref, _ = oracle_for(q, k, v, causal=causal, q_pos_base=qb, kv_pos_base=kb)
+    check_rows(out, None, ref, None)
+
+
+def test_run_attention_float_inputs_are_packed_like_the_board():
+    rng = np.random.default_rng(7)
+    L = 48
+    qf = rng.standard_normal((32, L, 128)).astype(np.float32)
+    kf = rng.standard_normal((8, L, 128)).astype(np.float32)
+    vf = rng.standard_normal((8, L, 128)).astype(np.float32)
+    with AttentionAccelerator() as acc:
+        out_f = acc.run_attention(qf, kf, vf, causal=True)
+        out_w = acc.run_attention(drv.fp32_to_bf16_u16(qf), drv.fp32_to_bf16_u16(kf), drv.fp32_to_bf16_u16(vf),
+                                  causal=True)
+    assert np.array_equal(out_f, out_w)
+
+
+def test_zero_input_gives_zero_output():
+    """Board smoke test (sw/board_test.py:44-48): all-zero Q/K/V must give all-zero O."""
+    L = 64
+    with AttentionAccelerator() as acc:
+        z = np.zeros((32, L, 128), np.uint16)
+        zk = np.zeros((8, L, 128), np.uint16)
+        out = acc.run_attention(z, zk, zk, causal=True)
+    assert not out.any()
+
+
+def test_transaction_protocol_and_busy_start():
+    rng = np.random.default_rng(8)
+    L = 96
+    q = bf16_normal(rng, (32, L, 128))
+    k = bf16_normal(rng, (8, L, 128))
+    v = bf16_normal(rng, (8, L, 128))
+    with AttentionAccelerator() as acc:
+        acc.load_kv(k, v)
+        acc.submit_query(q, kv_len=L, causal=False)
+        assert acc.status() & drv.STATUS_START_READY
+        acc.start()
+        acc.wait_done(q, k, v, L, timeout_ms=10000)
+        assert acc.status() & drv.STATUS_DONE
+        out = acc.read_output()
+        perf = acc.read_perf()
+        assert perf["cycles"] >= perf["mac_cycles"] > 0
+        with pytest.raises(RuntimeError):
+            acc.readback_o(L + 1)  # CSR_RESULT_LEN mismatch
+    ref, _ = oracle_for(q, k, v, causal=False)
+    check_rows(out, None, ref, None)
+
+
+def test_chunked_prefill_c5():
+    """2048-token prompt in 256-token chunks against a growing cache, causal (32q/8kv, D 128)."""
+    rng = np.random.default_rng(5)
+    P, C = 2048, 256
+    q = bf16_normal(rng, (32, P, 128))
+    k = bf16_normal(rng, (8, P, 128))
+    v = bf16_normal(rng, (8, P, 128))
+    with AttentionAccelerator(max_seq_len=P, max_q_len=C) as acc:
+        for c in range(P // C):
+            s = c * C
+            print(f"[c5] chunk {c}", flush=True)
+            acc.load_kv(k[:, s:s + C], v[:, s:s + C], start_pos=s)
+            out, lse = acc.prefill_chunk(q[:, s:s + C], q_pos_base=s, kv_len=s + C, causal=True, return_lse=True)
+            ref, ref_lse = oracle_for(q[:, s:s + C], k[:, :s + C], v[:, :s + C], causal=True, q_pos_base=s)
+            check_rows(out, lse, ref, ref_lse)
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (8, 8, 128), (16, 8, 128), (64, 8, 128), (64, 4, 128),
+                                      (8, 2, 64), (16, 16, 64), (32, 4, 64), (32, 2, 64)])
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_shapes_ragged(hq, hkv, d, causal):
+    """Every compiled (head_dim, group), ragged q_len / kv_len, absolute position bases."""
+    rng = np.random.default_rng(hq * 7 + hkv * 3 + d + causal)
+    q_len, kv_len, qb, kb = 77, 333, 300, 40
+    print(f"[prefill] hq={hq} hkv={hkv} d={d} causal={causal}", flush=True)
+    q = bf16_normal(rng, (hq, q_len, d))
+    k = bf16_normal(rng, (hkv, kv_len, d))
+    v = bf16_normal(rng, (hkv, kv_len, d))
+    with AttentionAccelerator(n_q_heads=hq, n_kv_heads=hkv, head_dim=d, max_seq_len=kv_len, max_q_len=q_len) as acc:
+        acc.load_kv(k, v)
+        out, lse = acc.prefill_chunk(q, q_pos_base=qb, kv_len=kv_len, kv_pos_base=kb, causal=causal,
+                                     return_lse=True)
+    ref, ref_lse = oracle_for(q, k, v, causal=causal, q_pos_base=qb, kv_pos_base=kb)
+    check_rows(out, lse, ref, ref_lse)
+
+
+def test_prefill_rows_without_keys_are_zero():
+    rng = np.random.default_rng(9)
+    q_len, kv_len = 50, 120
+    q = bf16_normal(rng, (32, q_len, 128))
+    k = bf16_normal(rng, (8, kv_len, 128))
+    v = bf16_normal(rng, (8, kv_len, 128))
+    with AttentionAccelerator(max_seq_len=kv_len, max_q_len=q_len) as acc:
+        acc.load_kv(k, v)
+        # queries at positions 0..49, keys at 20..139: rows 0..19 see no key
+        out, lse = acc.prefill_chunk(q, q_pos_base=0, kv_len=kv_len, kv_pos_base=20, causal=True, return_lse=True)
+    assert not out[:, :20].any() and np.all(np.isneginf(lse[:, :20]))
+    ref, ref_lse = oracle_for(q, k, v, causal=True, q_pos_base=0, kv_pos_base=20)
+    check_rows(out, lse, ref, ref_lse)
+
+
+def test_prefill_stale_cache_rows_do_not_leak():
+    """Rows past kv_len hold NaN words; the result must not see them."""
+    rng = np.random.default_rng(10)
+    q_len, kv_len = 40, 70
+    q = bf16_normal(rng, (32, q_len, 128))
+    k = bf16_normal(rng, (8, kv_len, 128))
+    v = bf16_normal(rng, (8, kv_len, 128))
+    nan = np.full((8, 58, 128), 0x7FC0, np.uint16)
+    with AttentionAccelerator(max_seq_len=128, max_q_len=q_len) as acc:
+        acc.load_kv(nan, nan, start_pos=70)
+        acc.load_kv(k, v)
+        out = acc.prefill_chunk(q, q_pos_base=kv_len - q_len, kv_len=kv_len, causal=True)
+    ref, _ = oracle_for(q, k, v, causal=True, q_pos_base=kv_len - q_len)
+    check_rows(out, None, ref, None)
+
+
+def test_single_row_prefill_matches_decode():
+    rng = np.random.default_rng(11)
+    L = 700
+    k = bf16_normal(rng, (8, L, 128))
+    v = bf16_normal(rng, (8, L, 128))
+    q = bf16_normal(rng, (32, 1, 128))
+    with AttentionAccelerator(max_seq_len=L, max_q_len=1) as acc:
+        acc.load_kv(k, v)
+        pre, lse_p = acc.prefill_chunk(q, q_pos_base=L - 1, kv_len=L, causal=True, return_lse=True)
+        dec, lse_d = acc.decode_step(q[:, 0][None], np.array([L], np.int32), return_lse=True)
+    ref, ref_lse = oracle_for(q, k, v, causal=False)
+    check_rows(pre, lse_p, ref, ref_lse)
+    check_rows(dec[0][:, None], lse_d[0][:, None], ref, ref_lse)
