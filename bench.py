@@ -93,14 +93,11 @@ class DecodeBench:
 
     def step(self) -> None:
         c = ctypes.c_void_p
-        rc = self.lib.gqa_append_kv_device(self.ctx, c(self.k_new.data_ptr()), c(self.v_new.data_ptr()),
-                                           c(self.pos.data_ptr()), self.sptr)
+        rc = self.lib.gqa_decode_append_device(self.ctx, c(self.q.data_ptr()), c(self.k_new.data_ptr()),
+                                               c(self.v_new.data_ptr()), c(self.pos.data_ptr()),
+                                               c(self.lens_dev.data_ptr()), c(self.o.data_ptr()), None, self.sptr)
         if rc:
-            self._lib.check(rc, "append")
-        rc = self.lib.gqa_decode_device(self.ctx, c(self.q.data_ptr()), c(self.lens_dev.data_ptr()),
-                                        c(self.o.data_ptr()), None, self.sptr)
-        if rc:
-            self._lib.check(rc, "decode")
+            self._lib.check(rc, "decode_append")
 
     def run(self, steps: int, warmup: int) -> dict:
         torch = self.torch
@@ -129,9 +126,7 @@ class DecodeBench:
         return {
             "wall_ms_per_step": wall_ms,
             "gpu_ms_per_step": gpu_ms,
-            "append_us": times[_lib.GQA_TIMER_APPEND],
             "decode_us": times[_lib.GQA_TIMER_DECODE],
-            "combine_us": times[_lib.GQA_TIMER_COMBINE],
             "decode_launches": int(counts[_lib.GQA_TIMER_DECODE]),
         }
 
@@ -170,6 +165,100 @@ def measure(name: str, steps: int, warmup: int, chunk: int = 0) -> dict:
     log(f"{name}: {r['us_per_step']:.1f} us/step, step {r['step_gbps']:.0f} GB/s, decode kernel "
         f"{r['decode_us']:.1f} us = {r.get('decode_kernel_gbps') or 0:.0f} GB/s")
     return r
+
+
+class PrefillBench:
+    """Chunked causal prefill: every chunk appends its K/V rows, then attends the growing cache."""
+
+    def __init__(self, w, device: int = 0):
+        import torch
+        from lara_amd import _lib
+
+        self.torch = torch
+        self.lib = _lib.lib()
+        self._lib = _lib
+        self.w = w
+        cfg = _lib.GqaConfig(1, w.n_q_heads, w.n_kv_heads, w.head_dim, w.prompt, w.chunk, 0.0, device)
+        self.ctx = ctypes.c_void_p()
+        _lib.check(self.lib.gqa_create(ctypes.byref(cfg), ctypes.byref(self.ctx)), "gqa_create")
+        dev = torch.device("cuda", device)
+        self.stream = torch.cuda.current_stream(dev)
+        self.sptr = ctypes.c_void_p(self.stream.cuda_stream)
+        g = torch.Generator(device=dev)
+        g.manual_seed(w.seed)
+        shape_q = (w.n_q_heads, w.prompt, w.head_dim)
+        shape_kv = (w.n_kv_heads, w.prompt, w.head_dim)
+        q = torch.randn(shape_q, generator=g, device=dev).to(torch.bfloat16)
+        k = torch.randn(shape_kv, generator=g, device=dev).to(torch.bfloat16)
+        v = torch.randn(shape_kv, generator=g, device=dev).to(torch.bfloat16)
+        from lara_amd.benchmark import prefill_chunk_schedule
+
+        self.chunks = []
+        for start, q_len, kv_len in prefill_chunk_schedule(w):
+            self.chunks.append((start, q_len, kv_len, q[:, start:start + q_len].contiguous(),
+                                k[:, start:start + q_len].contiguous(), v[:, start:start + q_len].contiguous()))
+        self.o = torch.empty((w.n_q_heads, w.chunk, w.head_dim), dtype=torch.bfloat16, device=dev)
+        torch.cuda.synchronize(dev)
+
+    def step(self) -> None:
+        c = ctypes.c_void_p
+        for start, q_len, kv_len, qc, kc, vc in self.chunks:
+            rc = self.lib.gqa_load_kv_device(self.ctx, 0, start, q_len, c(kc.data_ptr()), c(vc.data_ptr()), self.sptr)
+            if rc:
+                self._lib.check(rc, "load_kv_device")
+            rc = self.lib.gqa_prefill_device(self.ctx, 0, c(qc.data_ptr()), q_len, start, kv_len, 0, 1,
+                                             c(self.o.data_ptr()), None, self.sptr)
+            if rc:
+                self._lib.check(rc, "prefill_device")
+
+    def run(self, steps: int, warmup: int) -> dict:
+        torch = self.torch
+        _lib = self._lib
+        for _ in range(warmup):
+            self.step()
+        torch.cuda.synchronize()
+        _lib.check(self.lib.gqa_set_option(self.ctx, _lib.GQA_OPT_PROFILE, 1), "profile on")
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            self.step()
+        torch.cuda.synchronize()
+        wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+        times = (ctypes.c_float * _lib.GQA_TIMER_COUNT)()
+        _lib.check(self.lib.gqa_kernel_times(self.ctx, times, _lib.GQA_TIMER_COUNT), "kernel times")
+        _lib.check(self.lib.gqa_set_option(self.ctx, _lib.GQA_OPT_PROFILE, 0), "profile off")
+        return {"wall_ms_per_prompt": wall_ms, "prefill_us_per_launch": times[_lib.GQA_TIMER_PREFILL]}
+
+    def close(self) -> None:
+        self.lib.gqa_destroy(self.ctx)
+
+
+def measure_prefill(name: str, steps: int, warmup: int) -> dict:
+    from lara_amd.benchmark import BF16_DENSE_TFLOPS, PREFILL_WORKLOADS, prefill_chunk_schedule, prefill_flops, \
+        valid_pairs
+
+    w = PREFILL_WORKLOADS[name]
+    log(f"{name}: chunked prefill set-up")
+    bench = PrefillBench(w)
+    try:
+        r = bench.run(steps, warmup)
+    finally:
+        bench.close()
+    sched = prefill_chunk_schedule(w)
+    pairs = sum(valid_pairs(ql, kl, causal=w.causal, q_pos_base=qb) for qb, ql, kl in sched)
+    flops = prefill_flops(w.n_q_heads, w.head_dim, pairs)
+    kern_us = r["prefill_us_per_launch"] * len(sched)
+    out = {
+        "us_per_prompt": r["wall_ms_per_prompt"] * 1e3,
+        "prefill_kernel_us_per_prompt": kern_us,
+        "chunks": len(sched),
+        "flops_per_prompt": flops,
+        "kernel_tflops": flops / (kern_us * 1e-6) / 1e12 if kern_us > 0 else None,
+        "tokens_per_s": w.prompt / (r["wall_ms_per_prompt"] * 1e-3),
+    }
+    out["mfma_frac_of_bf16_peak"] = out["kernel_tflops"] / BF16_DENSE_TFLOPS if out["kernel_tflops"] else None
+    log(f"{name}: {out['us_per_prompt']:.1f} us/prompt, kernels {kern_us:.1f} us = {out['kernel_tflops'] or 0:.1f} "
+        f"TFLOP/s")
+    return out
 
 
 def read_traffic():
@@ -246,7 +335,7 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--workload", default="ns", choices=sorted(WORKLOAD_NAMES))
     parser.add_argument("--chunk", type=int, default=0, help="keys per split-KV work-group (0 = auto)")
-    parser.add_argument("--others", default="c2,c3,c4", help="extra decode workloads to report ('' = none)")
+    parser.add_argument("--others", default="c2,c3,c4,c5", help="extra decode workloads to report ('' = none)")
     parser.add_argument("--cpu-seconds", type=float, default=12.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--calibrate-copy-mib", type=int, default=0,
@@ -270,6 +359,9 @@ def main() -> int:
     main_r = measure(args.workload, args.steps, args.warmup, args.chunk)
     others = {}
     for name in [x for x in args.others.split(",") if x and x != args.workload]:
+        if name == "c5":
+            others[name] = measure_prefill(name, max(10, args.steps // 2), max(2, args.warmup // 2))
+            continue
         r = measure(name, max(10, args.steps // 2), max(2, args.warmup // 2))
         others[name] = {k: r[k] for k in ("us_per_step", "step_gbps", "step_frac_of_peak", "decode_us",
                                            "decode_kernel_gbps", "tokens_per_s")}
@@ -315,10 +407,10 @@ def main() -> int:
             "n_kv_heads": w.n_kv_heads,
             "head_dim": w.head_dim,
             "attended_keys": int(w.lengths().max()),
-            "step": "append 1 K/V row per sequence + split-KV decode + LSE combine",
+            "step": "one launch: append 1 K/V row per sequence + split-KV decode + in-kernel LSE merge",
             "accumulate": "fp32",
         },
-        "kernels_us": {k: main_r[k] for k in ("append_us", "decode_us", "combine_us")},
+        "kernels_us": {"decode_step": main_r["decode_us"]},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "other_workloads": others,

@@ -54,7 +54,7 @@ extern "C" {
 /* Per-kernel timer slots reported by gqa_kernel_times. */
 #define GQA_TIMER_APPEND  0
 #define GQA_TIMER_DECODE  1
-#define GQA_TIMER_COMBINE 2
+#define GQA_TIMER_COMBINE 2 /* split-KV merge launched on its own (prefill); decode merges in-kernel */
 #define GQA_TIMER_PREFILL 3
 #define GQA_TIMER_COUNT   4
 
@@ -111,6 +111,13 @@ int gqa_read_kv(gqa_ctx* ctx, int32_t b, int32_t start_pos, int32_t n,
  * (output_buffer.sv:276-277 semantics) and lse = -inf. */
 int gqa_decode(gqa_ctx* ctx, const uint16_t* q, const int32_t* ctx_lens,
                uint16_t* o, float* lse);
+/* gqa_decode_append: one decode step as a single kernel launch -- append one K/V row per
+ * sequence (k_rows, v_rows host [B][H_kv][D] at positions[b], -1 = none; the same write
+ * gqa_append_kv makes, bit-exact) and attend rows 0..ctx_lens[b]-1, which may include the
+ * row just appended.  Replaces the KV-load + run_attention pair of attn_driver.py:418-550
+ * for one new token per sequence; outputs as gqa_decode. */
+int gqa_decode_append(gqa_ctx* ctx, const uint16_t* q, const uint16_t* k_rows, const uint16_t* v_rows,
+                      const int32_t* positions, const int32_t* ctx_lens, uint16_t* o, float* lse);
 /* gqa_prefill replaces run_attention for a block of q_len query rows of sequence b
  * against cache rows 0..kv_len-1: q and o are host head-major [H_q][q_len][D]
  * (attn_driver.py:487-488, 464).  Query i sits at absolute position q_pos_base + i,
@@ -147,6 +154,9 @@ int gqa_append_kv_device(gqa_ctx* ctx, const void* k_rows, const void* v_rows,
                          const int32_t* positions, void* stream);
 int gqa_decode_device(gqa_ctx* ctx, const void* q, const int32_t* ctx_lens,
                       void* o, float* lse, void* stream);
+int gqa_decode_append_device(gqa_ctx* ctx, const void* q, const void* k_rows, const void* v_rows,
+                             const int32_t* positions, const int32_t* ctx_lens, void* o, float* lse,
+                             void* stream);
 int gqa_prefill_device(gqa_ctx* ctx, int32_t b, const void* q, int32_t q_len,
                        int32_t q_pos_base, int32_t kv_len, int32_t kv_pos_base,
                        int32_t causal, void* o, float* lse, void* stream);

@@ -81,6 +81,7 @@ _SIGNATURES = {
     "gqa_append_kv": [_CTX, _P16, _P16, _P32],
     "gqa_read_kv": [_CTX, c_int32, c_int32, c_int32, _P16, _P16],
     "gqa_decode": [_CTX, _P16, _P32, _P16, _PF],
+    "gqa_decode_append": [_CTX, _P16, _P16, _P16, _P32, _P32, _P16, _PF],
     "gqa_prefill": [_CTX, c_int32, _P16, c_int32, c_int32, c_int32, c_int32, c_int32, _P16, _PF],
     "gqa_submit": [_CTX, c_int32, _P16, c_int32, c_int32, c_int32, c_int32, c_int32],
     "gqa_start": [_CTX],
@@ -91,6 +92,8 @@ _SIGNATURES = {
     "gqa_load_kv_device": [_CTX, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p],
     "gqa_append_kv_device": [_CTX, c_void_p, c_void_p, c_void_p, c_void_p],
     "gqa_decode_device": [_CTX, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p],
+    "gqa_decode_append_device": [_CTX, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                 c_void_p],
     "gqa_prefill_device": [_CTX, c_int32, c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_void_p,
                            c_void_p, c_void_p],
     "gqa_cache_pointers": [_CTX, POINTER(c_void_p), POINTER(c_void_p), _P32],

@@ -522,9 +522,7 @@ class AttentionAccelerator:
             raise ValueError(f"rows {start_pos}..{start_pos + n - 1} exceed the cache capacity {self.max_seq_len}")
         self._call("gqa_load_kv", int(b), int(start_pos), int(n), _lib.as_u16_ptr(k), _lib.as_u16_ptr(v))
 
-    def append_kv(self, k_rows: np.ndarray, v_rows: np.ndarray, positions) -> None:
-        """Append one K/V row per sequence: rows [B, H_kv, D] at ``positions[b]`` (-1 skips)."""
-        self._ensure_open()
+    def _check_rows(self, k_rows, v_rows, positions):
         k = fp32_to_bf16_u16(k_rows)
         v = fp32_to_bf16_u16(v_rows)
         shape = (self.batch, self.n_kv_heads, self.head_dim)
@@ -535,6 +533,12 @@ class AttentionAccelerator:
             raise ValueError(f"expected {self.batch} positions, got {pos.shape}")
         if np.any(pos < -1) or np.any(pos >= self.max_seq_len):
             raise ValueError(f"append position outside -1..{self.max_seq_len - 1}")
+        return k, v, pos
+
+    def append_kv(self, k_rows: np.ndarray, v_rows: np.ndarray, positions) -> None:
+        """Append one K/V row per sequence: rows [B, H_kv, D] at ``positions[b]`` (-1 skips)."""
+        self._ensure_open()
+        k, v, pos = self._check_rows(k_rows, v_rows, positions)
         self._call("gqa_append_kv", _lib.as_u16_ptr(k), _lib.as_u16_ptr(v), _lib.as_i32_ptr(pos))
 
     def read_kv(self, b: int, start_pos: int, n: int) -> tuple[np.ndarray, np.ndarray]:
@@ -550,11 +554,15 @@ class AttentionAccelerator:
         return k, v
 
     # ---- attention ----------------------------------------------------------------------------
-    def decode_step(self, q: np.ndarray, ctx_lens, *, return_lse: bool = False):
+    def decode_step(self, q: np.ndarray, ctx_lens, *, k_rows: np.ndarray | None = None,
+                    v_rows: np.ndarray | None = None, positions=None, return_lse: bool = False):
         """One query row per sequence against rows 0..ctx_lens[b]-1 of the cache.
 
         q is [B, H_q, D] (bf16 words or floats); returns bf16 words [B, H_q, D], and with
-        ``return_lse`` also the natural-log LSE [B, H_q] of the scaled scores.
+        ``return_lse`` also the natural-log LSE [B, H_q] of the scaled scores.  With
+        ``k_rows``/``v_rows`` [B, H_kv, D] and ``positions`` [B] the step first appends
+        those rows (as ``append_kv``) in the same kernel launch, so the new token can be
+        attended by the same call.
         """
         self._ensure_open()
         qw = fp32_to_bf16_u16(q)
@@ -568,8 +576,15 @@ class AttentionAccelerator:
             raise ValueError(f"context length outside 0..{self.max_seq_len}")
         out = np.empty(shape, dtype=np.uint16)
         lse = np.empty(shape[:2], dtype=np.float32) if return_lse else None
-        self._call("gqa_decode", _lib.as_u16_ptr(qw), _lib.as_i32_ptr(lens), _lib.as_u16_ptr(out),
-                   _lib.as_f32_ptr(lse) if lse is not None else None)
+        lse_ptr = _lib.as_f32_ptr(lse) if lse is not None else None
+        if k_rows is None and v_rows is None and positions is None:
+            self._call("gqa_decode", _lib.as_u16_ptr(qw), _lib.as_i32_ptr(lens), _lib.as_u16_ptr(out), lse_ptr)
+        else:
+            if k_rows is None or v_rows is None or positions is None:
+                raise ValueError("k_rows, v_rows and positions must be given together")
+            k, v, pos = self._check_rows(k_rows, v_rows, positions)
+            self._call("gqa_decode_append", _lib.as_u16_ptr(qw), _lib.as_u16_ptr(k), _lib.as_u16_ptr(v),
+                       _lib.as_i32_ptr(pos), _lib.as_i32_ptr(lens), _lib.as_u16_ptr(out), lse_ptr)
         return (out, lse) if return_lse else out
 
     def submit_query(self, q_heads: np.ndarray, *, b: int = 0, q_pos_base: int = 0, kv_len: int | None = None,

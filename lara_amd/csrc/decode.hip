@@ -22,7 +22,17 @@
 //      (r, c) owning dims 8c..8c+7 of every head for rows r, r+RPL, ...
 // At the end the waves merge in LDS.  A sequence that fits in one split writes the
 // bf16 output directly; otherwise each split writes an fp32 partial (O, m, l) and
-// decode_combine_kernel merges the splits with log-sum-exp weights.
+// decode_combine_kernel merges the splits with log-sum-exp weights.  (Merging inside the
+// split kernel -- the last split to arrive combines -- needs a device-scope release per
+// split, i.e. an L2 write-back per wave on this multi-XCD part, and measured 2.7x slower
+// at batch 64 x 8 kv heads x 8192 keys than the second launch.)
+//
+// Fused append: when k_new/v_new are given, split 0 of every (sequence, kv head) writes
+// the new row to cache row positions[b], and any split whose key range contains that row
+// reads it from k_new/v_new instead of the cache, so no split depends on the write.
+//
+// K/V rows are streamed with nontemporal loads: they are read once per launch and
+// should not displace anything from the L2 / Infinity Cache.
 #include "gqa_internal.h"
 
 #include <math.h>
@@ -89,6 +99,8 @@ __device__ __forceinline__ int clamp_len(int len, int l_max) {
     return len < 0 ? 0 : (len > l_max ? l_max : len);
 }
 
+__device__ __forceinline__ u32x4 ld_stream(const u32x4* p) { return __builtin_nontemporal_load(p); }
+
 template <int D, int G, int NW>
 __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
     constexpr int NCH = D / 8;               // 16-byte words per K/V row
@@ -113,6 +125,18 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
+    const size_t row0 = (size_t)unit * a.l_cap;
+
+    // Fused append (see the file comment): the appended row, if any, and where it goes.
+    const int pos = (a.k_new != nullptr) ? a.positions[b] : -1;
+    const bool has_new = pos >= 0 && pos < a.l_max;
+    const u32x4* knew = reinterpret_cast<const u32x4*>(a.k_new) + (size_t)unit * NCH;
+    const u32x4* vnew = reinterpret_cast<const u32x4*>(a.v_new) + (size_t)unit * NCH;
+    if (has_new && split == 0 && threadIdx.x < 2 * NCH) {
+        const int c = threadIdx.x % NCH;
+        u32x4* dst = reinterpret_cast<u32x4*>(threadIdx.x < NCH ? a.kc : a.vc) + (row0 + pos) * NCH + c;
+        *dst = (threadIdx.x < NCH) ? knew[c] : vnew[c];
+    }
 
     __shared__ __attribute__((aligned(16))) u32x4 lds_k[NW][RK * NCH];
     __shared__ __attribute__((aligned(16))) float lds_p[NW][RK * G];
@@ -147,7 +171,6 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
     float m_run = -INFINITY;  // running max (log2 units) of head gq, uniform over its lanes
     float l_lane = 0.f;       // this lane's share of the running sum of head gq
 
-    const size_t row0 = (size_t)unit * a.l_cap;
     const u32x4* kbase = reinterpret_cast<const u32x4*>(a.kc) + row0 * NCH;
     const u32x4* vbase = reinterpret_cast<const u32x4*>(a.vc) + row0 * NCH;
 
@@ -155,15 +178,18 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
     // touches lies inside the sequence's cache region; rows >= k_end are masked below.
     const int n_rounds = (k_end - k_begin + RK - 1) / RK;
     u32x4 kr[NLD], vr[NLD];
+    // Row `key` of this lane's column: the cache, or the row appended by this launch.
+    auto load_row = [&](int key, u32x4& k, u32x4& v) {
+        const bool fresh = has_new && key == pos;
+        const size_t off = (size_t)key * NCH + cpv;
+        k = ld_stream(fresh ? knew + cpv : kbase + off);
+        v = ld_stream(fresh ? vnew + cpv : vbase + off);
+    };
     int r = wave;
     if (r < n_rounds) {
         const int key0 = k_begin + r * RK;
 #pragma unroll
-        for (int j = 0; j < NLD; ++j) {
-            const size_t off = (size_t)(key0 + j * RPL + rpv) * NCH + cpv;
-            kr[j] = kbase[off];
-            vr[j] = vbase[off];
-        }
+        for (int j = 0; j < NLD; ++j) load_row(key0 + j * RPL + rpv, kr[j], vr[j]);
     }
     for (; r < n_rounds; r += NW) {
         const int key0 = k_begin + r * RK;
@@ -186,11 +212,7 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
         if (r + NW < n_rounds) {
             const int key1 = key0 + NW * RK;
 #pragma unroll
-            for (int j = 0; j < NLD; ++j) {
-                const size_t off = (size_t)(key1 + j * RPL + rpv) * NCH + cpv;
-                kr[j] = kbase[off];
-                vr[j] = vbase[off];
-            }
+            for (int j = 0; j < NLD; ++j) load_row(key1 + j * RPL + rpv, kr[j], vr[j]);
         }
         wave_lds_sync();
 
@@ -304,17 +326,19 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
     }
 }
 
-// Log-sum-exp merge of the split partials of one (sequence, kv head).
+// Log-sum-exp merge of the split partials of one (sequence, kv head); each thread owns
+// (head, dim) output elements.
+constexpr int kCombineThreads = 512;
+
 template <int D, int G>
-__global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(DecodeArgs a) {
     const int unit = blockIdx.x;
     const int b = unit / a.n_kv_heads;
     const int h = unit - b * a.n_kv_heads;
     const int L = clamp_len(a.lens[b], a.l_max);
     const int n_splits = L > 0 ? (L + a.chunk - 1) / a.chunk : 1;
-    if (n_splits <= 1) return;
-    const int H_q = a.n_kv_heads * G;
-    for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
+    if (n_splits <= 1) return;  // written directly by the split kernel
+    for (int idx = threadIdx.x; idx < G * D; idx += kCombineThreads) {
         const int g = idx / D;
         const int d = idx - g * D;
         const size_t base = (size_t)unit * a.max_splits * G + g;  // partial index of split 0
@@ -329,7 +353,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
                 Ls = fmaf(sc, a.part_ml[pidx * 2 + 1], Ls);
             }
         }
-        const size_t row = (size_t)b * H_q + h * G + g;
+        const size_t row = (size_t)b * a.n_kv_heads * G + h * G + g;
         a.out[row * D + d] = f32_to_bf16_rne(Ls > 0.f ? O / Ls : 0.f);
         if (d == 0 && a.lse != nullptr) a.lse[row] = Ls > 0.f ? (M + log2f(Ls)) * kLn2 : -INFINITY;
     }
@@ -346,7 +370,7 @@ hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t s) {
 
 template <int D, int G>
 hipError_t launch_combine_t(const DecodeArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL((decode_combine_kernel<D, G>), dim3(a.batch * a.n_kv_heads), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((decode_combine_kernel<D, G>), dim3(a.batch * a.n_kv_heads), dim3(kCombineThreads), 0, s, a);
     return hipGetLastError();
 }
 
@@ -379,5 +403,6 @@ hipError_t launch_decode(int head_dim, int group, const DecodeArgs& a, hipStream
 hipError_t launch_combine(int head_dim, int group, const DecodeArgs& a, hipStream_t s) {
     LARA_DISPATCH_DG(launch_combine_t, head_dim, group, a, s);
 }
+
 
 }  // namespace lara

@@ -14,7 +14,7 @@ using namespace lara;
 namespace {
 
 constexpr int kMinChunk = 256;     // smallest split (keys); multiple of every decode round size
-constexpr int kTargetDecodeWgs = 2048;
+constexpr int kTargetDecodeWgs = 512;  // 2 per CU: one split per (sequence, kv head) once that fills the GPU
 
 struct Txn {
     int valid = 0;     // a transaction has been submitted (configure + Q staged)
@@ -40,6 +40,7 @@ struct gqa_ctx {
     uint16_t* o_dev = nullptr;   // same size as q_dev
     float* lse_dev = nullptr;    // max(B*H_q, H_q*max_q_len)
     int32_t* lens_dev = nullptr; // [B]
+    int32_t* pos_dev = nullptr;  // [B] append positions (host fused decode)
     uint16_t* rows_dev = nullptr;  // [2][B][H_kv][D] append staging
     uint16_t* o_pinned = nullptr;  // transaction output (host, pinned)
     size_t stage_words = 0;
@@ -122,8 +123,8 @@ int profile_enable(gqa_ctx* c, int on) {
     return GQA_OK;
 }
 
-int run_decode(gqa_ctx* c, const void* q, const int32_t* lens, void* o, float* lse, hipStream_t s,
-               int max_len) {
+int run_decode(gqa_ctx* c, const void* q, const int32_t* lens, const void* k_new, const void* v_new,
+               const int32_t* positions, void* o, float* lse, hipStream_t s, int max_len) {
     if (!decode_supported(c->cfg.head_dim, c->group)) return GQA_ERR_UNSUPPORTED;
     const int chunk = choose_chunk(c, max_len);
     int max_splits = max_len > 0 ? (max_len + chunk - 1) / chunk : 1;
@@ -133,6 +134,9 @@ int run_decode(gqa_ctx* c, const void* q, const int32_t* lens, void* o, float* l
     a.kc = c->k_cache;
     a.vc = c->v_cache;
     a.lens = lens;
+    a.k_new = (const uint16_t*)k_new;
+    a.v_new = (const uint16_t*)v_new;
+    a.positions = positions;
     a.batch = c->cfg.batch;
     a.n_kv_heads = c->cfg.n_kv_heads;
     a.l_cap = c->l_cap;
@@ -288,6 +292,7 @@ int gqa_create(const gqa_config* cfg, gqa_ctx** out_ctx) {
     alloc((void**)&c->o_dev, c->stage_words * 2);
     alloc((void**)&c->lse_dev, c->lse_words * sizeof(float));
     alloc((void**)&c->lens_dev, (size_t)k.batch * sizeof(int32_t));
+    alloc((void**)&c->pos_dev, (size_t)k.batch * sizeof(int32_t));
     alloc((void**)&c->rows_dev, 2 * units * D * 2);
     if (rc == GQA_OK && hipHostMalloc((void**)&c->o_pinned, c->stage_words * 2, 0) != hipSuccess) rc = GQA_ERR_OOM;
     if (rc == GQA_OK && hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) rc = GQA_ERR_HIP;
@@ -321,6 +326,7 @@ int gqa_destroy(gqa_ctx* c) {
     (void)hipFree(c->o_dev);
     (void)hipFree(c->lse_dev);
     (void)hipFree(c->lens_dev);
+    (void)hipFree(c->pos_dev);
     (void)hipFree(c->rows_dev);
     if (c->o_pinned) (void)hipHostFree(c->o_pinned);
     if (c->ev_begin) (void)hipEventDestroy(c->ev_begin);
@@ -467,7 +473,8 @@ int gqa_decode(gqa_ctx* c, const uint16_t* q, const int32_t* ctx_lens, uint16_t*
     HIP_TRY(hipEventRecord(c->ev_begin, c->stream));
     HIP_TRY(hipMemcpyAsync(c->q_dev, q, qwords * 2, hipMemcpyHostToDevice, c->stream));
     HIP_TRY(hipMemcpyAsync(c->lens_dev, ctx_lens, c->cfg.batch * sizeof(int32_t), hipMemcpyHostToDevice, c->stream));
-    rc = run_decode(c, c->q_dev, c->lens_dev, c->o_dev, lse ? c->lse_dev : nullptr, c->stream, max_len);
+    rc = run_decode(c, c->q_dev, c->lens_dev, nullptr, nullptr, nullptr, c->o_dev, lse ? c->lse_dev : nullptr,
+                    c->stream, max_len);
     if (rc != GQA_OK) return rc;
     HIP_TRY(hipMemcpyAsync(o, c->o_dev, qwords * 2, hipMemcpyDeviceToHost, c->stream));
     if (lse)
@@ -478,7 +485,45 @@ int gqa_decode(gqa_ctx* c, const uint16_t* q, const int32_t* ctx_lens, uint16_t*
 
 int gqa_decode_device(gqa_ctx* c, const void* q, const int32_t* ctx_lens, void* o, float* lse, void* stream) {
     if (!c || !q || !ctx_lens || !o) return GQA_ERR_NULL;
-    return run_decode(c, q, ctx_lens, o, lse, pick_stream(c, stream), c->cfg.max_seq_len);
+    return run_decode(c, q, ctx_lens, nullptr, nullptr, nullptr, o, lse, pick_stream(c, stream), c->cfg.max_seq_len);
+}
+
+int gqa_decode_append(gqa_ctx* c, const uint16_t* q, const uint16_t* k_rows, const uint16_t* v_rows,
+                      const int32_t* positions, const int32_t* ctx_lens, uint16_t* o, float* lse) {
+    if (!c || !q || !k_rows || !v_rows || !positions || !ctx_lens || !o) return GQA_ERR_NULL;
+    int max_len = 0;
+    for (int b = 0; b < c->cfg.batch; ++b) {
+        if (ctx_lens[b] < 0 || ctx_lens[b] > c->cfg.max_seq_len) return GQA_ERR_RANGE;
+        if (positions[b] < -1 || positions[b] >= c->cfg.max_seq_len) return GQA_ERR_RANGE;
+        if (ctx_lens[b] > max_len) max_len = ctx_lens[b];
+    }
+    int rc = txn_idle(c);
+    if (rc != GQA_OK) return rc;
+    HIP_TRY(hipSetDevice(c->cfg.device));
+    const size_t qwords = (size_t)c->cfg.batch * c->cfg.n_q_heads * c->cfg.head_dim;
+    const size_t row_words = (size_t)c->cfg.batch * c->cfg.n_kv_heads * c->cfg.head_dim;
+    const size_t i32 = (size_t)c->cfg.batch * sizeof(int32_t);
+    HIP_TRY(hipEventRecord(c->ev_begin, c->stream));
+    HIP_TRY(hipMemcpyAsync(c->q_dev, q, qwords * 2, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(hipMemcpyAsync(c->rows_dev, k_rows, row_words * 2, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(hipMemcpyAsync(c->rows_dev + row_words, v_rows, row_words * 2, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(hipMemcpyAsync(c->pos_dev, positions, i32, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(hipMemcpyAsync(c->lens_dev, ctx_lens, i32, hipMemcpyHostToDevice, c->stream));
+    rc = run_decode(c, c->q_dev, c->lens_dev, c->rows_dev, c->rows_dev + row_words, c->pos_dev, c->o_dev,
+                    lse ? c->lse_dev : nullptr, c->stream, max_len);
+    if (rc != GQA_OK) return rc;
+    HIP_TRY(hipMemcpyAsync(o, c->o_dev, qwords * 2, hipMemcpyDeviceToHost, c->stream));
+    if (lse)
+        HIP_TRY(hipMemcpyAsync(lse, c->lse_dev, (size_t)c->cfg.batch * c->cfg.n_q_heads * sizeof(float),
+                               hipMemcpyDeviceToHost, c->stream));
+    return finish_sync(c);
+}
+
+int gqa_decode_append_device(gqa_ctx* c, const void* q, const void* k_rows, const void* v_rows,
+                             const int32_t* positions, const int32_t* ctx_lens, void* o, float* lse, void* stream) {
+    if (!c || !q || !k_rows || !v_rows || !positions || !ctx_lens || !o) return GQA_ERR_NULL;
+    return run_decode(c, q, ctx_lens, k_rows, v_rows, positions, o, lse, pick_stream(c, stream),
+                      c->cfg.max_seq_len);
 }
 
 int gqa_prefill(gqa_ctx* c, int32_t b, const uint16_t* q, int32_t q_len, int32_t q_pos_base, int32_t kv_len,

@@ -11,9 +11,12 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // Split-KV decode launch description.  All pointers are device pointers.
 struct DecodeArgs {
     const uint16_t* q;      // [B][H_q][D] bf16
-    const uint16_t* kc;     // [B][H_kv][L_cap][D] bf16
-    const uint16_t* vc;     // same layout as kc
+    uint16_t* kc;           // [B][H_kv][L_cap][D] bf16
+    uint16_t* vc;           // same layout as kc
     const int32_t* lens;    // [B] keys attended per sequence
+    const uint16_t* k_new;  // [B][H_kv][D] rows appended by this launch, or nullptr
+    const uint16_t* v_new;  // same layout as k_new
+    const int32_t* positions;  // [B] cache row of the appended row (-1: none), or nullptr
     int32_t batch;
     int32_t n_kv_heads;
     int32_t l_cap;          // cache rows per (b, kv head), multiple of 64
@@ -46,6 +49,8 @@ struct PrefillArgs {
 };
 
 bool decode_supported(int head_dim, int group);
+// Split-KV attention with an optional fused row append; sequences longer than one split
+// leave fp32 partials that launch_combine merges.
 hipError_t launch_decode(int head_dim, int group, const DecodeArgs& a, hipStream_t s);
 hipError_t launch_combine(int head_dim, int group, const DecodeArgs& a, hipStream_t s);
 

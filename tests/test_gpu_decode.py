@@ -197,3 +197,42 @@ def test_decode_full_size_c3_ragged():
 
 def test_decode_full_size_c4_long_context():
     _full_size("c4")
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (64, 8, 128), (16, 8, 64)])
+def test_fused_append_decode_matches_two_launches(hq, hkv, d):
+    """decode_step with rows = append_kv + decode_step, bit for bit, over repeated steps.
+
+    A small split size gives many splits per sequence, so every step exercises the
+    in-kernel merge and the reset of its arrival counters for the next launch.
+    """
+    rng = np.random.default_rng(200 + hq + d)
+    B = 3
+    lens = np.array([700, 1, 1500], np.int32)
+    cap = 1600
+    with make_engine(B, hq, hkv, d, cap) as fused, make_engine(B, hq, hkv, d, cap) as split:
+        kc, vc = fill_cache(fused, rng, B, hkv, d, lens, lcap=cap)
+        for b in range(B):
+            split.load_kv(kc[b, :, :lens[b]], vc[b, :, :lens[b]], b=b)
+        for eng in (fused, split):
+            _lib.check(eng._lib.gqa_set_option(eng._ctx, _lib.GQA_OPT_DECODE_CHUNK, 256), "chunk")
+        cur = lens.copy()
+        for step in range(4):
+            nk = bf16_normal(rng, (B, hkv, d))
+            nv = bf16_normal(rng, (B, hkv, d))
+            pos = cur.copy()
+            pos[1] = -1 if step == 2 else pos[1]  # a sequence that skips the append this step
+            q = bf16_normal(rng, (B, hq, d))
+            attend = np.where(pos >= 0, pos + 1, cur).astype(np.int32)
+            out_f, lse_f = fused.decode_step(q, attend, k_rows=nk, v_rows=nv, positions=pos, return_lse=True)
+            split.append_kv(nk, nv, pos)
+            out_s, lse_s = split.decode_step(q, attend, return_lse=True)
+            assert np.array_equal(out_f, out_s)
+            assert np.array_equal(lse_f.view(np.uint32), lse_s.view(np.uint32))
+            for b in range(B):
+                if pos[b] >= 0:
+                    kc[b, :, pos[b]], vc[b, :, pos[b]] = nk[b], nv[b]
+                    kr, vr = fused.read_kv(b, int(pos[b]), 1)
+                    assert np.array_equal(kr[:, 0], nk[b]) and np.array_equal(vr[:, 0], nv[b])
+            check_decode(out_f, lse_f, q, kc, vc, attend, None)
+            cur = attend
