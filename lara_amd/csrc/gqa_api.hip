@@ -4,6 +4,8 @@
 #include "gqa_internal.h"
 
 #include <math.h>
+
+#include <algorithm>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -14,6 +16,8 @@ using namespace lara;
 namespace {
 
 constexpr int kMinChunk = 256;     // smallest split (keys); multiple of every decode round size
+constexpr int kTargetPrefillWgs = 512;  // 2 per CU
+constexpr int kMaxPrefillSegs = 16;
 constexpr int kTargetDecodeWgs = 512;  // 2 per CU: one split per (sequence, kv head) once that fills the GPU
 
 struct Txn {
@@ -36,6 +40,8 @@ struct gqa_ctx {
     uint16_t* v_cache = nullptr;
     float* part_o = nullptr;
     float* part_ml = nullptr;
+    float* pre_ws = nullptr;     // prefill KV-segment partials (O, then (m, l))
+    size_t pre_ws_floats = 0;
     uint16_t* q_dev = nullptr;   // staging: max(B*H_q*D, H_q*max_q_len*D) words
     uint16_t* o_dev = nullptr;   // same size as q_dev
     float* lse_dev = nullptr;    // max(B*H_q, H_q*max_q_len)
@@ -173,6 +179,11 @@ int check_prefill_args(const gqa_ctx* c, int32_t b, int32_t q_len, int32_t q_pos
 int run_prefill(gqa_ctx* c, int32_t b, const void* q, int32_t q_len, int32_t q_pos_base, int32_t kv_len,
                 int32_t kv_pos_base, int32_t causal, void* o, float* lse, hipStream_t s) {
     if (!prefill_supported(c->cfg.head_dim, c->group)) return GQA_ERR_UNSUPPORTED;
+    int kv_span = kv_len;
+    if (causal) kv_span = std::min(kv_len, std::max(0, q_pos_base + q_len - kv_pos_base));
+    PrefillPlan plan = plan_prefill(q_len, kv_span, c->group, c->cfg.n_kv_heads, kTargetPrefillWgs, kMaxPrefillSegs);
+    if (prefill_workspace_floats(plan, q_len, c->cfg.n_q_heads, c->cfg.head_dim) > c->pre_ws_floats)
+        plan = plan_prefill(q_len, kv_span, c->group, c->cfg.n_kv_heads, 1, 1);  // one segment
     PrefillArgs a{};
     const size_t seq_off = (size_t)b * c->cfg.n_kv_heads * c->l_cap * c->cfg.head_dim;
     a.q = (const uint16_t*)q;
@@ -189,9 +200,18 @@ int run_prefill(gqa_ctx* c, int32_t b, const void* q, int32_t q_len, int32_t q_p
     a.scale_log2 = c->scale * 1.4426950408889634f;
     a.out = (uint16_t*)o;
     a.lse = lse;
+    a.seg_len = plan.seg_len;
+    a.n_segs = plan.n_segs;
+    a.part_o = c->pre_ws;
+    a.part_ml = c->pre_ws + (size_t)plan.n_segs * c->cfg.n_q_heads * q_len * c->cfg.head_dim;
     timer_begin(c, GQA_TIMER_PREFILL, s);
     HIP_TRY(launch_prefill(c->cfg.head_dim, c->group, a, s));
     timer_end(c, GQA_TIMER_PREFILL, s);
+    if (plan.n_segs > 1) {
+        timer_begin(c, GQA_TIMER_COMBINE, s);
+        HIP_TRY(launch_prefill_combine(c->cfg.head_dim, a, s));
+        timer_end(c, GQA_TIMER_COMBINE, s);
+    }
     return GQA_OK;
 }
 
@@ -288,6 +308,16 @@ int gqa_create(const gqa_config* cfg, gqa_ctx** out_ctx) {
     alloc((void**)&c->v_cache, kv_words(c) * 2);
     alloc((void**)&c->part_o, units * c->max_splits_cap * group * D * sizeof(float));
     alloc((void**)&c->part_ml, units * c->max_splits_cap * group * 2 * sizeof(float));
+    if (prefill_supported(k.head_dim, group)) {
+        // Largest segmented plan over every query length up to max_q_len (keys up to L_max).
+        for (int q_len = 32; q_len < k.max_q_len + 32; q_len += 32) {
+            const int ql = q_len < k.max_q_len ? q_len : k.max_q_len;
+            const PrefillPlan p = plan_prefill(ql, k.max_seq_len, group, k.n_kv_heads, kTargetPrefillWgs, kMaxPrefillSegs);
+            const size_t f = prefill_workspace_floats(p, ql, k.n_q_heads, k.head_dim);
+            if (f > c->pre_ws_floats) c->pre_ws_floats = f;
+        }
+        if (c->pre_ws_floats > 0) alloc((void**)&c->pre_ws, c->pre_ws_floats * sizeof(float));
+    }
     alloc((void**)&c->q_dev, c->stage_words * 2);
     alloc((void**)&c->o_dev, c->stage_words * 2);
     alloc((void**)&c->lse_dev, c->lse_words * sizeof(float));
@@ -322,6 +352,7 @@ int gqa_destroy(gqa_ctx* c) {
     (void)hipFree(c->v_cache);
     (void)hipFree(c->part_o);
     (void)hipFree(c->part_ml);
+    (void)hipFree(c->pre_ws);
     (void)hipFree(c->q_dev);
     (void)hipFree(c->o_dev);
     (void)hipFree(c->lse_dev);

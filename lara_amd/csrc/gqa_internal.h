@@ -46,7 +46,21 @@ struct PrefillArgs {
     float scale_log2;
     uint16_t* out;          // [H_q][q_len][D] bf16
     float* lse;             // [H_q][q_len] or nullptr
+    int32_t seg_len;        // keys per KV segment (multiple of 64)
+    int32_t n_segs;         // KV segments (grid z); 1 = write the output directly
+    float* part_o;          // [n_segs][H_q][q_len][D] fp32 un-normalised partial O
+    float* part_ml;         // [n_segs][H_q][q_len][2] (running max in log2 units, sum)
 };
+
+// KV segmentation of a prefill launch: (seg_len, n_segs) for q_len query rows whose
+// attended key span is kv_span, sized so the launch has about target_wgs work-groups.
+struct PrefillPlan {
+    int32_t seg_len;
+    int32_t n_segs;
+};
+PrefillPlan plan_prefill(int q_len, int kv_span, int group, int n_kv_heads, int target_wgs, int max_segs);
+// fp32 words of partial-output workspace a plan needs (O and (m, l) per row, per segment).
+size_t prefill_workspace_floats(const PrefillPlan& p, int q_len, int n_q_heads, int head_dim);
 
 bool decode_supported(int head_dim, int group);
 // Split-KV attention with an optional fused row append; sequences longer than one split
@@ -56,13 +70,16 @@ hipError_t launch_combine(int head_dim, int group, const DecodeArgs& a, hipStrea
 
 bool prefill_supported(int head_dim, int group);
 hipError_t launch_prefill(int head_dim, int group, const PrefillArgs& a, hipStream_t s);
+// Merges the KV segments of a prefill launch with n_segs > 1.
+hipError_t launch_prefill_combine(int head_dim, const PrefillArgs& a, hipStream_t s);
 
 // K/V row append: rows [B][H_kv][D] -> cache row positions[b] (skipped if < 0 or >= l_max).
 hipError_t launch_append(const uint16_t* k_rows, const uint16_t* v_rows, const int32_t* positions,
                          uint16_t* kc, uint16_t* vc, int batch, int n_kv_heads, int head_dim,
                          int l_cap, int l_max, hipStream_t s);
 
-// fp32 -> bf16 word, round to nearest even on the upper half (sw/attn_driver.py:88-98).
+// fp32 -> bf16 word, round to nearest even on the upper half: the output rounding of
+// fp32_to_bf16 in hw/rtl/pkg/attn_pkg.sv:618-626 (no NaN special case).
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float x) {
     uint32_t bits = __float_as_uint(x);
     uint32_t lsb = (bits >> 16) & 1u;

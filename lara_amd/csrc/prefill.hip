@@ -22,6 +22,11 @@
 // MFMA result), so the softmax state of a row and its O accumulator live in the same lane
 // and no cross-lane shuffle is needed between the two products.
 //
+// KV segments.  A chunk of a few hundred query rows gives only tens of work-groups per KV
+// head, too few for 256 CUs, so the key range is cut into segments (grid z): each
+// work-group attends one segment and writes an fp32 partial (O, m, l) per row, and
+// prefill_combine_kernel merges a row's segments with log-sum-exp weights.
+//
 // MFMA 32x32x16 operand layout used below: lane l supplies row (A) / column (B) l % 32 and
 // the eight k-values 8*(l/32)..8*(l/32)+7 of the step; result register i of lane l holds
 // row 8*(i/4) + 4*(l/32) + (i%4), column l % 32.  The products only require A and B to
@@ -67,7 +72,8 @@ __device__ __forceinline__ int k_swz(int row) {
 __device__ __forceinline__ int vt_swz(int dim) { return (dim >> 1) & 7; }
 
 template <int D, int G>
-__global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_kernel(
+    PrefillArgs a) {
     constexpr int NCH = D / 8;                 // 16-byte chunks per K/V row
     constexpr int KSTEPS = D / 16;             // QK k-steps
     constexpr int MT = D / 32;                 // PV result tiles (32 dims each)
@@ -102,7 +108,12 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
     const int last_task = min(n_tasks, (int)(blockIdx.x + 1) * kWaves) - 1;
     const int wg_hi = kv_limit(last_task / G);  // row blocks grow with the task index
     const int wave_hi = active ? kv_limit(rb) : 0;
-    const int n_blocks = (wg_hi + kBN - 1) / kBN;
+    const int seg_begin = blockIdx.z * a.seg_len;
+    // With several segments, one that no row of this work-group reaches is not read by the
+    // merge; a single segment always reaches the epilogue (rows without keys output 0).
+    if (a.n_segs > 1 && seg_begin >= wg_hi) return;
+    const int seg_end = min(wg_hi, seg_begin + a.seg_len);
+    const int n_blocks = seg_end > seg_begin ? (seg_end - seg_begin + kBN - 1) / kBN : 0;
 
     const int col = lane & 31;   // query row within the wave's block (MFMA column)
     const int half = lane >> 5;  // which 8 k-values of a step this lane carries
@@ -174,10 +185,10 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
         }
     };
 
-    if (n_blocks > 0) load_block(0);
+    if (n_blocks > 0) load_block(seg_begin);
     for (int blk = 0; blk < n_blocks; ++blk) {
         const int buf = blk & 1;
-        const int j0 = blk * kBN;
+        const int j0 = seg_begin + blk * kBN;
         store_block(buf);
         __syncthreads();
         if (blk + 1 < n_blocks) load_block(j0 + kBN);
@@ -253,6 +264,20 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
 
     if (!row_ok) return;
     const float l_row = l_lane + __shfl_xor(l_lane, 32);
+    if (a.n_segs > 1) {
+        // Rows this wave never reached in the segment are not read by the merge.
+        if (seg_begin >= wave_hi) return;
+        const size_t prow = ((size_t)blockIdx.z * a.n_q_heads + hq) * a.q_len + row;
+        float* po = a.part_o + prow * D;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4)
+                *reinterpret_cast<float4*>(po + mt * 32 + 8 * r4 + 4 * half) =
+                    make_float4(o[mt][4 * r4 + 0], o[mt][4 * r4 + 1], o[mt][4 * r4 + 2], o[mt][4 * r4 + 3]);
+        if (half == 0) *reinterpret_cast<float2*>(a.part_ml + prow * 2) = make_float2(m_run, l_row);
+        return;
+    }
     const float inv = l_row > 0.f ? 1.f / l_row : 0.f;
     uint16_t* orow = a.out + ((size_t)hq * a.q_len + row) * D;
 #pragma unroll
@@ -268,16 +293,74 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
         a.lse[(size_t)hq * a.q_len + row] = l_row > 0.f ? (m_run + log2f(l_row)) * kLn2 : -INFINITY;
 }
 
+// Merge of a row's KV segments: one work-group per (query row, query head), one thread per
+// dim.  Segment s holds keys [s*seg_len, (s+1)*seg_len); a row reads the segments below its
+// own key limit, which are exactly the ones prefill_kernel wrote for it.
+template <int D>
+__global__ __launch_bounds__(D) void prefill_combine_kernel(PrefillArgs a) {
+    const int row = blockIdx.x;
+    const int hq = blockIdx.y;
+    const int d = threadIdx.x;
+    int hi = a.kv_len;
+    if (a.causal) hi = min(hi, a.q_pos_base + row - a.kv_pos_base + 1);
+    hi = max(hi, 0);
+    const int n_valid = min(a.n_segs, (hi + a.seg_len - 1) / a.seg_len);
+    const size_t seg_stride = (size_t)a.n_q_heads * a.q_len;
+    const size_t prow = (size_t)hq * a.q_len + row;
+    float M = -INFINITY;
+    for (int sp = 0; sp < n_valid; ++sp) M = fmaxf(M, a.part_ml[(sp * seg_stride + prow) * 2]);
+    float O = 0.f, Ls = 0.f;
+    if (M != -INFINITY) {
+        for (int sp = 0; sp < n_valid; ++sp) {
+            const size_t pr = sp * seg_stride + prow;
+            const float w = __builtin_amdgcn_exp2f(a.part_ml[pr * 2] - M);
+            O = fmaf(w, a.part_o[pr * D + d], O);
+            Ls = fmaf(w, a.part_ml[pr * 2 + 1], Ls);
+        }
+    }
+    a.out[prow * D + d] = f32_to_bf16_rne(Ls > 0.f ? O / Ls : 0.f);
+    if (d == 0 && a.lse != nullptr) a.lse[prow] = Ls > 0.f ? (M + log2f(Ls)) * kLn2 : -INFINITY;
+}
+
 template <int D, int G>
 hipError_t launch_prefill_t(const PrefillArgs& a, hipStream_t s) {
     const int n_rb = (a.q_len + kRows - 1) / kRows;
     const int n_tasks = n_rb * G;
-    dim3 grid((n_tasks + kWaves - 1) / kWaves, a.n_kv_heads);
+    dim3 grid((n_tasks + kWaves - 1) / kWaves, a.n_kv_heads, a.n_segs);
     hipLaunchKernelGGL((prefill_kernel<D, G>), grid, dim3(kWaves * 64), 0, s, a);
     return hipGetLastError();
 }
 
 }  // namespace
+
+PrefillPlan plan_prefill(int q_len, int kv_span, int group, int n_kv_heads, int target_wgs, int max_segs) {
+    const int n_rb = (q_len + kRows - 1) / kRows;
+    const int base = ((n_rb * group + kWaves - 1) / kWaves) * n_kv_heads;
+    const int blocks = (kv_span + kBN - 1) / kBN;
+    int segs = (target_wgs + base - 1) / base;
+    segs = min(segs, max_segs);
+    segs = min(segs, blocks);
+    if (segs <= 1) return PrefillPlan{blocks > 0 ? blocks * kBN : kBN, 1};
+    const int seg_blocks = (blocks + segs - 1) / segs;
+    const int seg_len = seg_blocks * kBN;
+    return PrefillPlan{seg_len, (blocks + seg_blocks - 1) / seg_blocks};
+}
+
+size_t prefill_workspace_floats(const PrefillPlan& p, int q_len, int n_q_heads, int head_dim) {
+    if (p.n_segs <= 1) return 0;
+    return (size_t)p.n_segs * n_q_heads * q_len * (head_dim + 2);
+}
+
+hipError_t launch_prefill_combine(int head_dim, const PrefillArgs& a, hipStream_t s) {
+    if (head_dim == 128) {
+        hipLaunchKernelGGL(prefill_combine_kernel<128>, dim3(a.q_len, a.n_q_heads), dim3(128), 0, s, a);
+    } else if (head_dim == 64) {
+        hipLaunchKernelGGL(prefill_combine_kernel<64>, dim3(a.q_len, a.n_q_heads), dim3(64), 0, s, a);
+    } else {
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
 
 bool prefill_supported(int head_dim, int group) {
     return (head_dim == 64 || head_dim == 128) && (group == 1 || group == 2 || group == 4 || group == 8 || group == 16);
