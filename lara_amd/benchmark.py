@@ -144,6 +144,66 @@ def prefill_flops(n_q_heads: int, head_dim: int, pairs: int) -> int:
     return 2 * (2 * n_q_heads * pairs * head_dim)
 
 
+# ---------------------------------------------------------------------------------------
+# report metrics (the board harness's, sw/board_performance.py:195-273)
+# ---------------------------------------------------------------------------------------
+
+def stats(values) -> dict:
+    """min / median / p95 / max of a sample (sw/board_performance.py:195-204)."""
+    arr = np.asarray(list(values), dtype=np.float64)
+    if arr.size == 0:
+        raise ValueError("cannot summarize an empty sample")
+    return {"min": float(arr.min()), "median": float(np.median(arr)), "p95": float(np.percentile(arr, 95)),
+            "max": float(arr.max())}
+
+
+def numeric_error(actual, reference) -> dict:
+    """Error metrics of sw/board_performance.py:207-219 (relative error floored at 1e-6)."""
+    a = np.asarray(actual, dtype=np.float64)
+    r = np.asarray(reference, dtype=np.float64)
+    delta = a - r
+    ref_rms = float(np.sqrt(np.mean(r * r)))
+    rmse = float(np.sqrt(np.mean(delta * delta)))
+    return {
+        "max_abs": float(np.max(np.abs(delta))),
+        "mean_abs": float(np.mean(np.abs(delta))),
+        "rmse": rmse,
+        "normalized_rmse": rmse / max(ref_rms, 1.0e-12),
+        "max_relative_floor_1e-6": float(np.max(np.abs(delta) / np.maximum(np.abs(r), 1.0e-6))),
+    }
+
+
+def collect_environment() -> dict:
+    """Host environment of a run (the GPU-host analogue of sw/board_performance.py:237-273)."""
+    import os
+    import platform
+    import socket
+    import sys
+    from datetime import datetime, timezone
+
+    model = None
+    try:
+        for line in open("/proc/cpuinfo", encoding="utf-8"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "timestamp_utc": datetime.now(timezone.utc).isoformat(),
+        "hostname": socket.gethostname(),
+        "platform": platform.platform(),
+        "python": sys.version.split()[0],
+        "numpy": np.__version__,
+        "cpu_model": model,
+        "os_cpu_count": os.cpu_count(),
+        "process_affinity": sorted(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None,
+        "thread_environment": {name: os.environ.get(name) for name in
+                               ("OMP_NUM_THREADS", "OPENBLAS_NUM_THREADS", "MKL_NUM_THREADS", "NUMEXPR_NUM_THREADS",
+                                "LARA_CPU_THREADS")},
+    }
+
+
 def prefill_chunk_schedule(w: PrefillWorkload):
     """(q_pos_base, q_len, kv_len) of every chunk of a chunked prefill."""
     out = []

@@ -106,3 +106,16 @@ def test_workload_lengths():
     assert np.all(bm.WORKLOADS["ns"].lengths() == 8192)
     sched = bm.prefill_chunk_schedule(bm.PREFILL_WORKLOADS["c5"])
     assert len(sched) == 8 and sched[-1] == (1792, 256, 2048)
+
+
+def test_report_metrics_closed_forms():
+    s = bm.stats([3.0, 1.0, 2.0, 4.0])
+    assert s["min"] == 1.0 and s["max"] == 4.0 and s["median"] == 2.5
+    assert abs(s["p95"] - 3.85) < 1e-12
+    e = bm.numeric_error(np.array([1.0, 2.0, 0.0]), np.array([1.0, 1.0, 0.0]))
+    assert e["max_abs"] == 1.0 and abs(e["mean_abs"] - 1 / 3) < 1e-15
+    assert abs(e["rmse"] - np.sqrt(1 / 3)) < 1e-15
+    assert abs(e["normalized_rmse"] - np.sqrt(1 / 3) / np.sqrt(2 / 3)) < 1e-15
+    assert e["max_relative_floor_1e-6"] == 1.0
+    env = bm.collect_environment()
+    assert env["os_cpu_count"] >= 1 and "thread_environment" in env
