@@ -170,7 +170,7 @@ def measure(name: str, steps: int, warmup: int, chunk: int = 0) -> dict:
 class PrefillBench:
     """Chunked causal prefill: every chunk appends its K/V rows, then attends the growing cache."""
 
-    def __init__(self, w, device: int = 0):
+    def __init__(self, w, device: int = 0, target_wgs: int = 0):
         import torch
         from lara_amd import _lib
 
@@ -181,6 +181,8 @@ class PrefillBench:
         cfg = _lib.GqaConfig(1, w.n_q_heads, w.n_kv_heads, w.head_dim, w.prompt, w.chunk, 0.0, device)
         self.ctx = ctypes.c_void_p()
         _lib.check(self.lib.gqa_create(ctypes.byref(cfg), ctypes.byref(self.ctx)), "gqa_create")
+        if target_wgs:
+            _lib.check(self.lib.gqa_set_option(self.ctx, _lib.GQA_OPT_PREFILL_WGS, target_wgs), "prefill wgs")
         dev = torch.device("cuda", device)
         self.stream = torch.cuda.current_stream(dev)
         self.sptr = ctypes.c_void_p(self.stream.cuda_stream)
@@ -203,13 +205,12 @@ class PrefillBench:
     def step(self) -> None:
         c = ctypes.c_void_p
         for start, q_len, kv_len, qc, kc, vc in self.chunks:
-            rc = self.lib.gqa_load_kv_device(self.ctx, 0, start, q_len, c(kc.data_ptr()), c(vc.data_ptr()), self.sptr)
+            # One launch per chunk: place the chunk's K/V rows and attend rows 0..kv_len-1.
+            rc = self.lib.gqa_prefill_append_device(self.ctx, 0, c(qc.data_ptr()), c(kc.data_ptr()),
+                                                    c(vc.data_ptr()), q_len, q_len, start, kv_len, 0, 1,
+                                                    c(self.o.data_ptr()), None, self.sptr)
             if rc:
-                self._lib.check(rc, "load_kv_device")
-            rc = self.lib.gqa_prefill_device(self.ctx, 0, c(qc.data_ptr()), q_len, start, kv_len, 0, 1,
-                                             c(self.o.data_ptr()), None, self.sptr)
-            if rc:
-                self._lib.check(rc, "prefill_device")
+                self._lib.check(rc, "prefill_append_device")
 
     def run(self, steps: int, warmup: int) -> dict:
         torch = self.torch
@@ -225,20 +226,24 @@ class PrefillBench:
         wall_ms = (time.perf_counter() - t0) * 1e3 / steps
         times = (ctypes.c_float * _lib.GQA_TIMER_COUNT)()
         _lib.check(self.lib.gqa_kernel_times(self.ctx, times, _lib.GQA_TIMER_COUNT), "kernel times")
+        counts = (ctypes.c_int32 * _lib.GQA_TIMER_COUNT)()
+        _lib.check(self.lib.gqa_kernel_launch_counts(self.ctx, counts, _lib.GQA_TIMER_COUNT), "counts")
         _lib.check(self.lib.gqa_set_option(self.ctx, _lib.GQA_OPT_PROFILE, 0), "profile off")
-        return {"wall_ms_per_prompt": wall_ms, "prefill_us_per_launch": times[_lib.GQA_TIMER_PREFILL]}
+        merges = counts[_lib.GQA_TIMER_COMBINE] / max(1, counts[_lib.GQA_TIMER_PREFILL])
+        return {"wall_ms_per_prompt": wall_ms, "prefill_us_per_launch": times[_lib.GQA_TIMER_PREFILL],
+                "merge_us_per_launch": times[_lib.GQA_TIMER_COMBINE] * merges}
 
     def close(self) -> None:
         self.lib.gqa_destroy(self.ctx)
 
 
-def measure_prefill(name: str, steps: int, warmup: int) -> dict:
+def measure_prefill(name: str, steps: int, warmup: int, target_wgs: int = 0) -> dict:
     from lara_amd.benchmark import BF16_DENSE_TFLOPS, PREFILL_WORKLOADS, prefill_chunk_schedule, prefill_flops, \
         valid_pairs
 
     w = PREFILL_WORKLOADS[name]
     log(f"{name}: chunked prefill set-up")
-    bench = PrefillBench(w)
+    bench = PrefillBench(w, target_wgs=target_wgs)
     try:
         r = bench.run(steps, warmup)
     finally:
@@ -247,17 +252,20 @@ def measure_prefill(name: str, steps: int, warmup: int) -> dict:
     pairs = sum(valid_pairs(ql, kl, causal=w.causal, q_pos_base=qb) for qb, ql, kl in sched)
     flops = prefill_flops(w.n_q_heads, w.head_dim, pairs)
     kern_us = r["prefill_us_per_launch"] * len(sched)
+    merge_us = r["merge_us_per_launch"] * len(sched)
     out = {
         "us_per_prompt": r["wall_ms_per_prompt"] * 1e3,
         "prefill_kernel_us_per_prompt": kern_us,
+        "segment_merge_us_per_prompt": merge_us,
+        "kernels_tflops_incl_merge": flops / ((kern_us + merge_us) * 1e-6) / 1e12 if kern_us > 0 else None,
         "chunks": len(sched),
         "flops_per_prompt": flops,
         "kernel_tflops": flops / (kern_us * 1e-6) / 1e12 if kern_us > 0 else None,
         "tokens_per_s": w.prompt / (r["wall_ms_per_prompt"] * 1e-3),
     }
     out["mfma_frac_of_bf16_peak"] = out["kernel_tflops"] / BF16_DENSE_TFLOPS if out["kernel_tflops"] else None
-    log(f"{name}: {out['us_per_prompt']:.1f} us/prompt, kernels {kern_us:.1f} us = {out['kernel_tflops'] or 0:.1f} "
-        f"TFLOP/s")
+    log(f"{name}: {out['us_per_prompt']:.1f} us/prompt, prefill kernels {kern_us:.1f} us = "
+        f"{out['kernel_tflops'] or 0:.1f} TFLOP/s, segment merges {merge_us:.1f} us")
     return out
 
 
@@ -436,6 +444,8 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--workload", default="ns", choices=sorted(WORKLOAD_NAMES))
     parser.add_argument("--chunk", type=int, default=0, help="keys per split-KV work-group (0 = auto)")
+    parser.add_argument("--prefill-wgs", type=int, default=0,
+                        help="work-groups the prefill KV segmentation aims for (0 = auto, 1 = no segments)")
     parser.add_argument("--others", default="c2,c3,c4,c5", help="extra decode workloads to report ('' = none)")
     parser.add_argument("--cpu-seconds", type=float, default=12.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
@@ -470,7 +480,7 @@ def main() -> int:
     others = {}
     for name in [x for x in args.others.split(",") if x and x != args.workload]:
         if name == "c5":
-            others[name] = measure_prefill(name, max(10, args.steps // 2), max(2, args.warmup // 2))
+            others[name] = measure_prefill(name, max(10, args.steps // 2), max(2, args.warmup // 2), args.prefill_wgs)
             continue
         r = measure(name, max(10, args.steps // 2), max(2, args.warmup // 2))
         others[name] = {k: r[k] for k in ("us_per_step", "step_gbps", "step_frac_of_peak", "decode_us",
@@ -517,7 +527,8 @@ def main() -> int:
             "n_kv_heads": w.n_kv_heads,
             "head_dim": w.head_dim,
             "attended_keys": int(w.lengths().max()),
-            "step": "one launch: append 1 K/V row per sequence + split-KV decode + in-kernel LSE merge",
+            "step": "append 1 K/V row per sequence fused into the split-KV decode launch (a second LSE-merge "
+                    "launch only when a sequence spans several splits; none at this shape)",
             "accumulate": "fp32",
         },
         "kernels_us": {"decode_step": main_r["decode_us"]},

@@ -61,6 +61,7 @@ extern "C" {
 /* Tunables for gqa_set_option. */
 #define GQA_OPT_DECODE_CHUNK 1 /* keys per split-KV work-group (multiple of 64; 0 = auto) */
 #define GQA_OPT_PROFILE      2 /* 1 = time every kernel launch with HIP events (restarts the record) */
+#define GQA_OPT_PREFILL_WGS  3 /* prefill work-groups the KV segmentation aims for (0 = auto, 1 = none) */
 
 typedef struct gqa_config {
     int32_t batch;       /* B: sequences resident in the cache                         */
@@ -127,6 +128,14 @@ int gqa_prefill(gqa_ctx* ctx, int32_t b, const uint16_t* q, int32_t q_len,
                 int32_t q_pos_base, int32_t kv_len, int32_t kv_pos_base, int32_t causal,
                 uint16_t* o, float* lse);
 
+/* gqa_prefill_append: one chunk of a chunked prefill as a single launch -- place the chunk's
+ * own K/V rows (k_rows, v_rows host [H_kv][n_new][D]) at cache rows kv_len-n_new .. kv_len-1 of
+ * sequence b (bit-exact, as gqa_load_kv) and attend as gqa_prefill.  Replaces the per-transaction
+ * K/V DMA + run_attention pair (attn_driver.py:418-550) when the cache grows chunk by chunk. */
+int gqa_prefill_append(gqa_ctx* ctx, int32_t b, const uint16_t* q, const uint16_t* k_rows,
+                       const uint16_t* v_rows, int32_t n_new, int32_t q_len, int32_t q_pos_base,
+                       int32_t kv_len, int32_t kv_pos_base, int32_t causal, uint16_t* o, float* lse);
+
 /* ---- transaction protocol (configure / start / status / wait_done / readback) -----
  * gqa_submit replaces configure() + the Q DMA (attn_driver.py:364-376, 423-432): it
  * validates the transaction and stages q (host head-major [H_q][q_len][D]) in HBM.
@@ -160,6 +169,10 @@ int gqa_decode_append_device(gqa_ctx* ctx, const void* q, const void* k_rows, co
 int gqa_prefill_device(gqa_ctx* ctx, int32_t b, const void* q, int32_t q_len,
                        int32_t q_pos_base, int32_t kv_len, int32_t kv_pos_base,
                        int32_t causal, void* o, float* lse, void* stream);
+int gqa_prefill_append_device(gqa_ctx* ctx, int32_t b, const void* q, const void* k_rows,
+                              const void* v_rows, int32_t n_new, int32_t q_len, int32_t q_pos_base,
+                              int32_t kv_len, int32_t kv_pos_base, int32_t causal, void* o, float* lse,
+                              void* stream);
 /* gqa_load_kv_device: gqa_load_kv from device memory (k, v are [H_kv][n][D] in HBM). */
 int gqa_load_kv_device(gqa_ctx* ctx, int32_t b, int32_t start_pos, int32_t n,
                        const void* k, const void* v, void* stream);

@@ -42,6 +42,7 @@ GQA_TIMER_COUNT = 4
 
 GQA_OPT_DECODE_CHUNK = 1
 GQA_OPT_PROFILE = 2
+GQA_OPT_PREFILL_WGS = 3
 
 
 class GqaConfig(Structure):
@@ -83,6 +84,8 @@ _SIGNATURES = {
     "gqa_decode": [_CTX, _P16, _P32, _P16, _PF],
     "gqa_decode_append": [_CTX, _P16, _P16, _P16, _P32, _P32, _P16, _PF],
     "gqa_prefill": [_CTX, c_int32, _P16, c_int32, c_int32, c_int32, c_int32, c_int32, _P16, _PF],
+    "gqa_prefill_append": [_CTX, c_int32, _P16, _P16, _P16, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,
+                           _P16, _PF],
     "gqa_submit": [_CTX, c_int32, _P16, c_int32, c_int32, c_int32, c_int32, c_int32],
     "gqa_start": [_CTX],
     "gqa_status": [_CTX, POINTER(c_uint32)],
@@ -96,6 +99,8 @@ _SIGNATURES = {
                                  c_void_p],
     "gqa_prefill_device": [_CTX, c_int32, c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_void_p,
                            c_void_p, c_void_p],
+    "gqa_prefill_append_device": [_CTX, c_int32, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32,
+                                  c_int32, c_int32, c_void_p, c_void_p, c_void_p],
     "gqa_cache_pointers": [_CTX, POINTER(c_void_p), POINTER(c_void_p), _P32],
     "gqa_last_elapsed_us": [_CTX, _PF],
     "gqa_kernel_times": [_CTX, _PF, c_int32],

@@ -615,8 +615,13 @@ class AttentionAccelerator:
         return self.readback_o(self._txn_len)
 
     def prefill_chunk(self, q_heads: np.ndarray, *, b: int = 0, q_pos_base: int = 0, kv_len: int | None = None,
-                      kv_pos_base: int = 0, causal: bool = True, return_lse: bool = False):
-        """Attend a block of query rows against cache rows 0..kv_len-1 (synchronous)."""
+                      kv_pos_base: int = 0, causal: bool = True, k_rows: np.ndarray | None = None,
+                      v_rows: np.ndarray | None = None, return_lse: bool = False):
+        """Attend a block of query rows [H_q, q_len, D] against cache rows 0..kv_len-1 (synchronous).
+
+        With ``k_rows``/``v_rows`` [H_kv, n, D] the same launch first places those rows at cache
+        rows kv_len-n .. kv_len-1 (the chunk's own keys of a chunked prefill), bit-exact.
+        """
         self._ensure_open()
         qw = fp32_to_bf16_u16(q_heads)
         if qw.ndim != 3 or qw.shape[0] != self.n_q_heads or qw.shape[2] != self.head_dim:
@@ -625,12 +630,28 @@ class AttentionAccelerator:
         kv_len = q_pos_base + q_len if kv_len is None else int(kv_len)
         if not 1 <= q_len <= self.max_q_len or not 0 <= kv_len <= self.max_seq_len:
             raise ValueError("q_len or kv_len outside the configured capacity")
+        if not 0 <= b < self.batch:
+            raise ValueError(f"sequence index {b} outside 0..{self.batch - 1}")
         self._check_positions(q_pos_base, kv_pos_base, q_len, kv_len)
         out = np.empty_like(qw)
         lse = np.empty((self.n_q_heads, q_len), dtype=np.float32) if return_lse else None
-        self._call("gqa_prefill", int(b), _lib.as_u16_ptr(qw), int(q_len), int(q_pos_base), int(kv_len),
-                   int(kv_pos_base), int(bool(causal)), _lib.as_u16_ptr(out),
-                   _lib.as_f32_ptr(lse) if lse is not None else None)
+        lse_ptr = _lib.as_f32_ptr(lse) if lse is not None else None
+        if k_rows is None and v_rows is None:
+            self._call("gqa_prefill", int(b), _lib.as_u16_ptr(qw), int(q_len), int(q_pos_base), int(kv_len),
+                       int(kv_pos_base), int(bool(causal)), _lib.as_u16_ptr(out), lse_ptr)
+        else:
+            if k_rows is None or v_rows is None:
+                raise ValueError("k_rows and v_rows must be given together")
+            k = fp32_to_bf16_u16(k_rows)
+            v = fp32_to_bf16_u16(v_rows)
+            if k.ndim != 3 or k.shape != v.shape or k.shape[0] != self.n_kv_heads or k.shape[2] != self.head_dim:
+                raise ValueError(f"expected K/V rows of shape ({self.n_kv_heads}, n, {self.head_dim}); got {k.shape}")
+            n = k.shape[1]
+            if not 1 <= n <= min(kv_len, self.max_q_len):
+                raise ValueError(f"{n} new rows do not fit below kv_len {kv_len} (at most {self.max_q_len})")
+            self._call("gqa_prefill_append", int(b), _lib.as_u16_ptr(qw), _lib.as_u16_ptr(k), _lib.as_u16_ptr(v),
+                       int(n), int(q_len), int(q_pos_base), int(kv_len), int(kv_pos_base), int(bool(causal)),
+                       _lib.as_u16_ptr(out), lse_ptr)
         return (out, lse) if return_lse else out
 
     def run_attention(

@@ -48,10 +48,12 @@ struct gqa_ctx {
     int32_t* lens_dev = nullptr; // [B]
     int32_t* pos_dev = nullptr;  // [B] append positions (host fused decode)
     uint16_t* rows_dev = nullptr;  // [2][B][H_kv][D] append staging
+    uint16_t* new_dev = nullptr;   // [2][H_kv][max_q_len][D] chunk-append staging
     uint16_t* o_pinned = nullptr;  // transaction output (host, pinned)
     size_t stage_words = 0;
     size_t lse_words = 0;
     int chunk_opt = 0;
+    int prefill_wgs_opt = 0;
     int profile = 0;
     hipEvent_t ev_begin = nullptr, ev_end = nullptr;
     // Profiling: a pool of event pairs per timer slot, filled launch by launch.
@@ -177,11 +179,13 @@ int check_prefill_args(const gqa_ctx* c, int32_t b, int32_t q_len, int32_t q_pos
 }
 
 int run_prefill(gqa_ctx* c, int32_t b, const void* q, int32_t q_len, int32_t q_pos_base, int32_t kv_len,
-                int32_t kv_pos_base, int32_t causal, void* o, float* lse, hipStream_t s) {
+                int32_t kv_pos_base, int32_t causal, void* o, float* lse, hipStream_t s,
+                const void* k_new = nullptr, const void* v_new = nullptr, int32_t n_new = 0) {
     if (!prefill_supported(c->cfg.head_dim, c->group)) return GQA_ERR_UNSUPPORTED;
     int kv_span = kv_len;
     if (causal) kv_span = std::min(kv_len, std::max(0, q_pos_base + q_len - kv_pos_base));
-    PrefillPlan plan = plan_prefill(q_len, kv_span, c->group, c->cfg.n_kv_heads, kTargetPrefillWgs, kMaxPrefillSegs);
+    const int target = c->prefill_wgs_opt > 0 ? c->prefill_wgs_opt : kTargetPrefillWgs;
+    PrefillPlan plan = plan_prefill(q_len, kv_span, c->group, c->cfg.n_kv_heads, target, kMaxPrefillSegs);
     if (prefill_workspace_floats(plan, q_len, c->cfg.n_q_heads, c->cfg.head_dim) > c->pre_ws_floats)
         plan = plan_prefill(q_len, kv_span, c->group, c->cfg.n_kv_heads, 1, 1);  // one segment
     PrefillArgs a{};
@@ -189,6 +193,10 @@ int run_prefill(gqa_ctx* c, int32_t b, const void* q, int32_t q_len, int32_t q_p
     a.q = (const uint16_t*)q;
     a.kc = c->k_cache + seq_off;
     a.vc = c->v_cache + seq_off;
+    a.k_new = (const uint16_t*)k_new;
+    a.v_new = (const uint16_t*)v_new;
+    a.new_begin = kv_len - n_new;
+    a.n_new = n_new;
     a.n_q_heads = c->cfg.n_q_heads;
     a.n_kv_heads = c->cfg.n_kv_heads;
     a.l_cap = c->l_cap;
@@ -324,6 +332,7 @@ int gqa_create(const gqa_config* cfg, gqa_ctx** out_ctx) {
     alloc((void**)&c->lens_dev, (size_t)k.batch * sizeof(int32_t));
     alloc((void**)&c->pos_dev, (size_t)k.batch * sizeof(int32_t));
     alloc((void**)&c->rows_dev, 2 * units * D * 2);
+    alloc((void**)&c->new_dev, 2 * (size_t)k.n_kv_heads * k.max_q_len * D * 2);
     if (rc == GQA_OK && hipHostMalloc((void**)&c->o_pinned, c->stage_words * 2, 0) != hipSuccess) rc = GQA_ERR_OOM;
     if (rc == GQA_OK && hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) rc = GQA_ERR_HIP;
     if (rc == GQA_OK) {
@@ -359,6 +368,7 @@ int gqa_destroy(gqa_ctx* c) {
     (void)hipFree(c->lens_dev);
     (void)hipFree(c->pos_dev);
     (void)hipFree(c->rows_dev);
+    (void)hipFree(c->new_dev);
     if (c->o_pinned) (void)hipHostFree(c->o_pinned);
     if (c->ev_begin) (void)hipEventDestroy(c->ev_begin);
     if (c->ev_end) (void)hipEventDestroy(c->ev_end);
@@ -391,6 +401,10 @@ int gqa_set_option(gqa_ctx* c, int32_t option, int64_t value) {
             return GQA_OK;
         case GQA_OPT_PROFILE:
             return profile_enable(c, value ? 1 : 0);
+        case GQA_OPT_PREFILL_WGS:
+            if (value < 0 || value > (1 << 20)) return GQA_ERR_RANGE;
+            c->prefill_wgs_opt = (int)value;
+            return GQA_OK;
         default:
             return GQA_ERR_BAD_CFG;
     }
@@ -576,6 +590,43 @@ int gqa_prefill(gqa_ctx* c, int32_t b, const uint16_t* q, int32_t q_len, int32_t
         HIP_TRY(hipMemcpyAsync(lse, c->lse_dev, (size_t)c->cfg.n_q_heads * q_len * sizeof(float),
                                hipMemcpyDeviceToHost, c->stream));
     return finish_sync(c);
+}
+
+int gqa_prefill_append(gqa_ctx* c, int32_t b, const uint16_t* q, const uint16_t* k_rows, const uint16_t* v_rows,
+                       int32_t n_new, int32_t q_len, int32_t q_pos_base, int32_t kv_len, int32_t kv_pos_base,
+                       int32_t causal, uint16_t* o, float* lse) {
+    if (!c || !q || !k_rows || !v_rows || !o) return GQA_ERR_NULL;
+    int rc = check_prefill_args(c, b, q_len, q_pos_base, kv_len, kv_pos_base);
+    if (rc != GQA_OK) return rc;
+    if (n_new < 1 || n_new > kv_len || n_new > c->cfg.max_q_len) return GQA_ERR_RANGE;
+    rc = txn_idle(c);
+    if (rc != GQA_OK) return rc;
+    HIP_TRY(hipSetDevice(c->cfg.device));
+    const size_t qwords = (size_t)c->cfg.n_q_heads * q_len * c->cfg.head_dim;
+    const size_t rwords = (size_t)c->cfg.n_kv_heads * n_new * c->cfg.head_dim;
+    HIP_TRY(hipEventRecord(c->ev_begin, c->stream));
+    HIP_TRY(hipMemcpyAsync(c->q_dev, q, qwords * 2, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(hipMemcpyAsync(c->new_dev, k_rows, rwords * 2, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(hipMemcpyAsync(c->new_dev + rwords, v_rows, rwords * 2, hipMemcpyHostToDevice, c->stream));
+    rc = run_prefill(c, b, c->q_dev, q_len, q_pos_base, kv_len, kv_pos_base, causal, c->o_dev,
+                     lse ? c->lse_dev : nullptr, c->stream, c->new_dev, c->new_dev + rwords, n_new);
+    if (rc != GQA_OK) return rc;
+    HIP_TRY(hipMemcpyAsync(o, c->o_dev, qwords * 2, hipMemcpyDeviceToHost, c->stream));
+    if (lse)
+        HIP_TRY(hipMemcpyAsync(lse, c->lse_dev, (size_t)c->cfg.n_q_heads * q_len * sizeof(float),
+                               hipMemcpyDeviceToHost, c->stream));
+    return finish_sync(c);
+}
+
+int gqa_prefill_append_device(gqa_ctx* c, int32_t b, const void* q, const void* k_rows, const void* v_rows,
+                              int32_t n_new, int32_t q_len, int32_t q_pos_base, int32_t kv_len, int32_t kv_pos_base,
+                              int32_t causal, void* o, float* lse, void* stream) {
+    if (!c || !q || !k_rows || !v_rows || !o) return GQA_ERR_NULL;
+    int rc = check_prefill_args(c, b, q_len, q_pos_base, kv_len, kv_pos_base);
+    if (rc != GQA_OK) return rc;
+    if (n_new < 1 || n_new > kv_len) return GQA_ERR_RANGE;
+    return run_prefill(c, b, q, q_len, q_pos_base, kv_len, kv_pos_base, causal, o, lse, pick_stream(c, stream),
+                       k_rows, v_rows, n_new);
 }
 
 int gqa_prefill_device(gqa_ctx* c, int32_t b, const void* q, int32_t q_len, int32_t q_pos_base, int32_t kv_len,

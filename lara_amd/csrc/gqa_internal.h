@@ -33,8 +33,12 @@ struct DecodeArgs {
 // Chunked prefill / full-transaction launch description (one sequence b).
 struct PrefillArgs {
     const uint16_t* q;      // [H_q][q_len][D] bf16, head-major
-    const uint16_t* kc;     // cache base of sequence b: [H_kv][L_cap][D]
-    const uint16_t* vc;
+    uint16_t* kc;           // cache base of sequence b: [H_kv][L_cap][D]
+    uint16_t* vc;
+    const uint16_t* k_new;  // [H_kv][n_new][D] rows placed at cache rows new_begin.. by this launch
+    const uint16_t* v_new;  //   (nullptr: none)
+    int32_t new_begin;
+    int32_t n_new;
     int32_t n_q_heads;
     int32_t n_kv_heads;
     int32_t l_cap;

@@ -22,6 +22,11 @@
 // MFMA result), so the softmax state of a row and its O accumulator live in the same lane
 // and no cross-lane shuffle is needed between the two products.
 //
+// Fused chunk append.  With k_new/v_new the launch also places the chunk's own K/V rows at
+// cache rows new_begin .. new_begin + n_new - 1: the work-groups with blockIdx.x == 0 copy
+// them (spread over kv heads and segments), and every work-group staging one of those rows
+// reads it from k_new/v_new instead of the cache, so no work-group waits for the copy.
+//
 // KV segments.  A chunk of a few hundred query rows gives only tens of work-groups per KV
 // head, too few for 256 CUs, so the key range is cut into segments (grid z): each
 // work-group attends one segment and writes an fp32 partial (O, m, l) per row, and
@@ -105,6 +110,19 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 
         }
         return max(hi, 0);
     };
+    // Fused append: the copy into the cache, before any early exit.
+    const bool has_new = a.k_new != nullptr && a.n_new > 0;
+    if (has_new && blockIdx.x == 0) {
+        const u32x4* ks = reinterpret_cast<const u32x4*>(a.k_new) + (size_t)h * a.n_new * (D / 8);
+        const u32x4* vs = reinterpret_cast<const u32x4*>(a.v_new) + (size_t)h * a.n_new * (D / 8);
+        u32x4* kd = reinterpret_cast<u32x4*>(a.kc + ((size_t)h * a.l_cap + a.new_begin) * D);
+        u32x4* vd = reinterpret_cast<u32x4*>(a.vc + ((size_t)h * a.l_cap + a.new_begin) * D);
+        const int words = a.n_new * (D / 8);
+        for (int i = blockIdx.z * (kWaves * 64) + threadIdx.x; i < words; i += gridDim.z * (kWaves * 64)) {
+            kd[i] = ks[i];
+            vd[i] = vs[i];
+        }
+    }
     const int last_task = min(n_tasks, (int)(blockIdx.x + 1) * kWaves) - 1;
     const int wg_hi = kv_limit(last_task / G);  // row blocks grow with the task index
     const int wave_hi = active ? kv_limit(rb) : 0;
@@ -137,25 +155,36 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 
     float m_run = -INFINITY;  // running max (log2 units) of this lane's row
     float l_lane = 0.f;       // this lane's half of the running sum
 
-    const u32x4* kg = reinterpret_cast<const u32x4*>(a.kc + (size_t)h * a.l_cap * D);
-    const u32x4* vg = reinterpret_cast<const u32x4*>(a.vc + (size_t)h * a.l_cap * D);
-
     // Staging roles: K chunk (key tid / NCH + 256/NCH * i, chunk tid % NCH);
     // V keys KPT*(tid / NCH) .. +KPT-1 of chunk tid % NCH.
     const int sc = tid % NCH;
     const int sk = tid / NCH;
+    const u32x4* kg = reinterpret_cast<const u32x4*>(a.kc + (size_t)h * a.l_cap * D);
+    const u32x4* vg = reinterpret_cast<const u32x4*>(a.vc + (size_t)h * a.l_cap * D);
+    const u32x4* kn = has_new ? reinterpret_cast<const u32x4*>(a.k_new) + (size_t)h * a.n_new * NCH : nullptr;
+    const u32x4* vn = has_new ? reinterpret_cast<const u32x4*>(a.v_new) + (size_t)h * a.n_new * NCH : nullptr;
+    // Row `row` of this thread's chunk: from the cache, or from this launch's new rows.
+    auto k_src = [&](int row) {
+        const unsigned r = (unsigned)(row - a.new_begin);
+        return (has_new && r < (unsigned)a.n_new) ? kn + (size_t)r * NCH + sc : kg + (size_t)row * NCH + sc;
+    };
+    auto v_src = [&](int row) {
+        const unsigned r = (unsigned)(row - a.new_begin);
+        return (has_new && r < (unsigned)a.n_new) ? vn + (size_t)r * NCH + sc : vg + (size_t)row * NCH + sc;
+    };
+
     u32x4 kr[KLD], vr[KPT];
     auto load_block = [&](int j0) {
 #pragma unroll
         for (int i = 0; i < KLD; ++i) {
             const int key = sk + i * (kWaves * 64 / NCH);
-            kr[i] = kg[(size_t)(j0 + key) * NCH + sc];
+            kr[i] = *k_src(j0 + key);
         }
 #pragma unroll
         for (int b = 0; b < KPT; ++b) {
             const int key = KPT * sk + b;
             // Rows past kv_len may hold stale words: P is 0 there, V must be finite.
-            vr[b] = (j0 + key < a.kv_len) ? vg[(size_t)(j0 + key) * NCH + sc] : u32x4{0u, 0u, 0u, 0u};
+            vr[b] = (j0 + key < a.kv_len) ? *v_src(j0 + key) : u32x4{0u, 0u, 0u, 0u};
         }
     };
     auto store_block = [&](int buf) {

@@ -178,3 +178,45 @@ def test_single_row_prefill_matches_decode():
     ref, ref_lse = oracle_for(q, k, v, causal=False)
     check_rows(pre, lse_p, ref, ref_lse)
     check_rows(dec[0][:, None], lse_d[0][:, None], ref, ref_lse)
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (16, 2, 64)])
+def test_fused_chunk_append_matches_load_then_prefill(hq, hkv, d):
+    """prefill_chunk with k_rows/v_rows = load_kv + prefill_chunk, bit for bit, chunk by chunk."""
+    rng = np.random.default_rng(300 + hq + d)
+    P, C = 700, 192  # the last chunk is partial
+    q = bf16_normal(rng, (hq, P, d))
+    k = bf16_normal(rng, (hkv, P, d))
+    v = bf16_normal(rng, (hkv, P, d))
+    kw = dict(n_q_heads=hq, n_kv_heads=hkv, head_dim=d, max_seq_len=P, max_q_len=C)
+    with AttentionAccelerator(**kw) as fused, AttentionAccelerator(**kw) as split:
+        for s in range(0, P, C):
+            e = min(P, s + C)
+            print(f"[fused chunk] {s}..{e}", flush=True)
+            out_f, lse_f = fused.prefill_chunk(q[:, s:e], q_pos_base=s, kv_len=e, k_rows=k[:, s:e], v_rows=v[:, s:e],
+                                               return_lse=True)
+            split.load_kv(k[:, s:e], v[:, s:e], start_pos=s)
+            out_s, lse_s = split.prefill_chunk(q[:, s:e], q_pos_base=s, kv_len=e, return_lse=True)
+            assert np.array_equal(out_f, out_s)
+            assert np.array_equal(lse_f.view(np.uint32), lse_s.view(np.uint32))
+            kr, vr = fused.read_kv(0, s, e - s)
+            assert np.array_equal(kr, k[:, s:e]) and np.array_equal(vr, v[:, s:e])
+            ref, ref_lse = oracle_for(q[:, s:e], k[:, :e], v[:, :e], causal=True, q_pos_base=s)
+            check_rows(out_f, lse_f, ref, ref_lse)
+
+
+@pytest.mark.parametrize("wgs", [1, 64, 0, 4096])
+def test_prefill_segmentation_invariance(wgs):
+    """Results for any KV segmentation agree with the oracle (1 = one segment)."""
+    rng = np.random.default_rng(400 + wgs)
+    q_len, kv_len = 256, 1536
+    q = bf16_normal(rng, (32, q_len, 128))
+    k = bf16_normal(rng, (8, kv_len, 128))
+    v = bf16_normal(rng, (8, kv_len, 128))
+    with AttentionAccelerator(max_seq_len=kv_len, max_q_len=q_len) as acc:
+        from lara_amd import _lib
+        _lib.check(acc._lib.gqa_set_option(acc._ctx, _lib.GQA_OPT_PREFILL_WGS, wgs), "prefill wgs")
+        acc.load_kv(k, v)
+        out, lse = acc.prefill_chunk(q, q_pos_base=kv_len - q_len, kv_len=kv_len, return_lse=True)
+    ref, ref_lse = oracle_for(q, k, v, causal=True, q_pos_base=kv_len - q_len)
+    check_rows(out, lse, ref, ref_lse)
