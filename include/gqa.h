@@ -62,6 +62,18 @@ extern "C" {
 #define GQA_OPT_DECODE_CHUNK 1 /* keys per split-KV work-group (multiple of 64; 0 = auto) */
 #define GQA_OPT_PROFILE      2 /* 1 = time every kernel launch with HIP events (restarts the record) */
 #define GQA_OPT_PREFILL_WGS  3 /* prefill work-groups the KV segmentation aims for (0 = auto, 1 = none) */
+#define GQA_OPT_NUMERICS     4 /* GQA_NUMERICS_*: arithmetic of prefill / transactions (decode: EXACT only) */
+
+/* Numerics of the attention kernels (GQA_OPT_NUMERICS).
+ * EXACT: fp32 accumulation, exact exp, exact divide -- within 2 bf16 ulp of exact attention.
+ * KV260: the deployed KV260 datapath bit for bit -- sequential fp32 sums of exact bf16 products,
+ *        the 1024-entry interpolated exp table (softmax_engine.sv:570-706), P truncated to bf16
+ *        for PV (attn_top.sv:653-658), reciprocal-table normalisation (output_buffer.sv:192-286),
+ *        16-key sub-blocks in the board's tile order (attn_core.sv:107-154); for comparing with
+ *        board results word for word.  Transactions with q_len == kv_len follow the board's
+ *        contract exactly; other shapes use the same walk over their own lengths. */
+#define GQA_NUMERICS_EXACT 0
+#define GQA_NUMERICS_KV260 1
 
 typedef struct gqa_config {
     int32_t batch;       /* B: sequences resident in the cache                         */

@@ -43,6 +43,9 @@ GQA_TIMER_COUNT = 4
 GQA_OPT_DECODE_CHUNK = 1
 GQA_OPT_PROFILE = 2
 GQA_OPT_PREFILL_WGS = 3
+GQA_OPT_NUMERICS = 4
+GQA_NUMERICS_EXACT = 0
+GQA_NUMERICS_KV260 = 1
 
 
 class GqaConfig(Structure):

@@ -300,6 +300,7 @@ class AttentionAccelerator:
         scale: float | None = None,
         device: int = 0,
         position_limit: int = ABSOLUTE_POSITION_LIMIT,
+        numerics: str = "exact",
     ) -> None:
         self._closed = True
         self._ctx = ctypes.c_void_p()
@@ -327,6 +328,7 @@ class AttentionAccelerator:
         _lib.check(lib.gqa_get_config(self._ctx, ctypes.byref(got)), "gqa_get_config")
         self.scale = float(got.scale)
         self._lib = lib
+        self.numerics = "exact"
         self._pl_clock_mhz = 0.0
         self._hw_ready = True
         self._closed = False
@@ -335,6 +337,12 @@ class AttentionAccelerator:
         self._pending: dict[str, int] | None = None
         self._txn_len = 0
         self.last_profile: RunProfile | None = None
+        if numerics != "exact":
+            try:
+                self.set_numerics(numerics)
+            except Exception:
+                self.close()
+                raise
 
     # ---- lifetime ---------------------------------------------------------------------
     @property
@@ -397,6 +405,16 @@ class AttentionAccelerator:
         if self.last_profile is None:
             raise RuntimeError("no completed attention run is available")
         Path(path).write_text(json.dumps(self.last_profile.to_dict(), indent=2) + "\n", encoding="utf-8")
+
+    def set_numerics(self, numerics: str) -> None:
+        """Arithmetic of prefill / transactions: "exact" (fp32, exact exp and divide) or "kv260"
+        (the deployed KV260 datapath bit for bit: LUT exp, bf16-truncated P, reciprocal-table
+        normalisation, the board's sub-block order).  Decode steps require "exact"."""
+        modes = {"exact": _lib.GQA_NUMERICS_EXACT, "kv260": _lib.GQA_NUMERICS_KV260}
+        if numerics not in modes:
+            raise ValueError(f"numerics must be one of {sorted(modes)}, got {numerics!r}")
+        self._call("gqa_set_option", _lib.GQA_OPT_NUMERICS, modes[numerics])
+        self.numerics = numerics
 
     # ---- size contract ------------------------------------------------------------------
     @staticmethod

@@ -54,6 +54,7 @@ struct gqa_ctx {
     size_t lse_words = 0;
     int chunk_opt = 0;
     int prefill_wgs_opt = 0;
+    int numerics = GQA_NUMERICS_EXACT;
     int profile = 0;
     hipEvent_t ev_begin = nullptr, ev_end = nullptr;
     // Profiling: a pool of event pairs per timer slot, filled launch by launch.
@@ -133,7 +134,7 @@ int profile_enable(gqa_ctx* c, int on) {
 
 int run_decode(gqa_ctx* c, const void* q, const int32_t* lens, const void* k_new, const void* v_new,
                const int32_t* positions, void* o, float* lse, hipStream_t s, int max_len) {
-    if (!decode_supported(c->cfg.head_dim, c->group)) return GQA_ERR_UNSUPPORTED;
+    if (!decode_supported(c->cfg.head_dim, c->group) || c->numerics != GQA_NUMERICS_EXACT) return GQA_ERR_UNSUPPORTED;
     const int chunk = choose_chunk(c, max_len);
     int max_splits = max_len > 0 ? (max_len + chunk - 1) / chunk : 1;
     if (max_splits > c->max_splits_cap) return GQA_ERR_RANGE;
@@ -181,6 +182,39 @@ int check_prefill_args(const gqa_ctx* c, int32_t b, int32_t q_len, int32_t q_pos
 int run_prefill(gqa_ctx* c, int32_t b, const void* q, int32_t q_len, int32_t q_pos_base, int32_t kv_len,
                 int32_t kv_pos_base, int32_t causal, void* o, float* lse, hipStream_t s,
                 const void* k_new = nullptr, const void* v_new = nullptr, int32_t n_new = 0) {
+    if (c->numerics == GQA_NUMERICS_KV260) {
+        const size_t seq = (size_t)b * c->cfg.n_kv_heads * c->l_cap * c->cfg.head_dim;
+        if (k_new != nullptr && n_new > 0) {
+            const size_t D = c->cfg.head_dim;
+            const size_t pitch_dst = (size_t)c->l_cap * D * 2, pitch_src = (size_t)n_new * D * 2;
+            const size_t dst = seq + (size_t)(kv_len - n_new) * D;
+            HIP_TRY(hipMemcpy2DAsync(c->k_cache + dst, pitch_dst, k_new, pitch_src, pitch_src, c->cfg.n_kv_heads,
+                                     hipMemcpyDeviceToDevice, s));
+            HIP_TRY(hipMemcpy2DAsync(c->v_cache + dst, pitch_dst, v_new, pitch_src, pitch_src, c->cfg.n_kv_heads,
+                                     hipMemcpyDeviceToDevice, s));
+        }
+        RtlArgs r{};
+        r.q = (const uint16_t*)q;
+        r.kc = c->k_cache + seq;
+        r.vc = c->v_cache + seq;
+        r.n_q_heads = c->cfg.n_q_heads;
+        r.n_kv_heads = c->cfg.n_kv_heads;
+        r.l_cap = c->l_cap;
+        r.q_len = q_len;
+        r.kv_len = kv_len;
+        r.q_pos_base = q_pos_base;
+        r.kv_pos_base = kv_pos_base;
+        r.causal = causal ? 1 : 0;
+        uint32_t sb;
+        memcpy(&sb, &c->scale, sizeof(sb));
+        r.scale_bits = sb;
+        r.out = (uint16_t*)o;
+        r.lse = lse;
+        timer_begin(c, GQA_TIMER_PREFILL, s);
+        HIP_TRY(launch_rtl_transaction(c->cfg.head_dim, r, s));
+        timer_end(c, GQA_TIMER_PREFILL, s);
+        return GQA_OK;
+    }
     if (!prefill_supported(c->cfg.head_dim, c->group)) return GQA_ERR_UNSUPPORTED;
     int kv_span = kv_len;
     if (causal) kv_span = std::min(kv_len, std::max(0, q_pos_base + q_len - kv_pos_base));
@@ -401,6 +435,12 @@ int gqa_set_option(gqa_ctx* c, int32_t option, int64_t value) {
             return GQA_OK;
         case GQA_OPT_PROFILE:
             return profile_enable(c, value ? 1 : 0);
+        case GQA_OPT_NUMERICS:
+            if (value != GQA_NUMERICS_EXACT && value != GQA_NUMERICS_KV260) return GQA_ERR_RANGE;
+            if (value == GQA_NUMERICS_KV260 && c->cfg.head_dim != 64 && c->cfg.head_dim != 128)
+                return GQA_ERR_UNSUPPORTED;
+            c->numerics = (int)value;
+            return GQA_OK;
         case GQA_OPT_PREFILL_WGS:
             if (value < 0 || value > (1 << 20)) return GQA_ERR_RANGE;
             c->prefill_wgs_opt = (int)value;

@@ -66,6 +66,25 @@ PrefillPlan plan_prefill(int q_len, int kv_span, int group, int n_kv_heads, int 
 // fp32 words of partial-output workspace a plan needs (O and (m, l) per row, per segment).
 size_t prefill_workspace_floats(const PrefillPlan& p, int q_len, int n_q_heads, int head_dim);
 
+// KV260 RTL-exact transaction (one sequence): the board's bit-level arithmetic.
+struct RtlArgs {
+    const uint16_t* q;      // [H_q][q_len][D] bf16, head-major
+    const uint16_t* kc;     // cache base of sequence b: [H_kv][L_cap][D]
+    const uint16_t* vc;
+    int32_t n_q_heads;
+    int32_t n_kv_heads;
+    int32_t l_cap;
+    int32_t q_len;
+    int32_t kv_len;
+    int32_t q_pos_base;
+    int32_t kv_pos_base;
+    int32_t causal;
+    uint32_t scale_bits;    // fp32 bits of the score scale (the board's INV_SQRT_D_FP32)
+    uint16_t* out;          // [H_q][q_len][D] bf16
+    float* lse;             // [H_q][q_len] or nullptr
+};
+hipError_t launch_rtl_transaction(int head_dim, const RtlArgs& a, hipStream_t s);
+
 bool decode_supported(int head_dim, int group);
 // Split-KV attention with an optional fused row append; sequences longer than one split
 // leave fp32 partials that launch_combine merges.

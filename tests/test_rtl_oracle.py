@@ -1,0 +1,169 @@
+"""Pins the C restatement of the KV260 bit-level arithmetic (oracle/rtl_exact.c) on the CPU.
+
+What fixes each part:
+* ROM tables: regenerated from their closed forms and compared word for word with the
+  committed images, whose SHA-256 equals the board ROM images' (and, where the reference
+  tree is present, the files themselves).
+* fp32_add / fp32_mul: IEEE float32 round-to-nearest-even (numpy) on normal operands with
+  normal results -- the RTL's 56-bit alignment with sticky bit rounds exactly like IEEE there.
+* bf16 products: exact (the float64 product), bf16 exponent 0 reads as zero.
+* exp lookup: within the linear-interpolation error of exp on [-8, 0]; 0 below -8, 1 above 0.
+* whole transactions: the float64 exact model within the LUT's and the truncated P's error;
+  one key returns V exactly; zero input returns +0.
+"""
+import hashlib
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from lara_amd.data import make_luts
+from oracle import gqa_oracle as orc
+from oracle import rtl_exact as rtl
+
+REF_DATA = Path("/root/reference/hw/data")
+
+
+def f2u(x):
+    return np.ascontiguousarray(np.asarray(x, dtype=np.float32)).view(np.uint32)
+
+
+def u2f(x):
+    return np.ascontiguousarray(np.asarray(x, dtype=np.uint32)).view(np.float32)
+
+
+def test_rom_tables_match_closed_forms_and_board_images():
+    assert np.array_equal(rtl.exp_lut(), make_luts.exp_table())
+    assert np.array_equal(rtl.recip_lut(), make_luts.recip_table())
+    for name, digest in make_luts.TABLE_SHA256.items():
+        text = (make_luts.HERE / name).read_bytes()
+        assert hashlib.sha256(text).hexdigest() == digest
+        if (REF_DATA / name).is_file():
+            assert (REF_DATA / name).read_bytes() == text
+    lut = u2f(rtl.exp_lut())
+    assert lut[0] == np.float32(np.exp(np.float32(-8.0))) and lut[1023] == 1.0
+
+
+def _normal_pairs(rng, n, spread=30):
+    a = (rng.standard_normal(n) * np.exp2(rng.integers(-spread, spread, n))).astype(np.float32)
+    b = (rng.standard_normal(n) * np.exp2(rng.integers(-spread, spread, n))).astype(np.float32)
+    return a, b
+
+
+def test_fp32_add_is_ieee_rne_on_normal_operands():
+    rng = np.random.default_rng(1)
+    a, b = _normal_pairs(rng, 400_000)
+    # near-cancellations: operands within a few ulp of each other's negation
+    c = rng.standard_normal(100_000).astype(np.float32)
+    d = (-c.view(np.int32) + 0).view(np.float32)
+    d = (d.view(np.uint32) + rng.integers(-3, 4, c.size).astype(np.uint32)).view(np.float32)
+    a = np.concatenate([a, c])
+    b = np.concatenate([b, d])
+    want = (a + b).astype(np.float32)
+    ok = np.isfinite(want) & (np.abs(want) >= np.finfo(np.float32).tiny)
+    got = rtl.fp32_add(f2u(a), f2u(b))
+    assert ok.mean() > 0.95
+    assert np.array_equal(got[ok], f2u(want)[ok])
+    exact_zero = (want == 0)
+    assert np.all(got[exact_zero] == 0)  # exact cancellation gives +0
+
+
+def test_fp32_mul_is_ieee_rne_on_normal_operands():
+    rng = np.random.default_rng(2)
+    a, b = _normal_pairs(rng, 400_000)
+    want = (a * b).astype(np.float32)
+    ok = np.isfinite(want) & (np.abs(want) >= np.finfo(np.float32).tiny)
+    got = rtl.fp32_mul(f2u(a), f2u(b))
+    assert np.array_equal(got[ok], f2u(want)[ok])
+
+
+def test_add_mul_special_values():
+    z, nz, one = 0x00000000, 0x80000000, 0x3F800000
+    nan, inf, ninf = 0x7FC00000, 0x7F800000, 0xFF800000
+    x = 0x40490FDB
+    add = lambda a, b: int(rtl.fp32_add(np.uint32([a]), np.uint32([b]))[0])
+    mul = lambda a, b: int(rtl.fp32_mul(np.uint32([a]), np.uint32([b]))[0])
+    assert add(z, x) == x and add(x, nz) == x          # a zero operand returns the other one
+    assert add(nz, z) == z and add(z, nz) == nz        # ... including its sign (IEEE would give +0)
+    assert add(nan, x) == nan and mul(x, 0x7FC12345) == nan
+    assert mul(x, nz) == nz and mul(nz, nz) == z
+    assert mul(ninf, x) == ninf and mul(one, x) == x
+    # -inf minus a finite value stays -inf (the correction exp of an all-masked history)
+    assert add(ninf, 0xC0000000) == ninf and add(ninf, 0x40000000) == ninf
+
+
+def test_bf16_products_are_exact():
+    rng = np.random.default_rng(3)
+    a = orc.fp32_to_bf16_u16(rng.standard_normal(200_000).astype(np.float32) * 4)
+    b = orc.fp32_to_bf16_u16(rng.standard_normal(200_000).astype(np.float32) * 4)
+    got = u2f(rtl.bf16_mul(a, b)).astype(np.float64)
+    want = orc.bf16_u16_to_fp32(a).astype(np.float64) * orc.bf16_u16_to_fp32(b).astype(np.float64)
+    live = (((a >> 7) & 0xFF) != 0) & (((b >> 7) & 0xFF) != 0)
+    assert np.array_equal(got[live], want[live])
+    sub = np.uint16([0x0001, 0x8040])  # bf16 subnormals count as zero
+    assert np.array_equal(rtl.bf16_mul(sub, np.uint16([0x3F80, 0x3F80])), np.uint32([0, 0x80000000]))
+
+
+def test_exp_lookup_interpolates_exp():
+    x = np.linspace(-8.0, 0.0, 200_001).astype(np.float32)
+    got = u2f(rtl.exp_lookup(f2u(x))).astype(np.float64)
+    want = np.exp(x.astype(np.float64))
+    h = 8.0 / 1023
+    bound = want * (h * h / 8 * 1.01) + 4 * np.spacing(want.astype(np.float32)).astype(np.float64)
+    assert np.all(np.abs(got - want) <= bound)
+    edge = f2u([0.0, -0.0, -8.0, -8.0001, -100.0, 1e-30, 5.0, -np.inf])
+    e = u2f(rtl.exp_lookup(edge))
+    assert e[0] == 1.0 and e[1] == 1.0 and e[2] == u2f(rtl.exp_lut())[0]
+    assert e[3] == 0 and e[4] == 0 and e[5] == 1.0 and e[6] == 1.0 and e[7] == 0
+
+
+def test_recip_lookup_close_to_reciprocal():
+    rng = np.random.default_rng(4)
+    l = (np.exp(rng.uniform(-10, 10, 100_000))).astype(np.float32)
+    r = u2f(rtl.recip_lookup(f2u(l))).astype(np.float64)
+    assert np.all(np.abs(r * l - 1.0) <= 2.0 ** -8)
+    p2 = np.float32([1.0, 2.0, 0.5, 1024.0])
+    assert np.array_equal(u2f(rtl.recip_lookup(f2u(p2))), np.float32([1.0, 0.5, 2.0, 1.0 / 1024]))
+
+
+@pytest.mark.parametrize("L,causal,qb,kb", [(1, True, 0, 0), (16, True, 0, 0), (33, False, 0, 0), (48, True, 3, 3),
+                                            (64, True, 31, 7), (70, False, 5, 9)])
+def test_transaction_close_to_exact_model(L, causal, qb, kb):
+    rng = np.random.default_rng(10 + L)
+    q = orc.fp32_to_bf16_u16(rng.standard_normal((32, L, 128)).astype(np.float32))
+    k = orc.fp32_to_bf16_u16(rng.standard_normal((8, L, 128)).astype(np.float32))
+    v = orc.fp32_to_bf16_u16(rng.standard_normal((8, L, 128)).astype(np.float32))
+    out, m, l = rtl.attention(q, k, v, causal=causal, q_pos_base=qb, kv_pos_base=kb)
+    exact, lse = orc.attention(orc.bf16_u16_to_fp32(q), orc.bf16_u16_to_fp32(k), orc.bf16_u16_to_fp32(v),
+                               causal=causal, q_pos_base=qb, kv_pos_base=kb)
+    # bf16-truncated P (relative error < 2^-7 per weight) and the LUT exp: measured <= 1.7 ulp
+    assert float(orc.row_ulp_error(out, exact).max()) <= 3.0
+    # m is the max scaled score, l the sum relative to it: lse = m + log(l)
+    got_lse = u2f(m).astype(np.float64) + np.log(u2f(l).astype(np.float64))
+    assert np.allclose(got_lse, lse, rtol=0, atol=1e-4)
+
+
+def test_one_key_returns_v_exactly_and_zero_input_returns_plus_zero():
+    rng = np.random.default_rng(5)
+    q = orc.fp32_to_bf16_u16(rng.standard_normal((32, 1, 128)).astype(np.float32))
+    k = orc.fp32_to_bf16_u16(rng.standard_normal((8, 1, 128)).astype(np.float32))
+    v = orc.fp32_to_bf16_u16(rng.standard_normal((8, 1, 128)).astype(np.float32))
+    out, _, _ = rtl.attention(q, k, v, causal=True)
+    assert np.array_equal(out, np.repeat(v, 4, axis=0))
+    z = np.zeros((32, 20, 128), np.uint16)
+    out, _, _ = rtl.attention(z, z[:8], z[:8], causal=True)
+    assert not out.any()
+
+
+def test_planted_mistake_is_detected():
+    """A dropped correction (l not rescaled) moves the result well past the tolerance."""
+    rng = np.random.default_rng(6)
+    L = 64
+    q = orc.fp32_to_bf16_u16(rng.standard_normal((32, L, 128)).astype(np.float32) * 3)
+    k = orc.fp32_to_bf16_u16(rng.standard_normal((8, L, 128)).astype(np.float32))
+    v = orc.fp32_to_bf16_u16(rng.standard_normal((8, L, 128)).astype(np.float32))
+    out, m, l = rtl.attention(q, k, v, causal=False)
+    exact, _ = orc.attention(orc.bf16_u16_to_fp32(q), orc.bf16_u16_to_fp32(k), orc.bf16_u16_to_fp32(v))
+    wrong = orc.bf16_rne(orc.bf16_u16_to_fp32(out) * np.float32(1.25))
+    assert float(orc.row_ulp_error(out, exact).max()) <= 3.0
+    assert float(orc.row_ulp_error(wrong, exact).max()) > 3.0
