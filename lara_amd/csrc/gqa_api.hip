@@ -16,7 +16,7 @@ using namespace lara;
 namespace {
 
 constexpr int kMinChunk = 256;     // smallest split (keys); multiple of every decode round size
-constexpr int kTargetPrefillWgs = 512;  // 2 per CU
+constexpr int kTargetPrefillWgs = kPrefillTargetWgs;
 constexpr int kMaxPrefillSegs = 16;
 constexpr int kTargetDecodeWgs = 512;  // 2 per CU: one split per (sequence, kv head) once that fills the GPU
 
@@ -41,6 +41,7 @@ struct gqa_ctx {
     float* part_o = nullptr;
     float* part_ml = nullptr;
     float* pre_ws = nullptr;     // prefill KV-segment partials (O, then (m, l))
+    uint16_t* zero_row = nullptr;  // one zero K/V row: the prefill source of rows past kv_len
     size_t pre_ws_floats = 0;
     uint16_t* q_dev = nullptr;   // staging: max(B*H_q*D, H_q*max_q_len*D) words
     uint16_t* o_dev = nullptr;   // same size as q_dev
@@ -244,6 +245,7 @@ int run_prefill(gqa_ctx* c, int32_t b, const void* q, int32_t q_len, int32_t q_p
     a.lse = lse;
     a.seg_len = plan.seg_len;
     a.n_segs = plan.n_segs;
+    a.zero_row = c->zero_row;
     a.part_o = c->pre_ws;
     a.part_ml = c->pre_ws + (size_t)plan.n_segs * c->cfg.n_q_heads * q_len * c->cfg.head_dim;
     timer_begin(c, GQA_TIMER_PREFILL, s);
@@ -364,6 +366,7 @@ int gqa_create(const gqa_config* cfg, gqa_ctx** out_ctx) {
     alloc((void**)&c->o_dev, c->stage_words * 2);
     alloc((void**)&c->lse_dev, c->lse_words * sizeof(float));
     alloc((void**)&c->lens_dev, (size_t)k.batch * sizeof(int32_t));
+    alloc((void**)&c->zero_row, D * 2);
     alloc((void**)&c->pos_dev, (size_t)k.batch * sizeof(int32_t));
     alloc((void**)&c->rows_dev, 2 * units * D * 2);
     alloc((void**)&c->new_dev, 2 * (size_t)k.n_kv_heads * k.max_q_len * D * 2);
@@ -375,7 +378,8 @@ int gqa_create(const gqa_config* cfg, gqa_ctx** out_ctx) {
         if (!ok) rc = GQA_ERR_HIP;
     }
     // Zero the caches once so rows beyond every sequence's length hold finite words.
-    if (rc == GQA_OK && (hipMemsetAsync(c->k_cache, 0, kv_words(c) * 2, c->stream) != hipSuccess ||
+    if (rc == GQA_OK && (hipMemsetAsync(c->zero_row, 0, D * 2, c->stream) != hipSuccess ||
+                         hipMemsetAsync(c->k_cache, 0, kv_words(c) * 2, c->stream) != hipSuccess ||
                          hipMemsetAsync(c->v_cache, 0, kv_words(c) * 2, c->stream) != hipSuccess ||
                          hipStreamSynchronize(c->stream) != hipSuccess))
         rc = GQA_ERR_HIP;
@@ -396,6 +400,7 @@ int gqa_destroy(gqa_ctx* c) {
     (void)hipFree(c->part_o);
     (void)hipFree(c->part_ml);
     (void)hipFree(c->pre_ws);
+    (void)hipFree(c->zero_row);
     (void)hipFree(c->q_dev);
     (void)hipFree(c->o_dev);
     (void)hipFree(c->lse_dev);

@@ -54,6 +54,7 @@ struct PrefillArgs {
     int32_t n_segs;         // KV segments (grid z); 1 = write the output directly
     float* part_o;          // [n_segs][H_q][q_len][D] fp32 un-normalised partial O
     float* part_ml;         // [n_segs][H_q][q_len][2] (running max in log2 units, sum)
+    const uint16_t* zero_row;  // >= D zero words: the source of K/V rows past kv_len
 };
 
 // KV segmentation of a prefill launch: (seg_len, n_segs) for q_len query rows whose
@@ -63,6 +64,8 @@ struct PrefillPlan {
     int32_t n_segs;
 };
 PrefillPlan plan_prefill(int q_len, int kv_span, int group, int n_kv_heads, int target_wgs, int max_segs);
+// Work-groups the KV segmentation of a prefill launch should aim for (one per CU).
+constexpr int kPrefillTargetWgs = 256;
 // fp32 words of partial-output workspace a plan needs (O and (m, l) per row, per segment).
 size_t prefill_workspace_floats(const PrefillPlan& p, int q_len, int n_q_heads, int head_dim);
 

@@ -10,27 +10,24 @@
 //                                               (attn_top.sv:462-625, output_buffer.sv:226-286)
 // Like the RTL (attn_top.sv:656), P enters the PV product as bf16 while l sums the fp32 p.
 //
-// Work decomposition.  A wave owns 32 query rows of one query head; the four waves of a
-// work-group own four (row block, head) tasks of one KV head, heads fastest, so for a GQA
-// group of 4 the whole group shares every K/V tile the work-group stages in LDS.  Keys are
-// processed in blocks of 64:
+// Work decomposition.  A wave owns 32 query rows of one query head; the eight waves of a
+// work-group own eight (row block, head) tasks of one KV head, heads fastest, so a GQA group
+// of 4 shares every K/V tile across its heads and two row blocks.  Keys are processed in
+// blocks of 64:
 //   S^T [64 keys x 32 rows] = K [64 x D] . Q^T [D x 32]   two v_mfma_f32_32x32x16_bf16 chains;
 //                                                          K from LDS (A), Q^T from VGPRs (B)
 //   O^T [D x 32 rows]      += V^T [D x 64] . P^T [64 x 32] D/32 chains of four MFMAs;
-//                                                          V^T from LDS (A), P^T from VGPRs (B)
+//                                                          V^T from LDS through transposing
+//                                                          reads (A), P^T from VGPRs (B)
 // Computing the transposed products keeps every lane on one query row (column l % 32 of the
 // MFMA result), so the softmax state of a row and its O accumulator live in the same lane
 // and no cross-lane shuffle is needed between the two products.
 //
-// Fused chunk append.  With k_new/v_new the launch also places the chunk's own K/V rows at
-// cache rows new_begin .. new_begin + n_new - 1: the work-groups with blockIdx.x == 0 copy
-// them (spread over kv heads and segments), and every work-group staging one of those rows
-// reads it from k_new/v_new instead of the cache, so no work-group waits for the copy.
-//
-// KV segments.  A chunk of a few hundred query rows gives only tens of work-groups per KV
-// head, too few for 256 CUs, so the key range is cut into segments (grid z): each
-// work-group attends one segment and writes an fp32 partial (O, m, l) per row, and
-// prefill_combine_kernel merges a row's segments with log-sum-exp weights.
+// Staging.  K and V tiles stream from HBM straight into a three-stage LDS ring with
+// direct-to-LDS loads (no register staging): while block j is computed, blocks j+1 and j+2
+// are in flight.  Each lane picks the global 16-byte chunk that the swizzled LDS layout wants
+// in its slot -- the cache row, the row this launch appends, or a zero row past kv_len (P is 0
+// there, and V must be finite).
 //
 // MFMA 32x32x16 operand layout used below: lane l supplies row (A) / column (B) l % 32 and
 // the eight k-values 8*(l/32)..8*(l/32)+7 of the step; result register i of lane l holds
@@ -50,7 +47,8 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kBN = 64;     // keys per block
 constexpr int kRows = 32;   // query rows per wave
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;   // waves per work-group: (row block, head) tasks, heads fastest
+constexpr int kStages = 3;  // LDS ring depth: two blocks in flight behind the one computed
 constexpr float kLn2 = 0.693147180559945309f;
 
 __device__ __forceinline__ f32x16 mfma32(const u32x4& a, const u32x4& b, const f32x16& c) {
@@ -63,35 +61,76 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, v);
 }
 
-// Key order inside the V^T tile: bits 2 and 3 of the key index are swapped, so the eight
-// keys one lane feeds to a PV step are contiguous (one 16-byte LDS read).
-__device__ __forceinline__ int vt_pos(int key) {
-    return (key & ~0xC) | ((key & 4) << 1) | ((key & 8) >> 1);
-}
-
 // 16-byte chunk swizzles (bank-conflict-free MFMA operand reads).
 template <int NCH>
 __device__ __forceinline__ int k_swz(int row) {
     return NCH == 16 ? (row & 15) : ((row >> 1) & 7);
 }
-__device__ __forceinline__ int vt_swz(int dim) { return (dim >> 1) & 7; }
+
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+
+// s_waitcnt vmcnt(N), leaving the LDS and export counters alone (gfx9 field layout).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Direct-to-LDS load of 16 bytes per lane (global_load_lds_dwordx4): lane L's bytes land at
+// LDS byte address lds_addr + 16*L.  Issued from inline assembly so that the compiler's
+// wait-count pass, which cannot tell which LDS bytes such a load writes, does not wait for
+// every load in flight before each LDS read; the kernel waits for them itself (wait_vmcnt)
+// before the barrier that publishes a stage.  lds_addr must be wave-uniform.
+// (M0 is declared clobbered; the compiler does not keep values in it in this file's kernels,
+// so its "reserved register" warning is silenced.)
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(gptr), "s"(lds_addr)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// Work-group barrier for the stage ring: LDS traffic is ordered by the explicit waits, so no
+// memory fence (which would wait for every load in flight) is attached.
+__device__ __forceinline__ void stage_barrier() { asm volatile("s_barrier" : : : "memory"); }
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)reinterpret_cast<uintptr_t>((lds_void_ptr)p);
+}
+
+// V tile: rows of keys, 16-byte chunks XOR-swizzled so that the four keys a transposing read
+// covers put their 64-byte runs (the 32 dims of one PV tile) in four different quarters of the
+// 64 banks: rows are 2*D bytes apart, so D = 128 rows all start in bank 0 and the swizzle uses
+// the key's two low bits; D = 64 rows alternate bank halves and the swizzle uses bit 1.
+template <int D>
+__device__ __forceinline__ int v_swz(int key) {
+    return D == 128 ? 4 * (key & 3) : 4 * ((key >> 1) & 1);
+}
+
+// V^T operand of one PV step (eight bf16: dims mt*32 + lane%32, keys kb + 4*half + 0..3 and
+// kb + 8 + 4*half + 0..3): ds_read_b64_tr_b16 hands lane i of each 16-lane group element (i % 4)
+// of the 8-byte piece that lane 4j + i/4 of the group addresses, for j = 0..3, so every lane
+// addresses key (lane%16)/4 of the four, dims d_g + 4*(lane%4) .. +3, and receives one dim of
+// four keys.
 
 template <int D, int G>
-__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_kernel(
-    PrefillArgs a) {
-    constexpr int NCH = D / 8;                 // 16-byte chunks per K/V row
-    constexpr int KSTEPS = D / 16;             // QK k-steps
-    constexpr int MT = D / 32;                 // PV result tiles (32 dims each)
-    constexpr int KLD = kBN * NCH / (kWaves * 64);  // K chunks staged per thread
-    constexpr int KPT = NCH / 4;               // V keys staged per thread (same chunk)
-    static_assert(KLD >= 1 && KPT >= 1 && KPT <= 4, "tile shape");
+__global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
+    constexpr int NCH = D / 8;                   // 16-byte chunks per K/V row
+    constexpr int KSTEPS = D / 16;               // QK k-steps
+    constexpr int MT = D / 32;                   // PV result tiles (32 dims each)
+    constexpr int TILE = kBN * NCH;              // 16-byte chunks per K (or V) tile
+    constexpr int DMA = TILE / (kWaves * 64);    // direct-to-LDS loads per thread per tile
+    constexpr int LPB = 2 * DMA;                 // per block (K and V)
+    static_assert(DMA >= 1 && DMA * kWaves * 64 == TILE, "tile shape");
 
-    __shared__ __attribute__((aligned(16))) u32x4 lds_k[2][kBN * NCH];
-    __shared__ __attribute__((aligned(16))) u32x4 lds_vt[2][D * (kBN / 8)];
+    __shared__ __attribute__((aligned(16))) u32x4 lds_k[kStages][TILE];
+    __shared__ __attribute__((aligned(16))) u32x4 lds_v[kStages][TILE];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = blockIdx.y;  // kv head
     const int n_rb = (a.q_len + kRows - 1) / kRows;
     const int n_tasks = n_rb * G;
@@ -101,7 +140,7 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 
     const int rb = task / G;
     const int hq = h * G + g;
 
-    // Keys this wave needs: [0, kv_hi) (causal rows stop at their diagonal).
+    // Keys a row block needs: [0, kv_limit) (causal rows stop at their diagonal).
     auto kv_limit = [&](int row_block) {
         int hi = a.kv_len;
         if (a.causal) {
@@ -110,15 +149,16 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 
         }
         return max(hi, 0);
     };
+
     // Fused append: the copy into the cache, before any early exit.
     const bool has_new = a.k_new != nullptr && a.n_new > 0;
     if (has_new && blockIdx.x == 0) {
-        const u32x4* ks = reinterpret_cast<const u32x4*>(a.k_new) + (size_t)h * a.n_new * (D / 8);
-        const u32x4* vs = reinterpret_cast<const u32x4*>(a.v_new) + (size_t)h * a.n_new * (D / 8);
+        const u32x4* ks = reinterpret_cast<const u32x4*>(a.k_new) + (size_t)h * a.n_new * NCH;
+        const u32x4* vs = reinterpret_cast<const u32x4*>(a.v_new) + (size_t)h * a.n_new * NCH;
         u32x4* kd = reinterpret_cast<u32x4*>(a.kc + ((size_t)h * a.l_cap + a.new_begin) * D);
         u32x4* vd = reinterpret_cast<u32x4*>(a.vc + ((size_t)h * a.l_cap + a.new_begin) * D);
-        const int words = a.n_new * (D / 8);
-        for (int i = blockIdx.z * (kWaves * 64) + threadIdx.x; i < words; i += gridDim.z * (kWaves * 64)) {
+        const int words = a.n_new * NCH;
+        for (int i = blockIdx.z * (kWaves * 64) + tid; i < words; i += gridDim.z * (kWaves * 64)) {
             kd[i] = ks[i];
             vd[i] = vs[i];
         }
@@ -146,6 +186,9 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks) qb[ks] = row_ok ? qp[2 * ks + half] : u32x4{0u, 0u, 0u, 0u};
     }
+    // Retire the Q loads now: with none of its own loads pending, the compiler inserts no
+    // wait-for-everything inside the loop, where the stage ring's loads are in flight.
+    wait_vmcnt<0>();
 
     f32x16 o[MT];
 #pragma unroll
@@ -155,109 +198,141 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 
     float m_run = -INFINITY;  // running max (log2 units) of this lane's row
     float l_lane = 0.f;       // this lane's half of the running sum
 
-    // Staging roles: K chunk (key tid / NCH + 256/NCH * i, chunk tid % NCH);
-    // V keys KPT*(tid / NCH) .. +KPT-1 of chunk tid % NCH.
-    const int sc = tid % NCH;
-    const int sk = tid / NCH;
     const u32x4* kg = reinterpret_cast<const u32x4*>(a.kc + (size_t)h * a.l_cap * D);
     const u32x4* vg = reinterpret_cast<const u32x4*>(a.vc + (size_t)h * a.l_cap * D);
     const u32x4* kn = has_new ? reinterpret_cast<const u32x4*>(a.k_new) + (size_t)h * a.n_new * NCH : nullptr;
     const u32x4* vn = has_new ? reinterpret_cast<const u32x4*>(a.v_new) + (size_t)h * a.n_new * NCH : nullptr;
-    // Row `row` of this thread's chunk: from the cache, or from this launch's new rows.
-    auto k_src = [&](int row) {
-        const unsigned r = (unsigned)(row - a.new_begin);
-        return (has_new && r < (unsigned)a.n_new) ? kn + (size_t)r * NCH + sc : kg + (size_t)row * NCH + sc;
-    };
-    auto v_src = [&](int row) {
-        const unsigned r = (unsigned)(row - a.new_begin);
-        return (has_new && r < (unsigned)a.n_new) ? vn + (size_t)r * NCH + sc : vg + (size_t)row * NCH + sc;
-    };
+    const u32x4* zero = reinterpret_cast<const u32x4*>(a.zero_row);
 
-    u32x4 kr[KLD], vr[KPT];
-    auto load_block = [&](int j0) {
+    // Direct-to-LDS staging of block j0 into ring stage st: wave-instruction i of wave w fills
+    // the 64 consecutive 16-byte slots (i*kWaves + w)*64 .., lane L slot +L; each lane loads the
+    // chunk the swizzled layout wants in its slot.  The slot -> (key, chunk) map is per lane and
+    // fixed; rows past kv_len (zero row) and rows this launch appends (k_new/v_new) occur in
+    // few blocks, so other blocks take the plain cache addresses.
+    int sl_key[DMA], sl_ck[DMA], sl_cv[DMA];
 #pragma unroll
-        for (int i = 0; i < KLD; ++i) {
-            const int key = sk + i * (kWaves * 64 / NCH);
-            kr[i] = *k_src(j0 + key);
-        }
+    for (int i = 0; i < DMA; ++i) {
+        const int slot = (i * kWaves + wave) * 64 + lane;
+        sl_key[i] = slot / NCH;
+        sl_ck[i] = (slot % NCH) ^ k_swz<NCH>(sl_key[i]);
+        sl_cv[i] = (slot % NCH) ^ v_swz<D>(sl_key[i]);
+    }
+    auto issue = [&](int j0, int st) {
+        const bool special = (j0 + kBN > a.kv_len) ||
+                             (has_new && j0 + kBN > a.new_begin && j0 < a.new_begin + a.n_new);
 #pragma unroll
-        for (int b = 0; b < KPT; ++b) {
-            const int key = KPT * sk + b;
-            // Rows past kv_len may hold stale words: P is 0 there, V must be finite.
-            vr[b] = (j0 + key < a.kv_len) ? *v_src(j0 + key) : u32x4{0u, 0u, 0u, 0u};
-        }
-    };
-    auto store_block = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < KLD; ++i) {
-            const int key = sk + i * (kWaves * 64 / NCH);
-            lds_k[buf][key * NCH + (sc ^ k_swz<NCH>(key))] = kr[i];
-        }
-        // Transpose: dims 8*sc .. 8*sc+7, keys KPT*sk .. +KPT-1 -> V^T rows.
-        const int pos = vt_pos(KPT * sk);
-        uint16_t* vt = reinterpret_cast<uint16_t*>(&lds_vt[buf][0]);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int dim = 8 * sc + e;
-            uint16_t w[KPT];
-#pragma unroll
-            for (int b = 0; b < KPT; ++b) w[b] = (uint16_t)(vr[b][e >> 1] >> (16 * (e & 1)));
-            const int elem = (dim * 8 + ((pos >> 3) ^ vt_swz(dim))) * 8 + (pos & 7);
-            if constexpr (KPT == 4) {
-                uint2 pk;
-                pk.x = (uint32_t)w[0] | ((uint32_t)w[1] << 16);
-                pk.y = (uint32_t)w[2] | ((uint32_t)w[3] << 16);
-                *reinterpret_cast<uint2*>(vt + elem) = pk;
-            } else {
-                *reinterpret_cast<uint32_t*>(vt + elem) = (uint32_t)w[0] | ((uint32_t)w[1] << 16);
+        for (int i = 0; i < DMA; ++i) {
+            const int row_idx = j0 + sl_key[i];
+            const u32x4* sk = kg + (size_t)row_idx * NCH + sl_ck[i];
+            const u32x4* sv = vg + (size_t)row_idx * NCH + sl_cv[i];
+            if (special) {
+                const unsigned r_new = (unsigned)(row_idx - a.new_begin);
+                if (row_idx >= a.kv_len) {
+                    sk = zero + sl_ck[i];
+                    sv = zero + sl_cv[i];
+                } else if (has_new && r_new < (unsigned)a.n_new) {
+                    sk = kn + (size_t)r_new * NCH + sl_ck[i];
+                    sv = vn + (size_t)r_new * NCH + sl_cv[i];
+                }
             }
+            const int base = (i * kWaves + wave) * 64;
+            dma16(sk, lds_addr(&lds_k[st][base]));
+            dma16(sv, lds_addr(&lds_v[st][base]));
         }
     };
 
-    if (n_blocks > 0) load_block(seg_begin);
+    // Per-lane operand offsets.  K (A of S^T): key kt*32 + col, chunk 2*ks + half, swizzled by
+    // the key's low bits, which kt does not change.  V^T (A of PV, transposing reads): the
+    // lane addresses key (lane%16)/4 + 4*half of the step's key base and dims
+    // mt*32 + 16*((lane/16)%2) + 4*(lane%4); the step's key base (a multiple of 4) only adds a
+    // constant, and the swizzle depends on the key's low two bits alone.
+    // LDS byte addresses in stage 0; a block adds its stage's (uniform) offset once, and the
+    // per-step parts are compile-time constants (instruction offsets).
+    uint32_t kaddr[KSTEPS];
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks)
+        kaddr[ks] = lds_addr(&lds_k[0][0]) + 16u * (uint32_t)(col * NCH + ((2 * ks + half) ^ k_swz<NCH>(col)));
+    uint32_t vaddr[MT];
+    {
+        const int key_off = (lane & 15) >> 2;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const int dim = mt * 32 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+            vaddr[mt] = lds_addr(&lds_v[0][0]) + (uint32_t)((key_off + 4 * half) * (D * 2) +
+                                                            (((dim >> 3) ^ v_swz<D>(key_off)) << 4) + (((dim >> 2) & 1) << 3));
+        }
+    }
+
+    // The running reference max only moves when a block's max exceeds it by more than
+    // kLazyLog2 (p <= 2^kLazyLog2 meanwhile), so most blocks skip the O rescale.
+    constexpr float kLazyLog2 = 8.0f;
+    const float c = a.scale_log2;
+
+    if (n_blocks > 0) issue(seg_begin, 0);
+    if (n_blocks > 1) issue(seg_begin + kBN, 1);
     for (int blk = 0; blk < n_blocks; ++blk) {
-        const int buf = blk & 1;
+        const int st = blk % kStages;
         const int j0 = seg_begin + blk * kBN;
-        store_block(buf);
-        __syncthreads();
-        if (blk + 1 < n_blocks) load_block(j0 + kBN);
+        // This thread's loads of block blk are done once at most the next block's remain.
+        if (blk + 1 < n_blocks) wait_vmcnt<LPB>(); else wait_vmcnt<0>();
+        stage_barrier();  // every wave's block blk landed; block blk-1's stage is free
+        if (blk + 2 < n_blocks) issue(j0 + 2 * kBN, (blk + 2) % kStages);
         if (j0 >= wave_hi) continue;  // this wave's rows see no key of the block
 
-        // ---- S^T = K . Q^T ----
-        f32x16 st[2];
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) st[kt][i] = 0.f;
-            const int key = kt * 32 + col;
-#pragma unroll
-            for (int ks = 0; ks < KSTEPS; ++ks) {
-                const u32x4 kw = lds_k[buf][key * NCH + ((2 * ks + half) ^ k_swz<NCH>(key))];
-                st[kt] = mfma32(kw, qb[ks], st[kt]);
-            }
-        }
+        const uint32_t stage_off = (uint32_t)st * (uint32_t)(TILE * 16);
 
-        // ---- online softmax (log2 domain) on this lane's row ----
-        const bool need_mask =
-            (j0 + kBN > a.kv_len) || (a.causal && a.kv_pos_base + j0 + kBN - 1 > a.q_pos_base + rb * kRows);
-        float mx = -INFINITY;
+        // ---- S^T = K . Q^T (raw scores) ----
+        f32x16 sacc[2];
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                float s = st[kt][i] * a.scale_log2;
-                if (need_mask) {
+            for (int i = 0; i < 16; ++i) sacc[kt][i] = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks) {
+            const uint32_t ka = kaddr[ks] + stage_off;
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt) {
+                const u32x4 kw = *(const __attribute__((address_space(3))) u32x4*)(uintptr_t)(ka + kt * 32 * NCH * 16);
+                sacc[kt] = mfma32(kw, qb[ks], sacc[kt]);
+            }
+        }
+
+        // ---- online softmax (log2 domain, scale folded into the exponent) ----
+        const bool need_mask =
+            (j0 + kBN > a.kv_len) || (a.causal && a.kv_pos_base + j0 + kBN - 1 > a.q_pos_base + rb * kRows);
+        float mx = -INFINITY;
+        if (need_mask) {
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
                     const int j = j0 + kt * 32 + 8 * (i >> 2) + 4 * half + (i & 3);
                     const bool ok = row_ok && j < a.kv_len && (!a.causal || a.kv_pos_base + j <= q_pos);
-                    s = ok ? s : -INFINITY;
+                    sacc[kt][i] = ok ? sacc[kt][i] : -INFINITY;
+                    mx = fmaxf(mx, sacc[kt][i]);
                 }
-                st[kt][i] = s;
-                mx = fmaxf(mx, s);
-            }
+        } else {
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[kt][i]);
+        }
         mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float m_new = fmaxf(m_run, mx);
-        const bool none = (m_new == -INFINITY);
-        const float corr = none ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
+        const float bm = mx * c;  // block max in log2 units (-inf if every key is masked)
+        const bool grow = bm > m_run + kLazyLog2;
+        if (__ballot(grow) != 0) {
+            const float m_new = grow ? bm : m_run;
+            const float corr = (m_run == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
+            m_run = m_new;
+            l_lane *= corr;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) o[mt][i] *= corr;
+        }
+        // p = 2^(s*c - m_run); with no valid key yet (m_run = -inf) every s of the block is -inf
+        // as well, and a finite offset keeps 2^(-inf) = 0 without a per-score select.
+        const float nm = (m_run == -INFINITY) ? 0.f : -m_run;
         float psum = 0.f;
         u32x4 pb[4];  // P^T operand of the four PV k-steps (kt, a2)
 #pragma unroll
@@ -267,25 +342,31 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 
                 float p[8];
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    const float s = st[kt][8 * a2 + j];
-                    p[j] = (s == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(s - m_new);
+                    const float sv = sacc[kt][8 * a2 + j];
+                    p[j] = __builtin_amdgcn_exp2f(fmaf(sv, c, nm));
                     psum += p[j];
                 }
                 pb[2 * kt + a2] = u32x4{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
                                         pack_bf16x2(p[6], p[7])};
             }
-        l_lane = l_lane * corr + psum;
-        m_run = m_new;
+        l_lane += psum;
 
-        // ---- O^T = O^T * corr + V^T . P^T ----
+        // ---- O^T += V^T . P^T ----
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) o[mt][i] *= corr;
-            const int dim = mt * 32 + col;
+            const uint32_t va = vaddr[mt] + stage_off;
 #pragma unroll
             for (int st_i = 0; st_i < 4; ++st_i) {
-                const u32x4 vw = lds_vt[buf][dim * 8 + ((st_i * 2 + half) ^ vt_swz(dim))];
+                const int kb = 32 * (st_i >> 1) + 16 * (st_i & 1);  // step's key base (half adds 4)
+                u32x4 vw;
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const v4i16_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (__attribute__((address_space(3))) v4i16_t*)(uintptr_t)(va + (uint32_t)((kb + 8 * e) * (D * 2))));
+                    const uint2 w = __builtin_bit_cast(uint2, r);
+                    vw[2 * e] = w.x;
+                    vw[2 * e + 1] = w.y;
+                }
                 o[mt] = mfma32(vw, pb[st_i], o[mt]);
             }
         }
@@ -322,33 +403,50 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 
         a.lse[(size_t)hq * a.q_len + row] = l_row > 0.f ? (m_run + log2f(l_row)) * kLn2 : -INFINITY;
 }
 
-// Merge of a row's KV segments: one work-group per (query row, query head), one thread per
-// dim.  Segment s holds keys [s*seg_len, (s+1)*seg_len); a row reads the segments below its
-// own key limit, which are exactly the ones prefill_kernel wrote for it.
+// Merge of a row's KV segments.  Segment s holds keys [s*seg_len, (s+1)*seg_len); a row
+// reads the segments below its own key limit, which are exactly the ones prefill_kernel
+// wrote for it.  A work-group merges kMergeRows rows of one query head; each row is handled
+// by D/4 threads owning four dims (16-byte loads), which all read the row's (m, l) pairs.
+constexpr int kMergeRows = 8;
+
 template <int D>
-__global__ __launch_bounds__(D) void prefill_combine_kernel(PrefillArgs a) {
-    const int row = blockIdx.x;
+__global__ __launch_bounds__(kMergeRows * D / 4) void prefill_combine_kernel(PrefillArgs a) {
+    constexpr int TPR = D / 4;  // threads per row
     const int hq = blockIdx.y;
-    const int d = threadIdx.x;
+    const int row = blockIdx.x * kMergeRows + threadIdx.x / TPR;
+    const int d4 = threadIdx.x % TPR;
+    if (row >= a.q_len) return;
     int hi = a.kv_len;
     if (a.causal) hi = min(hi, a.q_pos_base + row - a.kv_pos_base + 1);
     hi = max(hi, 0);
     const int n_valid = min(a.n_segs, (hi + a.seg_len - 1) / a.seg_len);
     const size_t seg_stride = (size_t)a.n_q_heads * a.q_len;
     const size_t prow = (size_t)hq * a.q_len + row;
+    const float2* ml = reinterpret_cast<const float2*>(a.part_ml);
     float M = -INFINITY;
-    for (int sp = 0; sp < n_valid; ++sp) M = fmaxf(M, a.part_ml[(sp * seg_stride + prow) * 2]);
-    float O = 0.f, Ls = 0.f;
+    for (int sp = 0; sp < n_valid; ++sp) M = fmaxf(M, ml[sp * seg_stride + prow].x);
+    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+    float Ls = 0.f;
     if (M != -INFINITY) {
+        const float4* po = reinterpret_cast<const float4*>(a.part_o) + prow * TPR + d4;
+#pragma unroll 4
         for (int sp = 0; sp < n_valid; ++sp) {
-            const size_t pr = sp * seg_stride + prow;
-            const float w = __builtin_amdgcn_exp2f(a.part_ml[pr * 2] - M);
-            O = fmaf(w, a.part_o[pr * D + d], O);
-            Ls = fmaf(w, a.part_ml[pr * 2 + 1], Ls);
+            const float2 e = ml[sp * seg_stride + prow];
+            const float w = __builtin_amdgcn_exp2f(e.x - M);
+            const float4 v = po[sp * seg_stride * TPR];
+            O.x = fmaf(w, v.x, O.x);
+            O.y = fmaf(w, v.y, O.y);
+            O.z = fmaf(w, v.z, O.z);
+            O.w = fmaf(w, v.w, O.w);
+            Ls = fmaf(w, e.y, Ls);
         }
     }
-    a.out[prow * D + d] = f32_to_bf16_rne(Ls > 0.f ? O / Ls : 0.f);
-    if (d == 0 && a.lse != nullptr) a.lse[prow] = Ls > 0.f ? (M + log2f(Ls)) * kLn2 : -INFINITY;
+    const float inv = Ls > 0.f ? 1.f / Ls : 0.f;
+    uint2 w;
+    w.x = (uint32_t)f32_to_bf16_rne(O.x * inv) | ((uint32_t)f32_to_bf16_rne(O.y * inv) << 16);
+    w.y = (uint32_t)f32_to_bf16_rne(O.z * inv) | ((uint32_t)f32_to_bf16_rne(O.w * inv) << 16);
+    *reinterpret_cast<uint2*>(a.out + prow * D + 4 * d4) = w;
+    if (d4 == 0 && a.lse != nullptr) a.lse[prow] = Ls > 0.f ? (M + log2f(Ls)) * kLn2 : -INFINITY;
 }
 
 template <int D, int G>
@@ -381,10 +479,11 @@ size_t prefill_workspace_floats(const PrefillPlan& p, int q_len, int n_q_heads, 
 }
 
 hipError_t launch_prefill_combine(int head_dim, const PrefillArgs& a, hipStream_t s) {
+    const dim3 grid((a.q_len + kMergeRows - 1) / kMergeRows, a.n_q_heads);
     if (head_dim == 128) {
-        hipLaunchKernelGGL(prefill_combine_kernel<128>, dim3(a.q_len, a.n_q_heads), dim3(128), 0, s, a);
+        hipLaunchKernelGGL(prefill_combine_kernel<128>, grid, dim3(kMergeRows * 32), 0, s, a);
     } else if (head_dim == 64) {
-        hipLaunchKernelGGL(prefill_combine_kernel<64>, dim3(a.q_len, a.n_q_heads), dim3(64), 0, s, a);
+        hipLaunchKernelGGL(prefill_combine_kernel<64>, grid, dim3(kMergeRows * 16), 0, s, a);
     } else {
         return hipErrorInvalidValue;
     }

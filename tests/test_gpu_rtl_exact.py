@@ -81,3 +81,23 @@ def test_kv260_mode_close_to_exact_and_decode_refuses():
     with AttentionAccelerator(max_seq_len=L, numerics="kv260") as acc:
         with pytest.raises(RuntimeError):
             acc.decode_step(q[:, 0][None], np.array([L], np.int32))
+
+
+def test_board_functional_matrix_on_board_format_cases(tmp_path):
+    """lara_amd.board_matrix over board-format case files: every word matches, and a planted
+    one-word error in expected_o is reported as a failure."""
+    from pathlib import Path
+
+    from lara_amd import board_matrix
+
+    cases = Path(__file__).resolve().parent / "golden" / "board_cases"
+    assert board_matrix.main(["--cases", str(cases), "--output-dir", str(tmp_path / "ok")]) == 0
+    bad = tmp_path / "bad_cases"
+    bad.mkdir()
+    src = sorted(cases.glob("case_*.npz"))[0]
+    with np.load(src, allow_pickle=False) as d:
+        files = {k: d[k] for k in d.files}
+    files["expected_o"] = files["expected_o"].copy()
+    files["expected_o"][3, 1, 7] ^= 1
+    np.savez(bad / src.name, **files)
+    assert board_matrix.main(["--cases", str(bad), "--output-dir", str(tmp_path / "bad")]) == 1

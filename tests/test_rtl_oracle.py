@@ -167,3 +167,16 @@ def test_planted_mistake_is_detected():
     wrong = orc.bf16_rne(orc.bf16_u16_to_fp32(out) * np.float32(1.25))
     assert float(orc.row_ulp_error(out, exact).max()) <= 3.0
     assert float(orc.row_ulp_error(wrong, exact).max()) > 3.0
+
+
+def test_board_format_cases_regenerate_from_the_oracle():
+    """tests/golden/board_cases hold the board's case format; expected_o is the oracle's output."""
+    cases = sorted((Path(__file__).resolve().parent / "golden" / "board_cases").glob("case_*.npz"))
+    assert len(cases) >= 3
+    for path in cases:
+        with np.load(path, allow_pickle=False) as d:
+            assert {"q_heads", "k_heads", "v_heads", "expected_o", "seq_len", "causal", "q_pos_base",
+                    "kv_pos_base"} <= set(d.files)
+            out, _, _ = rtl.attention(d["q_heads"], d["k_heads"], d["v_heads"], causal=bool(d["causal"]),
+                                      q_pos_base=int(d["q_pos_base"]), kv_pos_base=int(d["kv_pos_base"]))
+            assert np.array_equal(out, d["expected_o"])
