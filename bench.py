@@ -336,14 +336,59 @@ def copy_calibration(mib: int) -> int:
     return 0
 
 
+def _board_cases(args, orc):
+    """The matrix's transactions: board case files (--case-set LABEL=DIR) or seeded synthetic sets."""
+    lengths = [int(x) for x in args.lengths.split(",") if x]
+    cases = []
+    if args.case_set:
+        for spec in args.case_set:
+            label, _, directory = spec.partition("=")
+            if not directory:
+                raise SystemExit(f"--case-set wants LABEL=DIR, got {spec!r}")
+            paths = sorted(Path(directory).glob("case_*.npz"))
+            if not paths:
+                raise SystemExit(f"no case_*.npz files in {directory}")
+            for path in paths:
+                with np.load(path, allow_pickle=False) as d:
+                    q = np.asarray(d["q_heads"], dtype=np.uint16)
+                    L = int(np.asarray(d["seq_len"]).reshape(-1)[0]) if "seq_len" in d.files else q.shape[1]
+                    causal = bool(np.asarray(d["causal"]).reshape(-1)[0]) if "causal" in d.files else True
+                    qb = int(np.asarray(d["q_pos_base"]).reshape(-1)[0]) if "q_pos_base" in d.files else 0
+                    kb = int(np.asarray(d["kv_pos_base"]).reshape(-1)[0]) if "kv_pos_base" in d.files else 0
+                    if (args.lengths_given and L not in lengths) or (args.causal_only and not causal):
+                        continue
+                    cases.append(dict(case_id=f"{label}/{path.stem}", case_set=label, seq_len=L, causal=causal,
+                                      q_pos_base=qb, kv_pos_base=kb, q=q,
+                                      k=np.asarray(d["k_heads"], dtype=np.uint16),
+                                      v=np.asarray(d["v_heads"], dtype=np.uint16),
+                                      expected=np.asarray(d["expected_o"], dtype=np.uint16)
+                                      if "expected_o" in d.files else None, input=str(path)))
+        return cases
+    case_sets = {"q0kv0": (0, 0), "q3kv3": (3, 3), "q31kv7": (31, 7)}
+    for label, (qb, kb) in case_sets.items():
+        for L in lengths:
+            for causal in ((True,) if args.causal_only else (True, False)):
+                rng = np.random.default_rng(len(cases) + 7919 * L)
+                cases.append(dict(case_id=f"{label}_L{L}_q{qb}_kv{kb}_{'causal' if causal else 'noncausal'}",
+                                  case_set=label, seq_len=L, causal=causal, q_pos_base=qb, kv_pos_base=kb,
+                                  q=orc.fp32_to_bf16_u16(rng.standard_normal((32, L, 128), dtype=np.float32)),
+                                  k=orc.fp32_to_bf16_u16(rng.standard_normal((8, L, 128), dtype=np.float32)),
+                                  v=orc.fp32_to_bf16_u16(rng.standard_normal((8, L, 128), dtype=np.float32)),
+                                  expected=None, input=None))
+    return cases
+
+
 def board_matrix(args) -> int:
     """The board performance matrix on the GPU (sw/board_performance.py:281-473, 573-747 re-targeted).
 
-    For every (case set, L, causal) transaction of the KV260 contract -- Q [32, L, 128],
-    K/V [8, L, 128], bf16 N(0, 1) seeded -- it times ``run_attention`` (host-to-host and the
-    attention kernels alone) and the fp32 NumPy CPU model on the host, and checks the GPU
-    output against the float64 oracle (tolerance 2 bf16 ulp per row).  Writes
-    ``performance.json`` and ``performance.csv`` to --output-dir and prints a summary line.
+    For every transaction of the KV260 contract -- Q [32, L, 128], K/V [8, L, 128], bf16; from
+    board case files (--case-set LABEL=DIR, the sw/board_matrix.py:117-126 format) or seeded
+    N(0, 1) sets over (position bases, L, causal) -- it times ``run_attention`` (host-to-host
+    and the attention kernels alone) and the fp32 NumPy CPU model on the host.  Correctness:
+    with ``--numerics exact`` every row within 2 bf16 ulp of the float64 oracle; with
+    ``--numerics kv260`` the output equals the C restatement of the board arithmetic word for
+    word and, where a case file holds ``expected_o``, those words too (the board's
+    ``fpga_bit_exact_expected``).  Writes ``performance.json`` and ``performance.csv``.
     """
     import csv
 
@@ -353,88 +398,107 @@ def board_matrix(args) -> int:
     from lara_amd.attn_driver import AttentionAccelerator, RunProfile
     from oracle import gqa_oracle as orc
 
-    lengths = [int(x) for x in args.lengths.split(",") if x]
-    case_sets = {"q0kv0": (0, 0), "q3kv3": (3, 3), "q31kv7": (31, 7)}
+    rtl = None
+    if args.numerics == "kv260":
+        from oracle import rtl_exact as rtl
+    cases = _board_cases(args, orc)
+    if not cases:
+        raise SystemExit("board matrix: no cases selected")
     out_dir = Path(args.output_dir)
     out_dir.mkdir(parents=True, exist_ok=True)
-    rows = []
-    L_max = max(lengths)
-    with AttentionAccelerator(max_seq_len=L_max, max_q_len=L_max) as acc, threadpool_limits(limits=args.cpu_threads):
-        for label, (qb, kb) in case_sets.items():
-            for L in lengths:
-                for causal in (True, False):
-                    case_id = f"{label}_L{L}_q{qb}_kv{kb}_{'causal' if causal else 'noncausal'}"
-                    log(f"board case {case_id}")
-                    rng = np.random.default_rng(len(rows) + 7919 * L)
-                    q = orc.fp32_to_bf16_u16(rng.standard_normal((32, L, 128), dtype=np.float32))
-                    k = orc.fp32_to_bf16_u16(rng.standard_normal((8, L, 128), dtype=np.float32))
-                    v = orc.fp32_to_bf16_u16(rng.standard_normal((8, L, 128), dtype=np.float32))
-                    kw = dict(q_pos_base=qb, kv_pos_base=kb, causal=causal)
-                    for _ in range(args.board_warmup):
-                        acc.run_attention(q, k, v, **kw)
-                        orc.cpu_attention_numpy_fp32(q, k, v, **kw)
-                    profiles = []
-                    for _ in range(args.board_repeats):
-                        out = acc.run_attention(q, k, v, **kw)
-                        profiles.append(acc.last_profile.to_dict())
-                    cpu_ms = []
-                    for _ in range(args.board_repeats):
-                        t0 = time.perf_counter_ns()
-                        cpu_out = orc.cpu_attention_numpy_fp32(q, k, v, **kw)
-                        cpu_ms.append((time.perf_counter_ns() - t0) / 1e6)
-                    exact, _ = orc.attention(orc.bf16_u16_to_fp32(q), orc.bf16_u16_to_fp32(k),
-                                             orc.bf16_u16_to_fp32(v), **kw)
-                    gpu_f = orc.bf16_u16_to_fp32(out)
-                    ulp = float(orc.row_ulp_error(out, exact).max())
-                    pairs = bm.valid_pairs(L, L, causal=causal, q_pos_base=qb, kv_pos_base=kb)
-                    macs = 2 * 32 * pairs * 128
-                    ops = 2 * macs
-                    h2h = bm.stats(p["attention_total_ms"] for p in profiles)
-                    kern = bm.stats(p["pl_mac_ms"] for p in profiles)
-                    cpu = bm.stats(cpu_ms)
-                    rows.append({
-                        "case_id": case_id, "case_set": label, "seq_len": L, "causal": causal,
-                        "q_pos_base": qb, "kv_pos_base": kb,
-                        "warmup": args.board_warmup, "repeats": args.board_repeats,
-                        "correctness": {
-                            "gpu_max_row_error_bf16_ulp": ulp,
-                            "gpu_within_2_ulp": ulp <= 2.0,
-                            "gpu_bf16_vs_exact": bm.numeric_error(gpu_f, exact),
-                            "cpu_fp32_vs_exact": bm.numeric_error(cpu_out, exact),
-                            "cpu_fp32_vs_gpu_bf16": bm.numeric_error(cpu_out, gpu_f),
-                        },
-                        "work": {"valid_qk_pairs_per_q_head": pairs, "attention_macs_qk_plus_pv": macs,
-                                 "algorithmic_ops_two_per_mac": ops},
-                        "gpu": {"host_to_host_attention_ms": h2h, "attention_kernels_ms": kern,
-                                "host_to_host_effective_gops_median": ops / (h2h["median"] * 1e6),
-                                "kernel_effective_gops_median": ops / (kern["median"] * 1e6) if kern["median"] > 0
-                                else None,
-                                "profiles": profiles},
-                        "cpu_baseline": {"definition": "fp32 NumPy GQA attention on the GPU host; bf16 inputs; stable "
-                                                      "exact-exp softmax", "threads": args.cpu_threads,
-                                         "wall_ms": cpu,
-                                         "effective_gops_median": ops / (cpu["median"] * 1e6)},
-                        "speedup": {"cpu_over_gpu_host_to_host": cpu["median"] / h2h["median"],
-                                    "cpu_over_gpu_kernels": cpu["median"] / kern["median"] if kern["median"] > 0
-                                    else None},
-                    })
+    rows, errors = [], []
+    L_max = max(max(c["seq_len"] for c in cases), 16)
+    with AttentionAccelerator(max_seq_len=L_max, max_q_len=L_max, numerics=args.numerics) as acc, \
+            threadpool_limits(limits=args.cpu_threads):
+        for case in cases:
+            case_id, L, causal = case["case_id"], case["seq_len"], case["causal"]
+            qb, kb = case["q_pos_base"], case["kv_pos_base"]
+            q, k, v = case["q"], case["k"], case["v"]
+            log(f"board case {case_id}")
+            kw = dict(q_pos_base=qb, kv_pos_base=kb, causal=causal)
+            try:
+                for _ in range(args.board_warmup):
+                    acc.run_attention(q, k, v, seq_len=L, **kw)
+                    orc.cpu_attention_numpy_fp32(q[:, :L], k[:, :L], v[:, :L], **kw)
+                profiles = []
+                for _ in range(args.board_repeats):
+                    out = acc.run_attention(q, k, v, seq_len=L, **kw)
+                    profiles.append(acc.last_profile.to_dict())
+                cpu_ms = []
+                for _ in range(args.board_repeats):
+                    t0 = time.perf_counter_ns()
+                    cpu_out = orc.cpu_attention_numpy_fp32(q[:, :L], k[:, :L], v[:, :L], **kw)
+                    cpu_ms.append((time.perf_counter_ns() - t0) / 1e6)
+            except (ValueError, RuntimeError) as exc:  # keep the matrix going; the case is recorded as an error
+                errors.append({"case_id": case_id, "error": f"{type(exc).__name__}: {exc}"})
+                continue
+            exact, _ = orc.attention(orc.bf16_u16_to_fp32(q[:, :L]), orc.bf16_u16_to_fp32(k[:, :L]),
+                                     orc.bf16_u16_to_fp32(v[:, :L]), **kw)
+            gpu_f = orc.bf16_u16_to_fp32(out)
+            ulp = float(orc.row_ulp_error(out, exact).max())
+            correctness = {
+                "gpu_max_row_error_bf16_ulp": ulp,
+                "gpu_within_2_ulp": ulp <= 2.0,
+                "gpu_bf16_vs_exact": bm.numeric_error(gpu_f, exact),
+                "cpu_fp32_vs_exact": bm.numeric_error(cpu_out, exact),
+                "cpu_fp32_vs_gpu_bf16": bm.numeric_error(cpu_out, gpu_f),
+            }
+            if rtl is not None:
+                want, _, _ = rtl.attention(q[:, :L], k[:, :L], v[:, :L], **kw)
+                correctness["gpu_bit_exact_kv260_model"] = bool(np.array_equal(out, want))
+            if case["expected"] is not None:
+                mism = int(np.count_nonzero(out != case["expected"]))
+                correctness["gpu_bit_exact_expected"] = mism == 0
+                correctness["expected_mismatches"] = mism
+            correctness["passed"] = (correctness.get("gpu_bit_exact_kv260_model", correctness["gpu_within_2_ulp"])
+                                     and correctness.get("gpu_bit_exact_expected", True))
+            pairs = bm.valid_pairs(L, L, causal=causal, q_pos_base=qb, kv_pos_base=kb)
+            macs = 2 * 32 * pairs * 128
+            ops = 2 * macs
+            h2h = bm.stats(p["attention_total_ms"] for p in profiles)
+            kern = bm.stats(p["pl_mac_ms"] for p in profiles)
+            cpu = bm.stats(cpu_ms)
+            rows.append({
+                "case_id": case_id, "case_set": case["case_set"], "input": case["input"], "seq_len": L,
+                "causal": causal, "q_pos_base": qb, "kv_pos_base": kb, "numerics": args.numerics,
+                "warmup": args.board_warmup, "repeats": args.board_repeats,
+                "correctness": correctness,
+                "work": {"valid_qk_pairs_per_q_head": pairs, "attention_macs_qk_plus_pv": macs,
+                         "algorithmic_ops_two_per_mac": ops},
+                "gpu": {"host_to_host_attention_ms": h2h, "attention_kernels_ms": kern,
+                        "host_to_host_effective_gops_median": ops / (h2h["median"] * 1e6),
+                        "kernel_effective_gops_median": ops / (kern["median"] * 1e6) if kern["median"] > 0
+                        else None,
+                        "profiles": profiles},
+                "cpu_baseline": {"definition": "fp32 NumPy GQA attention on the GPU host; bf16 inputs; stable "
+                                              "exact-exp softmax", "threads": args.cpu_threads,
+                                 "wall_ms": cpu,
+                                 "effective_gops_median": ops / (cpu["median"] * 1e6)},
+                "speedup": {"cpu_over_gpu_host_to_host": cpu["median"] / h2h["median"],
+                            "cpu_over_gpu_kernels": cpu["median"] / kern["median"] if kern["median"] > 0
+                            else None},
+            })
     report = {"schema": "lara-mi355x-board-performance-v1", "environment": bm.collect_environment(),
-              "profile_fields": list(RunProfile.__dataclass_fields__), "cases": rows}
+              "numerics": args.numerics, "profile_fields": list(RunProfile.__dataclass_fields__),
+              "results": rows, "benchmark_errors": errors}
     (out_dir / "performance.json").write_text(json.dumps(report, indent=2) + "\n", encoding="utf-8")
     with (out_dir / "performance.csv").open("w", newline="", encoding="utf-8") as f:
         w = csv.writer(f)
-        w.writerow(["case_id", "seq_len", "causal", "max_row_ulp", "gpu_h2h_ms_median", "gpu_kernel_ms_median",
-                    "cpu_ms_median", "kernel_gops", "cpu_gops", "speedup_h2h", "speedup_kernel"])
+        w.writerow(["case_id", "seq_len", "causal", "passed", "max_row_ulp", "gpu_h2h_ms_median",
+                    "gpu_kernel_ms_median", "cpu_ms_median", "kernel_gops", "cpu_gops", "speedup_h2h",
+                    "speedup_kernel"])
         for r in rows:
-            w.writerow([r["case_id"], r["seq_len"], r["causal"], r["correctness"]["gpu_max_row_error_bf16_ulp"],
+            w.writerow([r["case_id"], r["seq_len"], r["causal"], r["correctness"]["passed"],
+                        r["correctness"]["gpu_max_row_error_bf16_ulp"],
                         r["gpu"]["host_to_host_attention_ms"]["median"], r["gpu"]["attention_kernels_ms"]["median"],
                         r["cpu_baseline"]["wall_ms"]["median"], r["gpu"]["kernel_effective_gops_median"],
                         r["cpu_baseline"]["effective_gops_median"], r["speedup"]["cpu_over_gpu_host_to_host"],
                         r["speedup"]["cpu_over_gpu_kernels"]])
-    passed = sum(r["correctness"]["gpu_within_2_ulp"] for r in rows)
-    print(json.dumps({"board_matrix": f"{passed}/{len(rows)} within 2 bf16 ulp", "output_dir": str(out_dir)}),
-          flush=True)
-    return 0 if passed == len(rows) else 1
+    passed = sum(r["correctness"]["passed"] for r in rows)
+    check = "bit-exact" if args.numerics == "kv260" else "within 2 bf16 ulp"
+    print(json.dumps({"board_matrix": f"{passed}/{len(cases)} {check}", "errors": len(errors),
+                      "output_dir": str(out_dir)}), flush=True)
+    return 0 if passed == len(cases) and not errors else 1
 
 
 def main() -> int:
@@ -454,12 +518,21 @@ def main() -> int:
                              "used to scale the FETCH_SIZE / WRITE_SIZE counters")
     parser.add_argument("--board-matrix", action="store_true",
                         help="run the board transaction matrix (lengths x causal x position bases) instead")
-    parser.add_argument("--lengths", default="1,16,32,64,128,512", help="board matrix sequence lengths")
+    parser.add_argument("--lengths", default=None,
+                        help="board matrix sequence lengths (default 1,16,32,64,128,512; with --case-set: all)")
+    parser.add_argument("--case-set", action="append", default=[], metavar="LABEL=DIR",
+                        help="board matrix: run the case_*.npz files of DIR (repeatable) instead of synthetic sets")
+    parser.add_argument("--causal-only", action="store_true", help="board matrix: causal transactions only")
+    parser.add_argument("--numerics", default="exact", choices=("exact", "kv260"),
+                        help="board matrix: engine arithmetic (kv260 = the board's, checked word for word)")
     parser.add_argument("--board-warmup", type=int, default=1)
     parser.add_argument("--board-repeats", type=int, default=5)
     parser.add_argument("--cpu-threads", type=int, default=int(os.environ.get("LARA_CPU_THREADS", "1")))
     parser.add_argument("--output-dir", default="gpurun_out/board_performance")
     args = parser.parse_args()
+    args.lengths_given = args.lengths is not None
+    if args.lengths is None:
+        args.lengths = "1,16,32,64,128,512"
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1).", file=sys.stderr)
