@@ -191,6 +191,34 @@ int gqa_load_kv_device(gqa_ctx* ctx, int32_t b, int32_t start_pos, int32_t n,
 /* Device addresses of the K and V caches ([B][H_kv][L_cap][D] bf16) and L_cap. */
 int gqa_cache_pointers(gqa_ctx* ctx, void** k_cache, void** v_cache, int32_t* l_cap);
 
+/* ---- layer input stage (run_layer) -------------------------------------------------
+ * Replace the host RMSNorm / QKV projection / RoPE / reshape_to_heads of
+ * AttentionAccelerator.run_layer (attn_driver.py:552-576; the absent host_attention module;
+ * hw/rtl/ext/rms_norm/rms_norm.sv:7-8, hw/rtl/ext/qkv_projection/qkv_projection.sv:7-8,
+ * hw/rtl/core/rope_engine.sv:4-10).  x is [n_tokens][hidden] bf16; wq is
+ * [H_q*D][hidden], wk and wv [H_kv*D][hidden] bf16 (out x in, Q = x Wq^T); rms_weight
+ * (gamma, [hidden] bf16) may be NULL for no normalisation, else
+ * y = x / sqrt(mean(x^2) + rms_eps) * gamma.  With rope != 0 the pair (2p, 2p+1) of each Q
+ * head of token t is rotated by (q_pos_base + t) * theta_p and of each K head by
+ * (kv_pos_base + t) * theta_p, theta_p = 10000^(-2p/D) in fp32 (hw/data/rope_theta.hex).
+ * Positions must stay below 2^24.
+ * gqa_submit_layer is gqa_submit for a layer: it uploads x and the weights, writes Q into
+ * the transaction's staging and K/V into rows [0, n_tokens) of sequence b, and leaves a
+ * transaction (q_len = kv_len = n_tokens) for gqa_start / gqa_wait / gqa_read_output.
+ * gqa_layer_qkv_device does the same from device memory without a transaction: Q goes to
+ * q_out ([H_q][n_tokens][D]), K/V to rows [kv_row0, kv_row0 + n_tokens) of sequence b; it
+ * allocates its workspace on first use.  gqa_layer_times returns the device time in us of
+ * the last call's RMSNorm, projection and RoPE stages (n <= 3; synchronises). */
+int gqa_submit_layer(gqa_ctx* ctx, int32_t b, const uint16_t* x, int32_t n_tokens, int32_t hidden,
+                     const uint16_t* wq, const uint16_t* wk, const uint16_t* wv,
+                     const uint16_t* rms_weight, float rms_eps, int32_t q_pos_base,
+                     int32_t kv_pos_base, int32_t causal, int32_t rope);
+int gqa_layer_qkv_device(gqa_ctx* ctx, int32_t b, const void* x, int32_t n_tokens, int32_t hidden,
+                         const void* wq, const void* wk, const void* wv, const void* rms_weight,
+                         float rms_eps, int32_t q_pos_base, int32_t kv_pos_base, int32_t kv_row0,
+                         int32_t rope, void* q_out, void* stream);
+int gqa_layer_times(gqa_ctx* ctx, float* out_us, int32_t n);
+
 /* ---- timing ---------------------------------------------------------------------
  * gqa_last_elapsed_us: elapsed time of the last synchronous call (HIP events on the ctx
  * stream).  With GQA_OPT_PROFILE on, every kernel launch is bracketed by HIP events on

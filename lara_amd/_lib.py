@@ -105,6 +105,11 @@ _SIGNATURES = {
     "gqa_prefill_append_device": [_CTX, c_int32, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32,
                                   c_int32, c_int32, c_void_p, c_void_p, c_void_p],
     "gqa_cache_pointers": [_CTX, POINTER(c_void_p), POINTER(c_void_p), _P32],
+    "gqa_submit_layer": [_CTX, c_int32, _P16, c_int32, c_int32, _P16, _P16, _P16, _P16, c_float, c_int32, c_int32,
+                         c_int32, c_int32],
+    "gqa_layer_qkv_device": [_CTX, c_int32, c_void_p, c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p,
+                             c_float, c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p],
+    "gqa_layer_times": [_CTX, _PF, c_int32],
     "gqa_last_elapsed_us": [_CTX, _PF],
     "gqa_kernel_times": [_CTX, _PF, c_int32],
     "gqa_kernel_launch_counts": [_CTX, _P32, c_int32],

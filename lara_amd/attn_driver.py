@@ -70,6 +70,7 @@ GQA_GROUP_SIZE = N_Q_HEADS // N_KV_HEADS
 MAX_SEQ_LEN = 512
 ABSOLUTE_POSITION_LIMIT = 1 << 16
 BF16_BYTES = 2
+RMS_NORM_EPS = 1e-5  # RMSNorm epsilon of the Llama-3 layer (run_layer); the reference does not state one
 PL_CLOCK_MHZ = 71.427856  # the board's signed-off PL clock; GPU timings use the device clock
 DMA_LENGTH_WIDTH = 26
 DMA_MAX_TRANSFER_BYTES = (1 << DMA_LENGTH_WIDTH) - 1
@@ -759,16 +760,124 @@ class AttentionAccelerator:
 
     def run_layer(self, hidden_states: np.ndarray, wq: np.ndarray, wk: np.ndarray, wv: np.ndarray,
                   rms_weight: np.ndarray | None = None, *, q_pos_base: int = 0, kv_pos_base: int = 0,
-                  causal: bool = True, timeout_ms: int | None = None) -> np.ndarray:
-        """Host RMSNorm + QKV projection + RoPE, then attention (sw/attn_driver.py:552-586).
+                  causal: bool = True, timeout_ms: int | None = None, rms_eps: float = RMS_NORM_EPS,
+                  rope: bool = True) -> np.ndarray:
+        """RMSNorm + QKV projection + RoPE, then attention (sw/attn_driver.py:552-586).
 
-        The reference delegates the host layer to a ``host_attention`` module that its
-        snapshot does not ship; this engine does not provide one either, so the call
-        raises ImportError exactly where the reference would.
+        ``hidden_states`` is [L, hidden]; ``wq`` [H_q*D, hidden] and ``wk``/``wv`` [H_kv*D,
+        hidden] (out x in: Q = x Wq^T, hw/rtl/ext/qkv_projection/qkv_projection.sv:7-8);
+        ``rms_weight`` (gamma, [hidden]) or None for no normalisation.  All are packed to bf16
+        words like the transaction inputs (uint16 passes through).  The reference runs these
+        steps on the host through its ``host_attention`` module; here they run on the GPU
+        (RMSNorm and RoPE kernels around a rocBLAS bf16 GEMM with fp32 accumulation) and write
+        Q and the cache directly.  ``rms_eps`` and ``rope`` extend the reference signature.
+        Returns fp32 [L, H_q*D] (``bf16_u16_to_fp32(o).transpose(1, 0, 2).reshape(L, -1)``).
+        The RunProfile fields host_rms_norm_ms / host_qkv_projection_ms / host_rope_ms hold
+        the device time of the three stages.
         """
         self._ensure_open()
-        raise ImportError("host_attention (rms_norm, qkv_project, reshape_to_heads, apply_rope_host) is not "
-                          "part of this engine; run the host layer yourself and call run_attention")
+        layer_start = time.perf_counter()
+        t = time.perf_counter()
+        x = np.ascontiguousarray(fp32_to_bf16_u16(hidden_states))
+        if x.ndim != 2:
+            raise ValueError(f"hidden_states must be [L, hidden]; got shape {x.shape}")
+        L, hidden = (int(n) for n in x.shape)
+        self._check_len(L)
+        self._check_positions(q_pos_base, kv_pos_base, L, L)
+        nq, nkv = self.n_q_heads * self.head_dim, self.n_kv_heads * self.head_dim
+        wq_u = np.ascontiguousarray(fp32_to_bf16_u16(wq))
+        wk_u = np.ascontiguousarray(fp32_to_bf16_u16(wk))
+        wv_u = np.ascontiguousarray(fp32_to_bf16_u16(wv))
+        if wq_u.shape != (nq, hidden) or wk_u.shape != (nkv, hidden) or wv_u.shape != (nkv, hidden):
+            raise ValueError(f"expected Wq ({nq}, {hidden}), Wk/Wv ({nkv}, {hidden}); got {wq_u.shape}, "
+                             f"{wk_u.shape}, {wv_u.shape}")
+        gamma = None
+        if rms_weight is not None:
+            gamma = np.ascontiguousarray(fp32_to_bf16_u16(rms_weight)).reshape(-1)
+            if gamma.size != hidden:
+                raise ValueError(f"rms_weight must have {hidden} elements; got {gamma.size}")
+        if not (np.isfinite(rms_eps) and rms_eps >= 0):
+            raise ValueError(f"rms_eps must be finite and >= 0; got {rms_eps}")
+        pack_ms = (time.perf_counter() - t) * 1000.0
+
+        prof = RunProfile(
+            timestamp_utc=datetime.now(timezone.utc).isoformat(),
+            git_commit=self._git_hash,
+            bitstream_sha256=self._bitstream_hash,
+            clock_mhz=self._pl_clock_mhz,
+            seq_len=L,
+            causal=causal,
+            q_pos_base=q_pos_base,
+            kv_pos_base=kv_pos_base,
+        )
+        self.last_profile = prof
+        prof.input_pack_ms = pack_ms
+        t = time.perf_counter()
+        self.configure(L, q_pos_base=q_pos_base, kv_pos_base=kv_pos_base, causal=causal)
+        self.clear_status()
+        o_bytes = self.n_q_heads * L * self.head_dim * BF16_BYTES
+        self._regs[CSR_RESULT_LEN] = o_bytes
+        prof.driver_setup_ms = (time.perf_counter() - t) * 1000.0
+
+        t = time.perf_counter()
+        self._call("gqa_submit_layer", 0, _lib.as_u16_ptr(x), L, hidden, _lib.as_u16_ptr(wq_u),
+                   _lib.as_u16_ptr(wk_u), _lib.as_u16_ptr(wv_u),
+                   None if gamma is None else _lib.as_u16_ptr(gamma), float(rms_eps), int(q_pos_base),
+                   int(kv_pos_base), int(bool(causal)), int(bool(rope)))
+        prof.q_dma_transfer_ms = (time.perf_counter() - t) * 1000.0
+        prof.q_dma_transfers = 1
+        prof.q_dma_bytes = int(x.nbytes + wq_u.nbytes + wk_u.nbytes + wv_u.nbytes
+                               + (0 if gamma is None else gamma.nbytes))
+        prof.output_dma_transfers = 1
+        prof.output_dma_bytes = o_bytes
+        stage_us = (ctypes.c_float * 3)()
+        self._call("gqa_layer_times", stage_us, 3)
+        prof.host_rms_norm_ms, prof.host_qkv_projection_ms, prof.host_rope_ms = (v / 1000.0 for v in stage_us)
+
+        attention_start = time.perf_counter()
+        self.start()
+        t = time.perf_counter()
+        self.wait_done(None, None, None, L, timeout_ms=timeout_ms)
+        prof.request_service_ms = (time.perf_counter() - t) * 1000.0
+        t = time.perf_counter()
+        words = self.readback_o(L)
+        prof.output_dma_transfer_ms = (time.perf_counter() - t) * 1000.0
+        perf = self.read_perf()
+        prof.clock_mhz = self._pl_clock_mhz
+        prof.pl_total_cycles = perf["cycles"]
+        prof.pl_mac_cycles = perf["mac_cycles"]
+        prof.pl_stall_cycles = perf["stall_cycles"]
+        prof.pl_core_active_cycles_excluding_stalls = max(perf["cycles"] - perf["stall_cycles"], 0)
+        per_ms = self._pl_clock_mhz * 1000.0 if self._pl_clock_mhz > 0 else 1.0
+        prof.pl_total_ms = perf["cycles"] / per_ms
+        prof.pl_mac_ms = perf["mac_cycles"] / per_ms
+        prof.pl_stall_ms = perf["stall_cycles"] / per_ms
+        prof.pl_core_active_ms_excluding_stalls = prof.pl_core_active_cycles_excluding_stalls / per_ms
+        result = bf16_u16_to_fp32(words).transpose(1, 0, 2).reshape(L, nq)
+        prof.attention_total_ms = (time.perf_counter() - attention_start) * 1000.0
+        prof.layer_total_ms = (time.perf_counter() - layer_start) * 1000.0
+        return result
+
+    def layer_qkv_device(self, x_ptr: int, n_tokens: int, hidden: int, wq_ptr: int, wk_ptr: int, wv_ptr: int,
+                         rms_weight_ptr: int | None, q_out_ptr: int, *, b: int = 0, q_pos_base: int = 0,
+                         kv_pos_base: int = 0, kv_row0: int = 0, rms_eps: float = RMS_NORM_EPS, rope: bool = True,
+                         stream: int | None = None) -> None:
+        """Device-pointer layer input stage (``gqa_layer_qkv_device``): Q to ``q_out_ptr``
+        ([H_q, n_tokens, D] bf16), K/V into rows kv_row0.. of sequence ``b``; enqueued, not
+        synchronised."""
+        self._ensure_open()
+        self._call("gqa_layer_qkv_device", int(b), ctypes.c_void_p(x_ptr), int(n_tokens), int(hidden),
+                   ctypes.c_void_p(wq_ptr), ctypes.c_void_p(wk_ptr), ctypes.c_void_p(wv_ptr),
+                   ctypes.c_void_p(rms_weight_ptr) if rms_weight_ptr else None, float(rms_eps), int(q_pos_base),
+                   int(kv_pos_base), int(kv_row0), int(bool(rope)), ctypes.c_void_p(q_out_ptr),
+                   ctypes.c_void_p(stream) if stream else None)
+
+    def layer_stage_us(self) -> tuple[float, float, float]:
+        """Device time (us) of the last layer call's RMSNorm, projection and RoPE stages."""
+        self._ensure_open()
+        out = (ctypes.c_float * 3)()
+        self._call("gqa_layer_times", out, 3)
+        return tuple(float(v) for v in out)
 
 
 def _self_test() -> None:

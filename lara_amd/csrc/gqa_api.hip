@@ -4,6 +4,7 @@
 #include "gqa_internal.h"
 
 #include <math.h>
+#include <rocblas/rocblas.h>
 
 #include <algorithm>
 #include <stdio.h>
@@ -65,6 +66,15 @@ struct gqa_ctx {
     float last_us = 0.f;
     double clock_mhz = 0.0;
     Txn txn;
+    // Layer input stage (run_layer): rocBLAS handle and grow-only device workspaces, created on
+    // first use; ev_layer brackets RMSNorm, projection and RoPE of the last layer call.
+    rocblas_handle blas = nullptr;
+    uint8_t* layer_in = nullptr;   // host-entry uploads: x, Wq, Wk, Wv, gamma
+    size_t layer_in_bytes = 0;
+    uint8_t* layer_tmp = nullptr;  // normalised x, then the [n_tokens][Q|K|V] projection
+    size_t layer_tmp_bytes = 0;
+    hipEvent_t ev_layer[4] = {};
+    float layer_us[3] = {};
 };
 
 namespace {
@@ -280,6 +290,120 @@ int txn_idle(gqa_ctx* c) {
     return GQA_OK;
 }
 
+// Grow-only device buffer (the old contents are not kept).
+int ensure_buffer(uint8_t** buf, size_t* cap, size_t bytes) {
+    if (bytes <= *cap) return GQA_OK;
+    if (*buf) {
+        HIP_TRY(hipDeviceSynchronize());
+        (void)hipFree(*buf);
+        *buf = nullptr;
+        *cap = 0;
+    }
+    if (hipMalloc(buf, bytes) != hipSuccess) {
+        *buf = nullptr;
+        return GQA_ERR_OOM;
+    }
+    *cap = bytes;
+    return GQA_OK;
+}
+
+constexpr double kRopeBase = 10000.0;  // theta_p = 10000^(-2p/D): hw/data/rope_theta.hex for D = 128
+
+int check_layer_args(const gqa_ctx* c, int32_t b, int32_t n_tokens, int32_t hidden, int32_t q_pos_base,
+                     int32_t kv_pos_base, int32_t row0) {
+    if (b < 0 || b >= c->cfg.batch) return GQA_ERR_STREAM_DEST;
+    if (n_tokens < 1 || n_tokens > c->cfg.max_q_len || hidden < 1) return GQA_ERR_RANGE;
+    if (row0 < 0 || (int64_t)row0 + n_tokens > c->cfg.max_seq_len) return GQA_ERR_RANGE;
+    if (q_pos_base < 0 || kv_pos_base < 0 || (int64_t)q_pos_base + n_tokens > (1 << 24) ||
+        (int64_t)kv_pos_base + n_tokens > (1 << 24))
+        return GQA_ERR_RANGE;  // positions are exact in the fp32 phase product below 2^24
+    if (c->cfg.head_dim > 2 * kMaxRopePairs || (c->cfg.head_dim & 1)) return GQA_ERR_UNSUPPORTED;
+    return GQA_OK;
+}
+
+// RMSNorm (if gamma) -> [Q|K|V] = x W^T (three rocBLAS bf16 GEMMs, fp32 accumulate) -> RoPE
+// (if rope) and scatter: Q to q_out [H_q][n_tokens][D], K/V to rows row0.. of sequence b.
+int run_layer_qkv(gqa_ctx* c, int32_t b, const void* x, int32_t n_tokens, int32_t hidden, const void* wq,
+                  const void* wk, const void* wv, const void* gamma, float eps, int32_t q_pos_base,
+                  int32_t kv_pos_base, int32_t row0, int32_t rope, void* q_out, hipStream_t s) {
+    const int D = c->cfg.head_dim, nq = c->cfg.n_q_heads * D, nkv = c->cfg.n_kv_heads * D;
+    const int ld = nq + 2 * nkv;
+    const size_t y_bytes = gamma ? ((size_t)n_tokens * hidden * 2 + 255) / 256 * 256 : 0;
+    int rc = ensure_buffer(&c->layer_tmp, &c->layer_tmp_bytes, y_bytes + (size_t)n_tokens * ld * 2);
+    if (rc != GQA_OK) return rc;
+    if (!c->blas) {
+        rocblas_status st = rocblas_create_handle(&c->blas);
+        if (st != rocblas_status_success) {
+            c->blas = nullptr;
+            snprintf(g_last_error, sizeof(g_last_error), "rocblas_create_handle: %s", rocblas_status_to_string(st));
+            return GQA_ERR_HIP;
+        }
+    }
+    if (!c->ev_layer[0])
+        for (int i = 0; i < 4; ++i) HIP_TRY(hipEventCreate(&c->ev_layer[i]));
+    HIP_TRY(hipEventRecord(c->ev_layer[0], s));
+    const uint16_t* src = (const uint16_t*)x;
+    if (gamma) {
+        NormArgs na{};
+        na.x = (const uint16_t*)x;
+        na.gamma = (const uint16_t*)gamma;
+        na.y = (uint16_t*)c->layer_tmp;
+        na.n_tokens = n_tokens;
+        na.hidden = hidden;
+        na.eps = eps;
+        HIP_TRY(launch_rms_norm(na, s));
+        src = na.y;
+    }
+    HIP_TRY(hipEventRecord(c->ev_layer[1], s));
+    uint16_t* qkv = (uint16_t*)(c->layer_tmp + y_bytes);
+    rocblas_status st = rocblas_set_stream(c->blas, s);
+    const float one = 1.f, zero = 0.f;
+    const void* ws[3] = {wq, wk, wv};
+    const int rows[3] = {nq, nkv, nkv}, off[3] = {0, nq, nq + nkv};
+    for (int i = 0; i < 3 && st == rocblas_status_success; ++i) {
+        // Column-major view: C[rows x n_tokens] (ld) = W[hidden x rows]^T . X[hidden x n_tokens].
+        st = rocblas_gemm_ex(c->blas, rocblas_operation_transpose, rocblas_operation_none, rows[i], n_tokens, hidden,
+                             &one, ws[i], rocblas_datatype_bf16_r, hidden, src, rocblas_datatype_bf16_r, hidden,
+                             &zero, qkv + off[i], rocblas_datatype_bf16_r, ld, qkv + off[i],
+                             rocblas_datatype_bf16_r, ld, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+    }
+    if (st != rocblas_status_success) {
+        snprintf(g_last_error, sizeof(g_last_error), "rocblas_gemm_ex: %s", rocblas_status_to_string(st));
+        return GQA_ERR_HIP;
+    }
+    HIP_TRY(hipEventRecord(c->ev_layer[2], s));
+    RopeArgs ra{};
+    ra.qkv = qkv;
+    ra.ld = ld;
+    ra.n_tokens = n_tokens;
+    ra.n_q_heads = c->cfg.n_q_heads;
+    ra.n_kv_heads = c->cfg.n_kv_heads;
+    ra.head_dim = D;
+    ra.q_pos_base = q_pos_base;
+    ra.kv_pos_base = kv_pos_base;
+    ra.rope = rope ? 1 : 0;
+    ra.q_out = (uint16_t*)q_out;
+    const size_t seq = (size_t)b * c->cfg.n_kv_heads * c->l_cap * D;
+    ra.kc = c->k_cache + seq;
+    ra.vc = c->v_cache + seq;
+    ra.l_cap = c->l_cap;
+    ra.row0 = row0;
+    for (int p = 0; p < D / 2; ++p) ra.theta[p] = (float)pow(kRopeBase, -2.0 * p / D);
+    HIP_TRY(launch_rope_scatter(ra, s));
+    HIP_TRY(hipEventRecord(c->ev_layer[3], s));
+    return GQA_OK;
+}
+
+int layer_times(gqa_ctx* c) {
+    HIP_TRY(hipEventSynchronize(c->ev_layer[3]));
+    for (int i = 0; i < 3; ++i) {
+        float ms = 0.f;
+        HIP_TRY(hipEventElapsedTime(&ms, c->ev_layer[i], c->ev_layer[i + 1]));
+        c->layer_us[i] = ms * 1000.f;
+    }
+    return GQA_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -419,6 +543,11 @@ int gqa_destroy(gqa_ctx* c) {
     }
     for (int i = 0; i < 4; ++i)
         if (c->ev_t[i]) (void)hipEventDestroy(c->ev_t[i]);
+    if (c->blas) (void)rocblas_destroy_handle(c->blas);
+    (void)hipFree(c->layer_in);
+    (void)hipFree(c->layer_tmp);
+    for (int i = 0; i < 4; ++i)
+        if (c->ev_layer[i]) (void)hipEventDestroy(c->ev_layer[i]);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
     return GQA_OK;
@@ -705,6 +834,78 @@ int gqa_submit(gqa_ctx* c, int32_t b, const uint16_t* q, int32_t q_len, int32_t 
     HIP_TRY(hipMemcpyAsync(c->q_dev, q, qwords * 2, hipMemcpyHostToDevice, c->stream));
     HIP_TRY(hipStreamSynchronize(c->stream));
     c->txn.valid = 1;
+    return GQA_OK;
+}
+
+int gqa_layer_qkv_device(gqa_ctx* c, int32_t b, const void* x, int32_t n_tokens, int32_t hidden, const void* wq,
+                         const void* wk, const void* wv, const void* rms_weight, float rms_eps, int32_t q_pos_base,
+                         int32_t kv_pos_base, int32_t kv_row0, int32_t rope, void* q_out, void* stream) {
+    if (!c || !x || !wq || !wk || !wv || !q_out) return GQA_ERR_NULL;
+    if (reinterpret_cast<uintptr_t>(q_out) & 3) return GQA_ERR_RANGE;  // Q is written as bf16 pairs
+    int rc = txn_idle(c);
+    if (rc != GQA_OK) return rc;
+    rc = check_layer_args(c, b, n_tokens, hidden, q_pos_base, kv_pos_base, kv_row0);
+    if (rc != GQA_OK) return rc;
+    if (!(rms_eps >= 0.f) || !isfinite(rms_eps)) return GQA_ERR_RANGE;
+    HIP_TRY(hipSetDevice(c->cfg.device));
+    return run_layer_qkv(c, b, x, n_tokens, hidden, wq, wk, wv, rms_weight, rms_eps, q_pos_base, kv_pos_base, kv_row0,
+                         rope, q_out, pick_stream(c, stream));
+}
+
+int gqa_submit_layer(gqa_ctx* c, int32_t b, const uint16_t* x, int32_t n_tokens, int32_t hidden, const uint16_t* wq,
+                     const uint16_t* wk, const uint16_t* wv, const uint16_t* rms_weight, float rms_eps,
+                     int32_t q_pos_base, int32_t kv_pos_base, int32_t causal, int32_t rope) {
+    if (!c || !x || !wq || !wk || !wv) return GQA_ERR_NULL;
+    int rc = txn_idle(c);
+    if (rc != GQA_OK) return rc;
+    rc = check_layer_args(c, b, n_tokens, hidden, q_pos_base, kv_pos_base, 0);
+    if (rc != GQA_OK) return rc;
+    rc = check_prefill_args(c, b, n_tokens, q_pos_base, n_tokens, kv_pos_base);
+    if (rc != GQA_OK) return rc;
+    if (!(rms_eps >= 0.f) || !isfinite(rms_eps)) return GQA_ERR_RANGE;
+    if (!prefill_supported(c->cfg.head_dim, c->group)) return GQA_ERR_UNSUPPORTED;
+    HIP_TRY(hipSetDevice(c->cfg.device));
+    const size_t D = c->cfg.head_dim, nq = (size_t)c->cfg.n_q_heads * D, nkv = (size_t)c->cfg.n_kv_heads * D;
+    auto pad = [](size_t bytes) { return (bytes + 255) / 256 * 256; };
+    const size_t xb = (size_t)n_tokens * hidden * 2, wqb = nq * hidden * 2, wkb = nkv * hidden * 2,
+                 gb = rms_weight ? (size_t)hidden * 2 : 0;
+    rc = ensure_buffer(&c->layer_in, &c->layer_in_bytes, pad(xb) + pad(wqb) + 2 * pad(wkb) + pad(gb));
+    if (rc != GQA_OK) return rc;
+    uint8_t* dx = c->layer_in;
+    uint8_t* dwq = dx + pad(xb);
+    uint8_t* dwk = dwq + pad(wqb);
+    uint8_t* dwv = dwk + pad(wkb);
+    uint8_t* dg = dwv + pad(wkb);
+    c->txn = Txn();
+    c->txn.b = b;
+    c->txn.q_len = n_tokens;
+    c->txn.q_pos_base = q_pos_base;
+    c->txn.kv_len = n_tokens;
+    c->txn.kv_pos_base = kv_pos_base;
+    c->txn.causal = causal ? 1 : 0;
+    HIP_TRY(hipEventRecord(c->ev_t[0], c->stream));
+    HIP_TRY(hipMemcpyAsync(dx, x, xb, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(hipMemcpyAsync(dwq, wq, wqb, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(hipMemcpyAsync(dwk, wk, wkb, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(hipMemcpyAsync(dwv, wv, wkb, hipMemcpyHostToDevice, c->stream));
+    if (rms_weight) HIP_TRY(hipMemcpyAsync(dg, rms_weight, gb, hipMemcpyHostToDevice, c->stream));
+    rc = run_layer_qkv(c, b, dx, n_tokens, hidden, dwq, dwk, dwv, rms_weight ? dg : nullptr, rms_eps, q_pos_base,
+                       kv_pos_base, 0, rope, c->q_dev, c->stream);
+    if (rc != GQA_OK) return rc;
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    rc = layer_times(c);
+    if (rc != GQA_OK) return rc;
+    c->txn.valid = 1;
+    return GQA_OK;
+}
+
+int gqa_layer_times(gqa_ctx* c, float* out_us, int32_t n) {
+    if (!c || !out_us) return GQA_ERR_NULL;
+    if (n < 0 || n > 3) return GQA_ERR_RANGE;
+    if (!c->ev_layer[0]) return GQA_ERR_NO_TRANSACTION;
+    int rc = layer_times(c);
+    if (rc != GQA_OK) return rc;
+    for (int i = 0; i < n; ++i) out_us[i] = c->layer_us[i];
     return GQA_OK;
 }
 

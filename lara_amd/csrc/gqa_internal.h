@@ -104,6 +104,32 @@ hipError_t launch_append(const uint16_t* k_rows, const uint16_t* v_rows, const i
                          uint16_t* kc, uint16_t* vc, int batch, int n_kv_heads, int head_dim,
                          int l_cap, int l_max, hipStream_t s);
 
+// Layer input stage of run_layer (sw/attn_driver.py:552-576): RMSNorm of the hidden states
+// and, after the QKV projection GEMM, RoPE plus the head-major scatter of Q and of K/V into
+// the cache.
+struct NormArgs {
+    const uint16_t* x;      // [n_tokens][hidden] bf16
+    const uint16_t* gamma;  // [hidden] bf16
+    uint16_t* y;            // [n_tokens][hidden] bf16
+    int n_tokens, hidden;
+    float eps;
+};
+hipError_t launch_rms_norm(const NormArgs& a, hipStream_t s);
+
+constexpr int kMaxRopePairs = 64;  // head_dim <= 128
+struct RopeArgs {
+    const uint16_t* qkv;   // [n_tokens][ld] bf16: Q heads, then K heads, then V heads, D columns each
+    int ld;
+    int n_tokens, n_q_heads, n_kv_heads, head_dim;
+    int q_pos_base, kv_pos_base, rope;
+    uint16_t* q_out;       // [n_q_heads][n_tokens][D]
+    uint16_t* kc;          // cache of one sequence: [n_kv_heads][l_cap][D], rows row0 ..
+    uint16_t* vc;
+    int l_cap, row0;
+    float theta[kMaxRopePairs];  // rotation frequency of pair (2p, 2p+1)
+};
+hipError_t launch_rope_scatter(const RopeArgs& a, hipStream_t s);
+
 // fp32 -> bf16 word, round to nearest even on the upper half: the output rounding of
 // fp32_to_bf16 in hw/rtl/pkg/attn_pkg.sv:618-626 (no NaN special case).
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float x) {

@@ -1,0 +1,189 @@
+"""GPU parity of the layer input stage (run_layer: RMSNorm, QKV projection, RoPE) and of run_layer.
+
+Bars (the stage specification is in oracle/layer_oracle.py):
+* projection: every output element within one bf16 ulp of the float64 product plus the fp32
+  accumulation term 2^-20 * sum |x w|;
+* RMSNorm, read through an identity projection: every element within one bf16 ulp of the
+  float64 value, and at least 99 % equal to its nearest-even rounding;
+* RoPE: word for word equal to the fp32 restatement applied to the GPU's own unrotated
+  projection (same bf16 inputs, same operations);
+* run_layer: within 2 bf16 ulp per row of the float64 attention of the GPU's Q/K/V, K/V
+  rows in the cache identical to the device-pointer stage's, and within 3 ulp of the float64
+  chain (rounding to bf16 at the same points); with KV260 numerics, word for word equal to
+  the C restatement of the board arithmetic on the GPU's Q/K/V.
+"""
+import numpy as np
+import pytest
+
+from lara_amd.attn_driver import AttentionAccelerator
+from oracle import gqa_oracle as orc
+from oracle import layer_oracle as lo
+from tests._gen import bf16_normal
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def dev(words: np.ndarray):
+    return torch.from_numpy(np.ascontiguousarray(words).view(np.int16)).cuda()
+
+
+def host(t) -> np.ndarray:
+    return t.cpu().numpy().view(np.uint16)
+
+
+def stage(acc, x, wq, wk, wv, gamma, *, b=0, q_pos_base=0, kv_pos_base=0, row0=0, rope=True, eps=1e-5):
+    """Run gqa_layer_qkv_device; returns Q [H_q, L, D] and the K/V rows written."""
+    L, hidden = x.shape
+    bufs = [dev(a) for a in (x, wq, wk, wv)]
+    g = dev(gamma) if gamma is not None else None
+    q = torch.empty((acc.n_q_heads, L, acc.head_dim), dtype=torch.int16, device="cuda")
+    torch.cuda.synchronize()  # the uploads ran on torch's stream; the stage runs on the engine's
+    acc.layer_qkv_device(bufs[0].data_ptr(), L, hidden, bufs[1].data_ptr(), bufs[2].data_ptr(), bufs[3].data_ptr(),
+                         g.data_ptr() if g is not None else None, q.data_ptr(), b=b, q_pos_base=q_pos_base,
+                         kv_pos_base=kv_pos_base, kv_row0=row0, rope=rope, rms_eps=eps)
+    torch.cuda.synchronize()
+    k, v = acc.read_kv(b, row0, L)
+    return host(q), k, v
+
+
+def weights(rng, nq, nkv, hidden):
+    s = 1.0 / np.sqrt(hidden)
+    return bf16_normal(rng, (nq, hidden), s), bf16_normal(rng, (nkv, hidden), s), bf16_normal(rng, (nkv, hidden), s)
+
+
+@pytest.mark.parametrize("hidden,L", [(768, 37), (1001, 5), (4096, 64)])
+def test_projection_within_fp32_accumulation_bound(hidden, L):
+    print(f"[layer] projection hidden={hidden} L={L}", flush=True)
+    rng = np.random.default_rng(hidden + L)
+    with AttentionAccelerator(n_q_heads=8, n_kv_heads=2, head_dim=128, max_seq_len=128) as acc:
+        x = bf16_normal(rng, (L, hidden))
+        wq, wk, wv = weights(rng, 1024, 256, hidden)
+        q, k, v = stage(acc, x, wq, wk, wv, None, rope=False, row0=3)
+    for got_heads, w, H in ((q, wq, 8), (k, wk, 2), (v, wv, 2)):
+        got = orc.bf16_u16_to_fp32(got_heads).astype(np.float64).transpose(1, 0, 2).reshape(L, H * 128)
+        exact = lo.project_exact(x, w)
+        bound = lo.projection_error_bound(x, w)
+        assert np.all(np.abs(got - exact) <= bound), float(np.max(np.abs(got - exact) / bound))
+        same = np.mean(orc.bf16_rne(exact.astype(np.float32)) == orc.fp32_to_bf16_u16(got.astype(np.float32)))
+        assert same > 0.95
+
+
+@pytest.mark.parametrize("extra_cols", [0, 3])
+def test_rms_norm_through_identity_projection(extra_cols):
+    """Wq = [I | 0] makes Q the first H_q*D columns of the normalised x exactly (fp32 sums of
+    one non-zero product); extra_cols = 3 exercises the unaligned (scalar) kernel path."""
+    nq = 1024
+    hidden = nq + extra_cols
+    L = 19
+    print(f"[layer] rms_norm hidden={hidden}", flush=True)
+    rng = np.random.default_rng(50 + extra_cols)
+    x = bf16_normal(rng, (L, hidden), 2.0)
+    x[3] = orc.fp32_to_bf16_u16(np.full(hidden, 0.001, np.float32))  # a small row: eps matters
+    gamma = orc.fp32_to_bf16_u16((1.0 + 0.2 * rng.standard_normal(hidden)).astype(np.float32))
+    wq = np.zeros((nq, hidden), np.uint16)
+    wq[np.arange(nq), np.arange(nq)] = 0x3F80  # 1.0
+    _, wk, wv = weights(rng, nq, 256, hidden)
+    with AttentionAccelerator(n_q_heads=8, n_kv_heads=2, head_dim=128, max_seq_len=64) as acc:
+        q, _, _ = stage(acc, x, wq, wk, wv, gamma, rope=False, eps=1e-5)
+    got = orc.bf16_u16_to_fp32(q).astype(np.float64).transpose(1, 0, 2).reshape(L, nq)
+    exact = lo.rms_norm_exact(x, gamma, 1e-5)[:, :nq]
+    assert np.all(np.abs(got - exact) <= orc.bf16_ulp(exact))
+    assert np.mean(orc.bf16_rne(exact.astype(np.float32)) == orc.fp32_to_bf16_u16(got.astype(np.float32))) > 0.99
+
+
+@pytest.mark.parametrize("qb,kb", [(0, 0), (5, 2), (60000, 59990)])
+def test_rope_is_word_exact(qb, kb):
+    print(f"[layer] rope q_pos_base={qb} kv_pos_base={kb}", flush=True)
+    rng = np.random.default_rng(qb + 7)
+    L, hidden = 40, 512
+    x = bf16_normal(rng, (L, hidden))
+    gamma = orc.fp32_to_bf16_u16((1.0 + 0.1 * rng.standard_normal(hidden)).astype(np.float32))
+    wq, wk, wv = weights(rng, 1024, 256, hidden)
+    with AttentionAccelerator(n_q_heads=8, n_kv_heads=2, head_dim=128, max_seq_len=64) as acc:
+        q0, k0, v0 = stage(acc, x, wq, wk, wv, gamma, rope=False, q_pos_base=qb, kv_pos_base=kb)
+        q1, k1, v1 = stage(acc, x, wq, wk, wv, gamma, rope=True, q_pos_base=qb, kv_pos_base=kb)
+    assert np.array_equal(q1, lo.apply_rope(q0, qb))
+    assert np.array_equal(k1, lo.apply_rope(k0, kb))
+    assert np.array_equal(v1, v0)
+    if qb == 0:
+        assert np.array_equal(q1[:, 0], q0[:, 0])  # position 0 is not rotated
+
+
+def test_rope_head_dim_64():
+    rng = np.random.default_rng(64)
+    L, hidden = 9, 256
+    x = bf16_normal(rng, (L, hidden))
+    wq, wk, wv = weights(rng, 8 * 64, 2 * 64, hidden)
+    with AttentionAccelerator(n_q_heads=8, n_kv_heads=2, head_dim=64, max_seq_len=32) as acc:
+        q0, k0, _ = stage(acc, x, wq, wk, wv, None, rope=False, q_pos_base=11, kv_pos_base=4)
+        q1, k1, _ = stage(acc, x, wq, wk, wv, None, rope=True, q_pos_base=11, kv_pos_base=4)
+    assert np.array_equal(q1, lo.apply_rope(q0, 11)) and np.array_equal(k1, lo.apply_rope(k0, 4))
+
+
+def _layer_inputs(rng, L, hidden=4096):
+    x = bf16_normal(rng, (L, hidden))
+    wq, wk, wv = weights(rng, 4096, 1024, hidden)
+    gamma = orc.fp32_to_bf16_u16((1.0 + 0.1 * rng.standard_normal(hidden)).astype(np.float32))
+    return x, wq, wk, wv, gamma
+
+
+@pytest.mark.parametrize("L,causal,qb,kb", [(64, True, 0, 0), (100, True, 7, 7), (33, False, 3, 0)])
+def test_run_layer_llama3_shape(L, causal, qb, kb):
+    print(f"[layer] run_layer L={L} causal={causal} qb={qb} kb={kb}", flush=True)
+    rng = np.random.default_rng(L * 3 + qb)
+    x, wq, wk, wv, gamma = _layer_inputs(rng, L)
+    with AttentionAccelerator(batch=2) as acc:
+        out = acc.run_layer(x, wq, wk, wv, gamma, q_pos_base=qb, kv_pos_base=kb, causal=causal)
+        prof = acc.last_profile.to_dict()
+        k_layer, v_layer = acc.read_kv(0, 0, L)
+        q, k, v = stage(acc, x, wq, wk, wv, gamma, b=1, q_pos_base=qb, kv_pos_base=kb)
+    assert out.dtype == np.float32 and out.shape == (L, 4096)
+    assert prof["host_qkv_projection_ms"] > 0 and prof["host_rope_ms"] > 0 and prof["layer_total_ms"] > 0
+    assert np.array_equal(k_layer, k) and np.array_equal(v_layer, v)
+    words = orc.fp32_to_bf16_u16(out.reshape(L, 32, 128).transpose(1, 0, 2))
+    ref, _ = orc.attention(orc.bf16_u16_to_fp32(q), orc.bf16_u16_to_fp32(k), orc.bf16_u16_to_fp32(v),
+                           causal=causal, q_pos_base=qb, kv_pos_base=kb)
+    assert float(orc.row_ulp_error(words, ref).max()) <= 2.0
+    # the float64 chain, rounded to bf16 at the stage boundaries of the specification
+    y = orc.bf16_rne(lo.rms_norm_exact(x, gamma, 1e-5).astype(np.float32))
+    proj = [orc.bf16_rne(lo.project_exact(y, w).astype(np.float32)) for w in (wq, wk, wv)]
+    qc = lo.apply_rope(lo.reshape_to_heads(proj[0], 32, 128), qb)
+    kc = lo.apply_rope(lo.reshape_to_heads(proj[1], 8, 128), kb)
+    vc = lo.reshape_to_heads(proj[2], 8, 128)
+    chain, _ = orc.attention(orc.bf16_u16_to_fp32(qc), orc.bf16_u16_to_fp32(kc), orc.bf16_u16_to_fp32(vc),
+                             causal=causal, q_pos_base=qb, kv_pos_base=kb)
+    assert float(orc.row_ulp_error(words, chain).max()) <= 3.0
+
+
+def test_run_layer_kv260_numerics_is_word_exact():
+    from oracle import rtl_exact as rtl
+
+    rng = np.random.default_rng(260)
+    L = 48
+    x, wq, wk, wv, gamma = _layer_inputs(rng, L)
+    with AttentionAccelerator(batch=2, numerics="kv260") as acc:
+        out = acc.run_layer(x, wq, wk, wv, gamma, q_pos_base=2, kv_pos_base=2, causal=True)
+        q, k, v = stage(acc, x, wq, wk, wv, gamma, b=1, q_pos_base=2, kv_pos_base=2)
+    want, _, _ = rtl.attention(q, k, v, causal=True, q_pos_base=2, kv_pos_base=2)
+    got = orc.fp32_to_bf16_u16(out.reshape(L, 32, 128).transpose(1, 0, 2))
+    assert np.array_equal(got, want)
+
+
+def test_run_layer_rejects_bad_shapes():
+    rng = np.random.default_rng(1)
+    x, wq, wk, wv, gamma = _layer_inputs(rng, 8, hidden=256)
+    with AttentionAccelerator() as acc:
+        with pytest.raises(ValueError):
+            acc.run_layer(x, wq[:, :100], wk, wv)
+        with pytest.raises(ValueError):
+            acc.run_layer(x, wq, wk, wv, gamma[:10])
+        with pytest.raises(ValueError):
+            acc.run_layer(x[None], wq, wk, wv)
+        with pytest.raises(ValueError):
+            acc.run_layer(bf16_normal(rng, (513, 256)), wq, wk, wv)  # beyond max_seq_len
+        with pytest.raises(ValueError):
+            acc.run_layer(x, wq, wk, wv, rms_eps=float("nan"))
+        out = acc.run_layer(x, wq, wk, wv, gamma, rope=False)
+        assert out.shape == (8, 4096) and np.isfinite(out).all()
