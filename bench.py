@@ -269,6 +269,113 @@ def measure_prefill(name: str, steps: int, warmup: int, target_wgs: int = 0) -> 
     return out
 
 
+class LayerBench:
+    """run_layer on the device: RMSNorm -> QKV GEMM -> RoPE/scatter (gqa_layer_qkv_device), then
+    causal attention of the whole prompt (gqa_prefill_device)."""
+
+    def __init__(self, w, device: int = 0):
+        import torch
+        from lara_amd import _lib
+
+        self.torch = torch
+        self.lib = _lib.lib()
+        self._lib = _lib
+        self.w = w
+        cfg = _lib.GqaConfig(1, w.n_q_heads, w.n_kv_heads, w.head_dim, w.tokens, w.tokens, 0.0, device)
+        self.ctx = ctypes.c_void_p()
+        _lib.check(self.lib.gqa_create(ctypes.byref(cfg), ctypes.byref(self.ctx)), "gqa_create")
+        dev = torch.device("cuda", device)
+        self.sptr = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        g = torch.Generator(device=dev)
+        g.manual_seed(w.seed)
+        nq, nkv = w.n_q_heads * w.head_dim, w.n_kv_heads * w.head_dim
+        s = w.hidden ** -0.5
+        self.x = torch.randn((w.tokens, w.hidden), generator=g, device=dev).to(torch.bfloat16)
+        # fused QKV weight [H_q + 2 H_kv][D][hidden]: the library runs one projection GEMM
+        self.wqkv = (torch.randn((nq + 2 * nkv, w.hidden), generator=g, device=dev) * s).to(torch.bfloat16)
+        self.wq, self.wk, self.wv = self.wqkv[:nq], self.wqkv[nq:nq + nkv], self.wqkv[nq + nkv:]
+        self.gamma = (1 + 0.1 * torch.randn((w.hidden,), generator=g, device=dev)).to(torch.bfloat16)
+        self.q = torch.empty((w.n_q_heads, w.tokens, w.head_dim), dtype=torch.bfloat16, device=dev)
+        self.o = torch.empty_like(self.q)
+        torch.cuda.synchronize(dev)
+
+    def step(self) -> None:
+        c = ctypes.c_void_p
+        w = self.w
+        rc = self.lib.gqa_layer_qkv_device(self.ctx, 0, c(self.x.data_ptr()), w.tokens, w.hidden, c(self.wq.data_ptr()),
+                                           c(self.wk.data_ptr()), c(self.wv.data_ptr()), c(self.gamma.data_ptr()),
+                                           ctypes.c_float(1e-5), 0, 0, 0, 1, c(self.q.data_ptr()), self.sptr)
+        self._lib.check(rc, "gqa_layer_qkv_device")
+        rc = self.lib.gqa_prefill_device(self.ctx, 0, c(self.q.data_ptr()), w.tokens, 0, w.tokens, 0, int(w.causal),
+                                         c(self.o.data_ptr()), None, self.sptr)
+        self._lib.check(rc, "gqa_prefill_device")
+
+    def run(self, steps: int, warmup: int) -> dict:
+        torch = self.torch
+        _lib = self._lib
+        for _ in range(warmup):
+            self.step()
+        torch.cuda.synchronize()
+        _lib.check(self.lib.gqa_set_option(self.ctx, _lib.GQA_OPT_PROFILE, 1), "profile on")
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            self.step()
+        torch.cuda.synchronize()
+        wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+        # stage times of one more (synchronised) call: the library's events on its stream
+        stage = np.zeros(3)
+        for _ in range(5):
+            self.step()
+            stage_us = (ctypes.c_float * 3)()
+            _lib.check(self.lib.gqa_layer_times(self.ctx, stage_us, 3), "layer times")
+            stage += np.array(stage_us[:]) / 5
+        times = (ctypes.c_float * _lib.GQA_TIMER_COUNT)()
+        _lib.check(self.lib.gqa_kernel_times(self.ctx, times, _lib.GQA_TIMER_COUNT), "kernel times")
+        counts = (ctypes.c_int32 * _lib.GQA_TIMER_COUNT)()
+        _lib.check(self.lib.gqa_kernel_launch_counts(self.ctx, counts, _lib.GQA_TIMER_COUNT), "counts")
+        _lib.check(self.lib.gqa_set_option(self.ctx, _lib.GQA_OPT_PROFILE, 0), "profile off")
+        merges = counts[_lib.GQA_TIMER_COMBINE] / max(1, counts[_lib.GQA_TIMER_PREFILL])
+        return {"wall_ms": wall_ms, "stage_us": stage, "prefill_us": times[_lib.GQA_TIMER_PREFILL],
+                "merge_us": times[_lib.GQA_TIMER_COMBINE] * merges}
+
+    def close(self) -> None:
+        self.lib.gqa_destroy(self.ctx)
+
+
+def measure_layer(name: str, steps: int, warmup: int) -> dict:
+    from lara_amd.benchmark import BF16_DENSE_TFLOPS, LAYER_WORKLOADS, layer_projection_flops, prefill_flops, \
+        valid_pairs
+
+    w = LAYER_WORKLOADS[name]
+    log(f"{name}: layer set-up")
+    bench = LayerBench(w)
+    try:
+        r = bench.run(steps, warmup)
+    finally:
+        bench.close()
+    norm_us, proj_us, rope_us = (float(v) for v in r["stage_us"])
+    proj_flops = layer_projection_flops(w)
+    attn_flops = prefill_flops(w.n_q_heads, w.head_dim, valid_pairs(w.tokens, w.tokens, causal=w.causal))
+    attn_us = r["prefill_us"] + r["merge_us"]
+    out = {
+        "us_per_layer": r["wall_ms"] * 1e3,
+        "tokens": w.tokens,
+        "rms_norm_us": norm_us,
+        "qkv_projection_us": proj_us,
+        "qkv_projection_tflops": proj_flops / (proj_us * 1e-6) / 1e12 if proj_us > 0 else None,
+        "rope_scatter_us": rope_us,
+        "attention_us": attn_us,
+        "attention_tflops": attn_flops / (attn_us * 1e-6) / 1e12 if attn_us > 0 else None,
+        "tokens_per_s": w.tokens / (r["wall_ms"] * 1e-3),
+    }
+    out["qkv_projection_frac_of_bf16_peak"] = (out["qkv_projection_tflops"] / BF16_DENSE_TFLOPS
+                                               if out["qkv_projection_tflops"] else None)
+    log(f"{name}: {out['us_per_layer']:.1f} us/layer: norm {norm_us:.1f} us, QKV GEMM {proj_us:.1f} us = "
+        f"{out['qkv_projection_tflops'] or 0:.0f} TFLOP/s, RoPE {rope_us:.1f} us, attention {attn_us:.1f} us = "
+        f"{out['attention_tflops'] or 0:.0f} TFLOP/s")
+    return out
+
+
 def read_traffic():
     """HBM bytes per decode launch from the committed rocprofv3 PMC summary, if present."""
     if not PROFILE_TRAFFIC.is_file():
@@ -510,7 +617,7 @@ def main() -> int:
     parser.add_argument("--chunk", type=int, default=0, help="keys per split-KV work-group (0 = auto)")
     parser.add_argument("--prefill-wgs", type=int, default=0,
                         help="work-groups the prefill KV segmentation aims for (0 = auto, 1 = no segments)")
-    parser.add_argument("--others", default="c2,c3,c4,c5", help="extra decode workloads to report ('' = none)")
+    parser.add_argument("--others", default="c2,c3,c4,c5,layer", help="extra decode workloads to report ('' = none)")
     parser.add_argument("--cpu-seconds", type=float, default=12.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--calibrate-copy-mib", type=int, default=0,
@@ -554,6 +661,9 @@ def main() -> int:
     for name in [x for x in args.others.split(",") if x and x != args.workload]:
         if name == "c5":
             others[name] = measure_prefill(name, max(10, args.steps // 2), max(2, args.warmup // 2), args.prefill_wgs)
+            continue
+        if name == "layer":
+            others[name] = measure_layer(name, max(10, args.steps // 4), max(2, args.warmup // 2))
             continue
         r = measure(name, max(10, args.steps // 2), max(2, args.warmup // 2))
         others[name] = {k: r[k] for k in ("us_per_step", "step_gbps", "step_frac_of_peak", "decode_us",

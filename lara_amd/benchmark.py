@@ -100,6 +100,31 @@ WORKLOADS = {
                          attended=8192, seed=5),
 }
 
+@dataclass(frozen=True)
+class LayerWorkload:
+    name: str
+    description: str
+    n_q_heads: int
+    n_kv_heads: int
+    head_dim: int
+    hidden: int
+    tokens: int
+    causal: bool = True
+    seed: int = 0
+
+
+LAYER_WORKLOADS = {
+    "layer": LayerWorkload("layer", "run_layer input stage + attention: Llama-3-8B shape (hidden 4096, 32q/8kv, D128), "
+                                    "2048-token prompt, RMSNorm -> QKV GEMM -> RoPE -> causal attention",
+                           32, 8, 128, hidden=4096, tokens=2048, seed=8),
+}
+
+
+def layer_projection_flops(w: LayerWorkload) -> int:
+    """2 * tokens * hidden * (H_q + 2 H_kv) * D: the three projections."""
+    return 2 * w.tokens * w.hidden * (w.n_q_heads + 2 * w.n_kv_heads) * w.head_dim
+
+
 PREFILL_WORKLOADS = {
     "c5": PrefillWorkload("c5", "chunked prefill: B1, 32q/8kv, D128, 2048 tokens in 256-token chunks, causal",
                           32, 8, 128, prompt=2048, chunk=256, seed=6),

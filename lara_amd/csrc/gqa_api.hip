@@ -359,8 +359,16 @@ int run_layer_qkv(gqa_ctx* c, int32_t b, const void* x, int32_t n_tokens, int32_
     rocblas_status st = rocblas_set_stream(c->blas, s);
     const float one = 1.f, zero = 0.f;
     const void* ws[3] = {wq, wk, wv};
-    const int rows[3] = {nq, nkv, nkv}, off[3] = {0, nq, nq + nkv};
-    for (int i = 0; i < 3 && st == rocblas_status_success; ++i) {
+    int rows[3] = {nq, nkv, nkv}, off[3] = {0, nq, nq + nkv};
+    int n_gemm = 3;
+    // Wq, Wk, Wv stored back to back ([H_q + 2 H_kv][D][hidden]) are one fused projection.
+    const size_t row_bytes = (size_t)hidden * 2;
+    if ((const uint8_t*)wk == (const uint8_t*)wq + (size_t)nq * row_bytes &&
+        (const uint8_t*)wv == (const uint8_t*)wk + (size_t)nkv * row_bytes) {
+        rows[0] = ld;
+        n_gemm = 1;
+    }
+    for (int i = 0; i < n_gemm && st == rocblas_status_success; ++i) {
         // Column-major view: C[rows x n_tokens] (ld) = W[hidden x rows]^T . X[hidden x n_tokens].
         st = rocblas_gemm_ex(c->blas, rocblas_operation_transpose, rocblas_operation_none, rows[i], n_tokens, hidden,
                              &one, ws[i], rocblas_datatype_bf16_r, hidden, src, rocblas_datatype_bf16_r, hidden,
@@ -869,13 +877,13 @@ int gqa_submit_layer(gqa_ctx* c, int32_t b, const uint16_t* x, int32_t n_tokens,
     auto pad = [](size_t bytes) { return (bytes + 255) / 256 * 256; };
     const size_t xb = (size_t)n_tokens * hidden * 2, wqb = nq * hidden * 2, wkb = nkv * hidden * 2,
                  gb = rms_weight ? (size_t)hidden * 2 : 0;
-    rc = ensure_buffer(&c->layer_in, &c->layer_in_bytes, pad(xb) + pad(wqb) + 2 * pad(wkb) + pad(gb));
+    rc = ensure_buffer(&c->layer_in, &c->layer_in_bytes, pad(xb) + pad(wqb + 2 * wkb) + pad(gb));
     if (rc != GQA_OK) return rc;
     uint8_t* dx = c->layer_in;
-    uint8_t* dwq = dx + pad(xb);
-    uint8_t* dwk = dwq + pad(wqb);
-    uint8_t* dwv = dwk + pad(wkb);
-    uint8_t* dg = dwv + pad(wkb);
+    uint8_t* dwq = dx + pad(xb);  // Wq, Wk, Wv back to back: one fused projection GEMM
+    uint8_t* dwk = dwq + wqb;
+    uint8_t* dwv = dwk + wkb;
+    uint8_t* dg = dwq + pad(wqb + 2 * wkb);
     c->txn = Txn();
     c->txn.b = b;
     c->txn.q_len = n_tokens;

@@ -20,24 +20,51 @@ __device__ __forceinline__ float bf16_to_f32(uint32_t w) { return __uint_as_floa
 
 constexpr int kNormThreads = 256;
 
-// One work-group per token row; 8 bf16 (16 bytes) per thread and step when hidden % 8 == 0.
+constexpr int kNormCached = 4;  // 16-byte chunks a thread keeps in registers (hidden <= 8192)
+
+__device__ __forceinline__ float sum_squares(const u32x4& w) {
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float lo = bf16_to_f32(w[j] & 0xFFFFu), hi = bf16_to_f32(w[j] >> 16);
+        ss += lo * lo;
+        ss += hi * hi;
+    }
+    return ss;
+}
+
+__device__ __forceinline__ u32x4 scale_row(const u32x4& w, const u32x4& g, float inv) {
+    u32x4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float lo = __fmul_rn(__fmul_rn(bf16_to_f32(w[j] & 0xFFFFu), inv), bf16_to_f32(g[j] & 0xFFFFu));
+        const float hi = __fmul_rn(__fmul_rn(bf16_to_f32(w[j] >> 16), inv), bf16_to_f32(g[j] >> 16));
+        o[j] = (uint32_t)f32_to_bf16_rne(lo) | ((uint32_t)f32_to_bf16_rne(hi) << 16);
+    }
+    return o;
+}
+
+// One work-group per token row.  With hidden % 8 == 0 and 16-byte aligned rows each thread
+// moves 16-byte chunks and keeps its first kNormCached chunks in registers between the sum
+// of squares and the scaling pass; otherwise one bf16 per thread and step.
 __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(NormArgs a) {
     const int row = blockIdx.x;
     const uint16_t* x = a.x + (size_t)row * a.hidden;
     uint16_t* y = a.y + (size_t)row * a.hidden;
     const bool vec = (a.hidden & 7) == 0 && ((reinterpret_cast<uintptr_t>(a.x) | reinterpret_cast<uintptr_t>(a.gamma) |
                                                reinterpret_cast<uintptr_t>(a.y)) & 15) == 0;
+    constexpr int kStep = kNormThreads * 8;
     float ss = 0.f;
+    u32x4 cache[kNormCached];
     if (vec) {
-        for (int i = threadIdx.x * 8; i < a.hidden; i += kNormThreads * 8) {
-            const u32x4 w = *(const u32x4*)(x + i);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float lo = bf16_to_f32(w[j] & 0xFFFFu), hi = bf16_to_f32(w[j] >> 16);
-                ss += lo * lo;
-                ss += hi * hi;
-            }
+        for (int c = 0; c < kNormCached; ++c) {
+            const int i = c * kStep + threadIdx.x * 8;
+            cache[c] = i < a.hidden ? __builtin_nontemporal_load((const u32x4*)(x + i)) : u32x4{0u, 0u, 0u, 0u};
+            ss += sum_squares(cache[c]);
         }
+        for (int i = kNormCached * kStep + threadIdx.x * 8; i < a.hidden; i += kStep)
+            ss += sum_squares(*(const u32x4*)(x + i));
     } else {
         for (int i = threadIdx.x; i < a.hidden; i += kNormThreads) {
             const float f = bf16_to_f32(x[i]);
@@ -55,52 +82,75 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(NormArgs a) {
     for (int w = 0; w < kNormThreads / 64; ++w) total += part[w];
     const float inv = 1.0f / sqrtf(total / (float)a.hidden + a.eps);
     if (vec) {
-        for (int i = threadIdx.x * 8; i < a.hidden; i += kNormThreads * 8) {
-            const u32x4 w = *(const u32x4*)(x + i);
-            const u32x4 g = *(const u32x4*)(a.gamma + i);
-            u32x4 o;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float lo = __fmul_rn(__fmul_rn(bf16_to_f32(w[j] & 0xFFFFu), inv), bf16_to_f32(g[j] & 0xFFFFu));
-                const float hi = __fmul_rn(__fmul_rn(bf16_to_f32(w[j] >> 16), inv), bf16_to_f32(g[j] >> 16));
-                o[j] = (uint32_t)f32_to_bf16_rne(lo) | ((uint32_t)f32_to_bf16_rne(hi) << 16);
-            }
-            *(u32x4*)(y + i) = o;
+        for (int c = 0; c < kNormCached; ++c) {
+            const int i = c * kStep + threadIdx.x * 8;
+            if (i < a.hidden) *(u32x4*)(y + i) = scale_row(cache[c], *(const u32x4*)(a.gamma + i), inv);
         }
+        for (int i = kNormCached * kStep + threadIdx.x * 8; i < a.hidden; i += kStep)
+            *(u32x4*)(y + i) = scale_row(*(const u32x4*)(x + i), *(const u32x4*)(a.gamma + i), inv);
     } else {
         for (int i = threadIdx.x; i < a.hidden; i += kNormThreads)
             y[i] = f32_to_bf16_rne(__fmul_rn(__fmul_rn(bf16_to_f32(x[i]), inv), bf16_to_f32(a.gamma[i])));
     }
 }
 
-// grid (n_tokens, H_q + 2 H_kv), one thread per (2p, 2p+1) pair of one head of one token.
+constexpr int kRopeHeadsPerBlock = 8;
+
+// grid (n_tokens, ceil((H_q + 2 H_kv) / 8)); one wave per block, one lane per (2p, 2p+1)
+// pair.  A lane evaluates cos/sin once for the Q position and once for the K position, loads
+// its pair of all 8 heads (each head row is D*2 contiguous bytes across the wave) before
+// rotating and storing them.
 __global__ __launch_bounds__(kMaxRopePairs) void rope_scatter_kernel(RopeArgs a) {
-    const int t = blockIdx.x, h = blockIdx.y, p = threadIdx.x;
+    const int t = blockIdx.x, p = threadIdx.x;
     const int D = a.head_dim;
-    const uint32_t w = *(const uint32_t*)(a.qkv + (size_t)t * a.ld + (size_t)h * D + 2 * p);
-    uint32_t out = w;
-    const bool is_q = h < a.n_q_heads, is_k = !is_q && h < a.n_q_heads + a.n_kv_heads;
-    if (a.rope && (is_q || is_k)) {
+    const int H = a.n_q_heads + 2 * a.n_kv_heads;
+    const int h0 = blockIdx.y * kRopeHeadsPerBlock;
+    const uint32_t* src = (const uint32_t*)(a.qkv + (size_t)t * a.ld) + p;
+    uint32_t w[kRopeHeadsPerBlock];
+#pragma unroll
+    for (int i = 0; i < kRopeHeadsPerBlock; ++i)
+        w[i] = (h0 + i < H) ? __builtin_nontemporal_load(src + (size_t)(h0 + i) * (D / 2)) : 0u;
+    float cq = 1.f, sq = 0.f, ck = 1.f, sk = 0.f;
+    if (a.rope) {
         // Each product and sum is rounded to fp32 on its own: no fused multiply-add.
 #pragma clang fp contract(off)
-        const int pos = (is_q ? a.q_pos_base : a.kv_pos_base) + t;
-        const float phase = (float)pos * a.theta[p];
         double sd, cd;
-        sincos((double)phase, &sd, &cd);
-        const float s = (float)sd, c = (float)cd;
-        const float x0 = bf16_to_f32(w & 0xFFFFu), x1 = bf16_to_f32(w >> 16);
-        const float r0 = x0 * c - x1 * s;
-        const float r1 = x0 * s + x1 * c;
-        out = (uint32_t)f32_to_bf16_rne(r0) | ((uint32_t)f32_to_bf16_rne(r1) << 16);
+        sincos((double)((float)(a.q_pos_base + t) * a.theta[p]), &sd, &cd);
+        sq = (float)sd;
+        cq = (float)cd;
+        if (a.kv_pos_base == a.q_pos_base) {
+            sk = sq;
+            ck = cq;
+        } else {
+            sincos((double)((float)(a.kv_pos_base + t) * a.theta[p]), &sd, &cd);
+            sk = (float)sd;
+            ck = (float)cd;
+        }
     }
-    uint16_t* dst;
-    if (is_q) {
-        dst = a.q_out + ((size_t)h * a.n_tokens + t) * D;
-    } else {
-        const int g = is_k ? h - a.n_q_heads : h - a.n_q_heads - a.n_kv_heads;
-        dst = (is_k ? a.kc : a.vc) + ((size_t)g * a.l_cap + a.row0 + t) * D;
+#pragma unroll
+    for (int i = 0; i < kRopeHeadsPerBlock; ++i) {
+        const int h = h0 + i;
+        if (h >= H) break;
+        uint32_t out = w[i];
+        const bool is_q = h < a.n_q_heads, is_k = !is_q && h < a.n_q_heads + a.n_kv_heads;
+        if (a.rope && (is_q || is_k)) {
+#pragma clang fp contract(off)
+            const float c = is_q ? cq : ck, s = is_q ? sq : sk;
+            const float x0 = bf16_to_f32(w[i] & 0xFFFFu), x1 = bf16_to_f32(w[i] >> 16);
+            const float r0 = x0 * c - x1 * s;
+            const float r1 = x0 * s + x1 * c;
+            out = (uint32_t)f32_to_bf16_rne(r0) | ((uint32_t)f32_to_bf16_rne(r1) << 16);
+        }
+        uint16_t* dst;
+        if (is_q) {
+            dst = a.q_out + ((size_t)h * a.n_tokens + t) * D;
+        } else {
+            const int g = is_k ? h - a.n_q_heads : h - a.n_q_heads - a.n_kv_heads;
+            dst = (is_k ? a.kc : a.vc) + ((size_t)g * a.l_cap + a.row0 + t) * D;
+        }
+        *(uint32_t*)(dst + 2 * p) = out;
     }
-    *(uint32_t*)(dst + 2 * p) = out;
 }
 
 }  // namespace
@@ -114,8 +164,9 @@ hipError_t launch_rms_norm(const NormArgs& a, hipStream_t s) {
 hipError_t launch_rope_scatter(const RopeArgs& a, hipStream_t s) {
     if (a.n_tokens < 1) return hipSuccess;
     if (a.head_dim < 2 || a.head_dim > 2 * kMaxRopePairs || (a.head_dim & 1)) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(rope_scatter_kernel, dim3(a.n_tokens, a.n_q_heads + 2 * a.n_kv_heads), dim3(a.head_dim / 2), 0,
-                       s, a);
+    const int heads = a.n_q_heads + 2 * a.n_kv_heads;
+    hipLaunchKernelGGL(rope_scatter_kernel, dim3(a.n_tokens, (heads + kRopeHeadsPerBlock - 1) / kRopeHeadsPerBlock),
+                       dim3(a.head_dim / 2), 0, s, a);
     return hipGetLastError();
 }
 

@@ -33,10 +33,17 @@ def host(t) -> np.ndarray:
     return t.cpu().numpy().view(np.uint16)
 
 
-def stage(acc, x, wq, wk, wv, gamma, *, b=0, q_pos_base=0, kv_pos_base=0, row0=0, rope=True, eps=1e-5):
-    """Run gqa_layer_qkv_device; returns Q [H_q, L, D] and the K/V rows written."""
+def stage(acc, x, wq, wk, wv, gamma, *, b=0, q_pos_base=0, kv_pos_base=0, row0=0, rope=True, eps=1e-5,
+          fused=False):
+    """Run gqa_layer_qkv_device; returns Q [H_q, L, D] and the K/V rows written.  fused=True
+    stores Wq, Wk, Wv back to back (the library then runs one projection GEMM)."""
     L, hidden = x.shape
-    bufs = [dev(a) for a in (x, wq, wk, wv)]
+    if fused:
+        wqkv = dev(np.concatenate([wq, wk, wv]))
+        nq, nkv = wq.shape[0], wk.shape[0]
+        bufs = [dev(x), wqkv[:nq], wqkv[nq:nq + nkv], wqkv[nq + nkv:]]
+    else:
+        bufs = [dev(a) for a in (x, wq, wk, wv)]
     g = dev(gamma) if gamma is not None else None
     q = torch.empty((acc.n_q_heads, L, acc.head_dim), dtype=torch.int16, device="cuda")
     torch.cuda.synchronize()  # the uploads ran on torch's stream; the stage runs on the engine's
@@ -53,14 +60,15 @@ def weights(rng, nq, nkv, hidden):
     return bf16_normal(rng, (nq, hidden), s), bf16_normal(rng, (nkv, hidden), s), bf16_normal(rng, (nkv, hidden), s)
 
 
+@pytest.mark.parametrize("fused", [False, True])
 @pytest.mark.parametrize("hidden,L", [(768, 37), (1001, 5), (4096, 64)])
-def test_projection_within_fp32_accumulation_bound(hidden, L):
-    print(f"[layer] projection hidden={hidden} L={L}", flush=True)
+def test_projection_within_fp32_accumulation_bound(hidden, L, fused):
+    print(f"[layer] projection hidden={hidden} L={L} fused={fused}", flush=True)
     rng = np.random.default_rng(hidden + L)
     with AttentionAccelerator(n_q_heads=8, n_kv_heads=2, head_dim=128, max_seq_len=128) as acc:
         x = bf16_normal(rng, (L, hidden))
         wq, wk, wv = weights(rng, 1024, 256, hidden)
-        q, k, v = stage(acc, x, wq, wk, wv, None, rope=False, row0=3)
+        q, k, v = stage(acc, x, wq, wk, wv, None, rope=False, row0=3, fused=fused)
     for got_heads, w, H in ((q, wq, 8), (k, wk, 2), (v, wv, 2)):
         got = orc.bf16_u16_to_fp32(got_heads).astype(np.float64).transpose(1, 0, 2).reshape(L, H * 128)
         exact = lo.project_exact(x, w)
@@ -70,10 +78,11 @@ def test_projection_within_fp32_accumulation_bound(hidden, L):
         assert same > 0.95
 
 
-@pytest.mark.parametrize("extra_cols", [0, 3])
+@pytest.mark.parametrize("extra_cols", [0, 3, 8192])
 def test_rms_norm_through_identity_projection(extra_cols):
     """Wq = [I | 0] makes Q the first H_q*D columns of the normalised x exactly (fp32 sums of
-    one non-zero product); extra_cols = 3 exercises the unaligned (scalar) kernel path."""
+    one non-zero product); extra_cols = 3 exercises the unaligned (scalar) kernel path and
+    8192 rows longer than the register-cached part."""
     nq = 1024
     hidden = nq + extra_cols
     L = 19
@@ -138,7 +147,7 @@ def test_run_layer_llama3_shape(L, causal, qb, kb):
         out = acc.run_layer(x, wq, wk, wv, gamma, q_pos_base=qb, kv_pos_base=kb, causal=causal)
         prof = acc.last_profile.to_dict()
         k_layer, v_layer = acc.read_kv(0, 0, L)
-        q, k, v = stage(acc, x, wq, wk, wv, gamma, b=1, q_pos_base=qb, kv_pos_base=kb)
+        q, k, v = stage(acc, x, wq, wk, wv, gamma, b=1, q_pos_base=qb, kv_pos_base=kb, fused=True)
     assert out.dtype == np.float32 and out.shape == (L, 4096)
     assert prof["host_qkv_projection_ms"] > 0 and prof["host_rope_ms"] > 0 and prof["layer_total_ms"] > 0
     assert np.array_equal(k_layer, k) and np.array_equal(v_layer, v)
@@ -165,7 +174,7 @@ def test_run_layer_kv260_numerics_is_word_exact():
     x, wq, wk, wv, gamma = _layer_inputs(rng, L)
     with AttentionAccelerator(batch=2, numerics="kv260") as acc:
         out = acc.run_layer(x, wq, wk, wv, gamma, q_pos_base=2, kv_pos_base=2, causal=True)
-        q, k, v = stage(acc, x, wq, wk, wv, gamma, b=1, q_pos_base=2, kv_pos_base=2)
+        q, k, v = stage(acc, x, wq, wk, wv, gamma, b=1, q_pos_base=2, kv_pos_base=2, fused=True)
     want, _, _ = rtl.attention(q, k, v, causal=True, q_pos_base=2, kv_pos_base=2)
     got = orc.fp32_to_bf16_u16(out.reshape(L, 32, 128).transpose(1, 0, 2))
     assert np.array_equal(got, want)
