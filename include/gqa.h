@@ -99,6 +99,33 @@ int gqa_set_option(gqa_ctx* ctx, int32_t option, int64_t value);
 const char* gqa_status_string(int32_t code);
 int gqa_device_count(int32_t* out_count);
 
+/* ---- paged K/V cache --------------------------------------------------------
+ * No reference counterpart: the KV260 reloads its cache on every transaction
+ * (kv_cache_ram.sv:77-91, attn_driver.py:418-422), so it has no cache manager.  A paged
+ * context keeps K and V in pools of n_pages pages of page_size rows (a power of two >= 64;
+ * layout [n_pages][H_kv][page_size][D]) and one block table per sequence (page of each
+ * page_size-row run of token rows, -1 = unmapped).  Every entry point works as on a
+ * contiguous context, reading and writing through the tables; host-pointer forms return
+ * GQA_ERR_RANGE when a row they touch is unmapped, device forms read unmapped rows as
+ * zeros and skip writes to them.  KV260 numerics are not available on a paged context.
+ * gqa_paged_reserve maps pages so rows [0, n_rows) of sequence b are backed (GQA_ERR_OOM,
+ * changing nothing, when the pool is short); gqa_paged_release returns a sequence's pages;
+ * gqa_paged_evict_lru releases whole sequences, least recently used first (reserve, load,
+ * prefill and host-pointer decode calls count as uses) and skipping the n_pinned sequence
+ * indices in pinned, until n_free_pages pages are free, writing up to max_evicted evicted
+ * sequence indices (GQA_ERR_OOM, releasing nothing, if that cannot be reached).  Reserve,
+ * release and evict synchronise the context stream; launches on other streams that read a
+ * sequence must finish before its pages are released.  gqa_cache_pointers returns the
+ * pools and page_size as l_cap. */
+int gqa_create_paged(const gqa_config* cfg, int32_t page_size, int32_t n_pages, gqa_ctx** out_ctx);
+int gqa_paged_reserve(gqa_ctx* ctx, int32_t b, int32_t n_rows);
+int gqa_paged_release(gqa_ctx* ctx, int32_t b);
+int gqa_paged_evict_lru(gqa_ctx* ctx, int32_t n_free_pages, const int32_t* pinned, int32_t n_pinned,
+                        int32_t* evicted, int32_t max_evicted, int32_t* n_evicted);
+int gqa_paged_info(gqa_ctx* ctx, int32_t* page_size, int32_t* n_pages, int32_t* n_free,
+                   int32_t* max_pages);
+int gqa_paged_table(gqa_ctx* ctx, int32_t b, int32_t* out, int32_t n);
+
 /* ---- K/V cache --------------------------------------------------------------
  * gqa_load_kv replaces the KV branch of _service_request + _transfer(DEST_K_CACHE /
  * DEST_V_CACHE) (attn_driver.py:378-422) and the cache write of kv_cache_ram.sv:77-83:

@@ -77,6 +77,7 @@ _CTX = c_void_p
 # name -> argtypes; every function returns int (status)
 _SIGNATURES = {
     "gqa_create": [POINTER(GqaConfig), POINTER(c_void_p)],
+    "gqa_create_paged": [POINTER(GqaConfig), c_int32, c_int32, POINTER(c_void_p)],
     "gqa_destroy": [_CTX],
     "gqa_get_config": [_CTX, POINTER(GqaConfig)],
     "gqa_set_option": [_CTX, c_int32, c_int64],
@@ -105,6 +106,11 @@ _SIGNATURES = {
     "gqa_prefill_append_device": [_CTX, c_int32, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32,
                                   c_int32, c_int32, c_void_p, c_void_p, c_void_p],
     "gqa_cache_pointers": [_CTX, POINTER(c_void_p), POINTER(c_void_p), _P32],
+    "gqa_paged_reserve": [_CTX, c_int32, c_int32],
+    "gqa_paged_release": [_CTX, c_int32],
+    "gqa_paged_evict_lru": [_CTX, c_int32, _P32, c_int32, _P32, c_int32, _P32],
+    "gqa_paged_info": [_CTX, _P32, _P32, _P32, _P32],
+    "gqa_paged_table": [_CTX, c_int32, _P32, c_int32],
     "gqa_submit_layer": [_CTX, c_int32, _P16, c_int32, c_int32, _P16, _P16, _P16, _P16, c_float, c_int32, c_int32,
                          c_int32, c_int32],
     "gqa_layer_qkv_device": [_CTX, c_int32, c_void_p, c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p,

@@ -302,6 +302,8 @@ class AttentionAccelerator:
         device: int = 0,
         position_limit: int = ABSOLUTE_POSITION_LIMIT,
         numerics: str = "exact",
+        page_size: int | None = None,
+        n_pages: int | None = None,
     ) -> None:
         self._closed = True
         self._ctx = ctypes.c_void_p()
@@ -322,7 +324,13 @@ class AttentionAccelerator:
         cfg = _lib.GqaConfig(self.batch, self.n_q_heads, self.n_kv_heads, self.head_dim, self.max_seq_len,
                              self.max_q_len, float(scale or 0.0), int(device))
         lib = _lib.lib()
-        rc = lib.gqa_create(ctypes.byref(cfg), ctypes.byref(self._ctx))
+        self.paged = page_size is not None
+        if self.paged:
+            if n_pages is None:
+                n_pages = self.batch * -(-self.max_seq_len // int(page_size))
+            rc = lib.gqa_create_paged(ctypes.byref(cfg), int(page_size), int(n_pages), ctypes.byref(self._ctx))
+        else:
+            rc = lib.gqa_create(ctypes.byref(cfg), ctypes.byref(self._ctx))
         if rc != _lib.GQA_OK:
             raise RuntimeError(f"unable to create the GPU attention engine: {_lib.status_string(rc)} (0x{rc:02x})")
         got = _lib.GqaConfig()
@@ -526,6 +534,53 @@ class AttentionAccelerator:
         self._pl_clock_mhz = float(mhz.value)
         return {"cycles": int(total.value), "mac_cycles": int(kern.value), "stall_cycles": int(copy.value)}
 
+    # ---- paged cache ------------------------------------------------------------------------
+    def reserve(self, b: int, n_rows: int) -> None:
+        """Map pages so rows 0..n_rows-1 of sequence ``b`` are backed (paged engines only).
+        Raises ``MemoryError`` when the pool has too few free pages (nothing changes)."""
+        self._ensure_open()
+        rc = self._lib.gqa_paged_reserve(self._ctx, int(b), int(n_rows))
+        if rc == _lib.GQA_ERR_OOM:
+            raise MemoryError(f"page pool exhausted reserving {n_rows} rows for sequence {b}")
+        _lib.check(rc, "gqa_paged_reserve")
+
+    def release(self, b: int) -> None:
+        """Return every page of sequence ``b`` to the pool."""
+        self._call("gqa_paged_release", int(b))
+
+    def evict_lru(self, n_free_pages: int, pinned=()) -> list[int]:
+        """Release whole sequences, least recently used first and never those in ``pinned``,
+        until ``n_free_pages`` pages are free; returns the evicted sequence indices.  Raises
+        ``MemoryError`` (releasing nothing) when that is impossible."""
+        self._ensure_open()
+        pin = np.ascontiguousarray(np.asarray(list(pinned), dtype=np.int32))
+        out = np.empty(self.batch, dtype=np.int32)
+        n = ctypes.c_int32(0)
+        rc = self._lib.gqa_paged_evict_lru(self._ctx, int(n_free_pages), _lib.as_i32_ptr(pin) if pin.size else None,
+                                           int(pin.size), _lib.as_i32_ptr(out), int(out.size), ctypes.byref(n))
+        if rc == _lib.GQA_ERR_OOM:
+            raise MemoryError(f"cannot free {n_free_pages} pages without evicting a pinned sequence")
+        _lib.check(rc, "gqa_paged_evict_lru")
+        return [int(x) for x in out[: n.value]]
+
+    def page_info(self) -> dict[str, int]:
+        """Page size, pool size, free pages and block-table width of a paged engine."""
+        vals = [ctypes.c_int32(0) for _ in range(4)]
+        self._call("gqa_paged_info", *(ctypes.byref(v) for v in vals))
+        return dict(zip(("page_size", "n_pages", "free_pages", "max_pages"), (int(v.value) for v in vals)))
+
+    def page_table(self, b: int) -> np.ndarray:
+        """Block table of sequence ``b``: page index per page-sized run of rows (-1 unmapped)."""
+        width = self.page_info()["max_pages"]
+        out = np.empty(width, dtype=np.int32)
+        self._call("gqa_paged_table", int(b), _lib.as_i32_ptr(out), int(width))
+        return out
+
+    def _reserve_transaction(self, L: int) -> None:
+        # A board transaction reloads the whole cache of its one sequence.
+        if self.paged:
+            self.reserve(0, L)
+
     # ---- data movement ----------------------------------------------------------------------
     def load_kv(self, k_heads: np.ndarray, v_heads: np.ndarray, *, b: int = 0, start_pos: int = 0) -> None:
         """Write K/V rows [H_kv, n, D] of sequence ``b`` at rows start_pos.. (bit-exact)."""
@@ -723,6 +778,7 @@ class AttentionAccelerator:
         prof.driver_setup_ms = (time.perf_counter() - t) * 1000.0
 
         t = time.perf_counter()
+        self._reserve_transaction(L)
         self.load_kv(k_u16, v_u16, b=0, start_pos=0)
         prof.kv_dma_transfer_ms = (time.perf_counter() - t) * 1000.0
         prof.kv_dma_transfers = 2
@@ -820,6 +876,7 @@ class AttentionAccelerator:
         prof.driver_setup_ms = (time.perf_counter() - t) * 1000.0
 
         t = time.perf_counter()
+        self._reserve_transaction(L)
         self._call("gqa_submit_layer", 0, _lib.as_u16_ptr(x), L, hidden, _lib.as_u16_ptr(wq_u),
                    _lib.as_u16_ptr(wk_u), _lib.as_u16_ptr(wv_u),
                    None if gamma is None else _lib.as_u16_ptr(gamma), float(rms_eps), int(q_pos_base),

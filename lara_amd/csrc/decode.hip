@@ -101,7 +101,7 @@ __device__ __forceinline__ int clamp_len(int len, int l_max) {
 
 __device__ __forceinline__ u32x4 ld_stream(const u32x4* p) { return __builtin_nontemporal_load(p); }
 
-template <int D, int G, int NW>
+template <int D, int G, int NW, bool PAGED>
 __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
     constexpr int NCH = D / 8;               // 16-byte words per K/V row
     constexpr int QKG = 64 / G;              // lanes (keys) per head in the QK layout
@@ -132,10 +132,18 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
     const bool has_new = pos >= 0 && pos < a.l_max;
     const u32x4* knew = reinterpret_cast<const u32x4*>(a.k_new) + (size_t)unit * NCH;
     const u32x4* vnew = reinterpret_cast<const u32x4*>(a.v_new) + (size_t)unit * NCH;
+    const int32_t* trow = PAGED ? a.block_table + (size_t)b * a.max_pages : nullptr;
     if (has_new && split == 0 && threadIdx.x < 2 * NCH) {
         const int c = threadIdx.x % NCH;
-        u32x4* dst = reinterpret_cast<u32x4*>(threadIdx.x < NCH ? a.kc : a.vc) + (row0 + pos) * NCH + c;
-        *dst = (threadIdx.x < NCH) ? knew[c] : vnew[c];
+        int64_t r;
+        if constexpr (PAGED)
+            r = paged_row(trow, a.page_shift, a.n_kv_heads, h, pos);  // -1: unmapped, not written
+        else
+            r = (int64_t)(row0 + pos);
+        if (r >= 0) {
+            u32x4* dst = reinterpret_cast<u32x4*>(threadIdx.x < NCH ? a.kc : a.vc) + (size_t)r * NCH + c;
+            *dst = (threadIdx.x < NCH) ? knew[c] : vnew[c];
+        }
     }
 
     __shared__ __attribute__((aligned(16))) u32x4 lds_k[NW][RK * NCH];
@@ -171,25 +179,44 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
     float m_run = -INFINITY;  // running max (log2 units) of head gq, uniform over its lanes
     float l_lane = 0.f;       // this lane's share of the running sum of head gq
 
-    const u32x4* kbase = reinterpret_cast<const u32x4*>(a.kc) + row0 * NCH;
-    const u32x4* vbase = reinterpret_cast<const u32x4*>(a.vc) + row0 * NCH;
+    const u32x4* kbase = reinterpret_cast<const u32x4*>(a.kc) + (PAGED ? 0 : row0 * NCH);
+    const u32x4* vbase = reinterpret_cast<const u32x4*>(a.vc) + (PAGED ? 0 : row0 * NCH);
+    const u32x4* zero = reinterpret_cast<const u32x4*>(a.zero_row);
 
-    // Rounds start at multiples of RK and l_cap is a multiple of 64, so every row a round
-    // touches lies inside the sequence's cache region; rows >= k_end are masked below.
+    // Rounds start at multiples of RK and l_cap (the page size, when paged) is a multiple of
+    // 64, so every row a round touches lies inside the sequence's cache region (one page);
+    // rows >= k_end are masked below.
     const int n_rounds = (k_end - k_begin + RK - 1) / RK;
     u32x4 kr[NLD], vr[NLD];
-    // Row `key` of this lane's column: the cache, or the row appended by this launch.
-    auto load_row = [&](int key, u32x4& k, u32x4& v) {
-        const bool fresh = has_new && key == pos;
-        const size_t off = (size_t)key * NCH + cpv;
-        k = ld_stream(fresh ? knew + cpv : kbase + off);
-        v = ld_stream(fresh ? vnew + cpv : vbase + off);
+    // Rows of a round: first word of row key0 and the row stride (0: an unmapped page, read
+    // as the zero row).  key0 is uniform across the wave, so the page lookup is scalar.
+    struct RoundSrc {
+        const u32x4* k;
+        const u32x4* v;
+        int stride;
+    };
+    auto round_src = [&](int key0) -> RoundSrc {
+        if constexpr (PAGED) {
+            const int64_t r = paged_row(trow, a.page_shift, a.n_kv_heads, h, __builtin_amdgcn_readfirstlane(key0));
+            if (r < 0) return {zero, zero, 0};
+            return {kbase + (size_t)r * NCH, vbase + (size_t)r * NCH, NCH};
+        } else {
+            return {kbase + (size_t)key0 * NCH, vbase + (size_t)key0 * NCH, NCH};
+        }
+    };
+    // Row key0 + rel of this lane's column: the cache, or the row appended by this launch.
+    auto load_row = [&](const RoundSrc& src, int key0, int rel, u32x4& k, u32x4& v) {
+        const bool fresh = has_new && key0 + rel == pos;
+        const size_t off = (size_t)rel * src.stride + cpv;
+        k = ld_stream(fresh ? knew + cpv : src.k + off);
+        v = ld_stream(fresh ? vnew + cpv : src.v + off);
     };
     int r = wave;
     if (r < n_rounds) {
         const int key0 = k_begin + r * RK;
+        const RoundSrc src = round_src(key0);
 #pragma unroll
-        for (int j = 0; j < NLD; ++j) load_row(key0 + j * RPL + rpv, kr[j], vr[j]);
+        for (int j = 0; j < NLD; ++j) load_row(src, key0, j * RPL + rpv, kr[j], vr[j]);
     }
     for (; r < n_rounds; r += NW) {
         const int key0 = k_begin + r * RK;
@@ -211,8 +238,9 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
         // Prefetch the next round of this wave.
         if (r + NW < n_rounds) {
             const int key1 = key0 + NW * RK;
+            const RoundSrc src = round_src(key1);
 #pragma unroll
-            for (int j = 0; j < NLD; ++j) load_row(key1 + j * RPL + rpv, kr[j], vr[j]);
+            for (int j = 0; j < NLD; ++j) load_row(src, key1, j * RPL + rpv, kr[j], vr[j]);
         }
         wave_lds_sync();
 
@@ -395,7 +423,10 @@ constexpr int kDecodeWaves = 4;
 template <int D, int G>
 hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t s) {
     dim3 grid(a.max_splits, a.batch * a.n_kv_heads);
-    hipLaunchKernelGGL((decode_split_kernel<D, G, kDecodeWaves>), grid, dim3(kDecodeWaves * 64), 0, s, a);
+    if (a.block_table != nullptr)
+        hipLaunchKernelGGL((decode_split_kernel<D, G, kDecodeWaves, true>), grid, dim3(kDecodeWaves * 64), 0, s, a);
+    else
+        hipLaunchKernelGGL((decode_split_kernel<D, G, kDecodeWaves, false>), grid, dim3(kDecodeWaves * 64), 0, s, a);
     return hipGetLastError();
 }
 

@@ -2,6 +2,7 @@
 // Declarations and the reference interface each entry point replaces are in include/gqa.h.
 #include "../../include/gqa.h"
 #include "gqa_internal.h"
+#include "page_table.h"
 
 #include <math.h>
 #include <rocblas/rocblas.h>
@@ -75,6 +76,12 @@ struct gqa_ctx {
     size_t layer_tmp_bytes = 0;
     hipEvent_t ev_layer[4] = {};
     float layer_us[3] = {};
+    // Paged cache (gqa_create_paged): k_cache/v_cache are page pools [n_pages][H_kv][P][D], the
+    // block tables [B][max_pages] live on the device (table_dev) and in `pages` on the host.
+    int paged = 0;
+    int page_size = 0, page_shift = 0, n_pages = 0, max_pages = 0;
+    int32_t* table_dev = nullptr;
+    PageTable pages;
 };
 
 namespace {
@@ -95,7 +102,21 @@ void last_hip_error(hipError_t e, const char* what) {
 }
 
 inline size_t kv_words(const gqa_ctx* c) {
+    if (c->paged) return (size_t)c->n_pages * c->cfg.n_kv_heads * c->page_size * c->cfg.head_dim;
     return (size_t)c->cfg.batch * c->cfg.n_kv_heads * c->l_cap * c->cfg.head_dim;
+}
+
+// Row (in units of D elements) of token t of (b, h) in the cache, or -1 (unmapped page).
+int64_t cache_row(const gqa_ctx* c, int b, int h, int t) {
+    if (!c->paged) return ((int64_t)b * c->cfg.n_kv_heads + h) * c->l_cap + t;
+    const int page = c->pages.row(b)[t >> c->page_shift];
+    if (page < 0) return -1;
+    return (((int64_t)page * c->cfg.n_kv_heads + h) << c->page_shift) + (t & (c->page_size - 1));
+}
+
+// True when rows [row0, row0 + n) of sequence b are backed (always, for a contiguous cache).
+bool rows_backed(const gqa_ctx* c, int b, int64_t row0, int64_t n) {
+    return !c->paged || c->pages.covers(b, row0, n, c->page_size);
 }
 
 hipStream_t pick_stream(gqa_ctx* c, void* s) { return s ? (hipStream_t)s : c->stream; }
@@ -168,6 +189,10 @@ int run_decode(gqa_ctx* c, const void* q, const int32_t* lens, const void* k_new
     a.part_ml = c->part_ml;
     a.out = (uint16_t*)o;
     a.lse = lse;
+    a.block_table = c->paged ? c->table_dev : nullptr;
+    a.page_shift = c->page_shift;
+    a.max_pages = c->max_pages;
+    a.zero_row = c->zero_row;
     timer_begin(c, GQA_TIMER_DECODE, s);
     HIP_TRY(launch_decode(c->cfg.head_dim, c->group, a, s));
     timer_end(c, GQA_TIMER_DECODE, s);
@@ -193,7 +218,9 @@ int check_prefill_args(const gqa_ctx* c, int32_t b, int32_t q_len, int32_t q_pos
 int run_prefill(gqa_ctx* c, int32_t b, const void* q, int32_t q_len, int32_t q_pos_base, int32_t kv_len,
                 int32_t kv_pos_base, int32_t causal, void* o, float* lse, hipStream_t s,
                 const void* k_new = nullptr, const void* v_new = nullptr, int32_t n_new = 0) {
+    if (c->paged) c->pages.touch(b);
     if (c->numerics == GQA_NUMERICS_KV260) {
+        if (c->paged) return GQA_ERR_UNSUPPORTED;
         const size_t seq = (size_t)b * c->cfg.n_kv_heads * c->l_cap * c->cfg.head_dim;
         if (k_new != nullptr && n_new > 0) {
             const size_t D = c->cfg.head_dim;
@@ -234,10 +261,12 @@ int run_prefill(gqa_ctx* c, int32_t b, const void* q, int32_t q_len, int32_t q_p
     if (prefill_workspace_floats(plan, q_len, c->cfg.n_q_heads, c->cfg.head_dim) > c->pre_ws_floats)
         plan = plan_prefill(q_len, kv_span, c->group, c->cfg.n_kv_heads, 1, 1);  // one segment
     PrefillArgs a{};
-    const size_t seq_off = (size_t)b * c->cfg.n_kv_heads * c->l_cap * c->cfg.head_dim;
+    const size_t seq_off = c->paged ? 0 : (size_t)b * c->cfg.n_kv_heads * c->l_cap * c->cfg.head_dim;
     a.q = (const uint16_t*)q;
     a.kc = c->k_cache + seq_off;
     a.vc = c->v_cache + seq_off;
+    a.block_table = c->paged ? c->table_dev + (size_t)b * c->max_pages : nullptr;
+    a.page_shift = c->page_shift;
     a.k_new = (const uint16_t*)k_new;
     a.v_new = (const uint16_t*)v_new;
     a.new_begin = kv_len - n_new;
@@ -391,9 +420,11 @@ int run_layer_qkv(gqa_ctx* c, int32_t b, const void* x, int32_t n_tokens, int32_
     ra.kv_pos_base = kv_pos_base;
     ra.rope = rope ? 1 : 0;
     ra.q_out = (uint16_t*)q_out;
-    const size_t seq = (size_t)b * c->cfg.n_kv_heads * c->l_cap * D;
+    const size_t seq = c->paged ? 0 : (size_t)b * c->cfg.n_kv_heads * c->l_cap * D;
     ra.kc = c->k_cache + seq;
     ra.vc = c->v_cache + seq;
+    ra.block_table = c->paged ? c->table_dev + (size_t)b * c->max_pages : nullptr;
+    ra.page_shift = c->page_shift;
     ra.l_cap = c->l_cap;
     ra.row0 = row0;
     for (int p = 0; p < D / 2; ++p) ra.theta[p] = (float)pow(kRopeBase, -2.0 * p / D);
@@ -408,6 +439,134 @@ int layer_times(gqa_ctx* c) {
         float ms = 0.f;
         HIP_TRY(hipEventElapsedTime(&ms, c->ev_layer[i], c->ev_layer[i + 1]));
         c->layer_us[i] = ms * 1000.f;
+    }
+    return GQA_OK;
+}
+
+int create_ctx(const gqa_config* cfg, int32_t page_size, int32_t n_pages, gqa_ctx** out_ctx) {
+    if (!cfg || !out_ctx) return GQA_ERR_NULL;
+    *out_ctx = nullptr;
+    const gqa_config& k = *cfg;
+    if (k.batch < 1 || k.n_q_heads < 1 || k.n_kv_heads < 1 || k.n_q_heads % k.n_kv_heads != 0 ||
+        k.max_seq_len < 1 || k.max_q_len < 1 || !(k.scale >= 0.f) || !isfinite(k.scale))
+        return GQA_ERR_BAD_CFG;
+    const int group = k.n_q_heads / k.n_kv_heads;
+    if (!decode_supported(k.head_dim, group) && !prefill_supported(k.head_dim, group)) return GQA_ERR_UNSUPPORTED;
+
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n < 1) return GQA_ERR_NO_DEVICE;
+    if (k.device < 0 || k.device >= n) return GQA_ERR_NO_DEVICE;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, k.device) != hipSuccess) return GQA_ERR_NO_DEVICE;
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) return GQA_ERR_NO_DEVICE;
+    HIP_TRY(hipSetDevice(k.device));
+
+    gqa_ctx* c = new gqa_ctx();
+    c->cfg = k;
+    c->group = group;
+    c->l_cap = ((k.max_seq_len + 63) / 64) * 64;
+    c->max_splits_cap = (c->l_cap + kMinChunk - 1) / kMinChunk;
+    c->scale = k.scale > 0.f ? k.scale : (float)(1.0 / sqrt((double)k.head_dim));
+    c->cfg.scale = c->scale;
+    c->clock_mhz = prop.clockRate / 1000.0;
+    if (page_size > 0) {
+        c->paged = 1;
+        c->page_size = page_size;
+        while ((1 << c->page_shift) < page_size) ++c->page_shift;
+        c->n_pages = n_pages;
+        c->max_pages = (k.max_seq_len + page_size - 1) / page_size;
+        c->pages = PageTable(k.batch, c->max_pages, n_pages);
+    }
+    const size_t D = (size_t)k.head_dim;
+    const size_t units = (size_t)k.batch * k.n_kv_heads;
+    c->stage_words = (size_t)k.n_q_heads * D * (size_t)(k.batch > k.max_q_len ? k.batch : k.max_q_len);
+    c->lse_words = (size_t)k.n_q_heads * (size_t)(k.batch > k.max_q_len ? k.batch : k.max_q_len);
+
+    int rc = GQA_OK;
+    auto alloc = [&](void** p, size_t bytes) {
+        if (rc != GQA_OK) return;
+        if (hipMalloc(p, bytes) != hipSuccess) rc = GQA_ERR_OOM;
+    };
+    alloc((void**)&c->k_cache, kv_words(c) * 2);
+    alloc((void**)&c->v_cache, kv_words(c) * 2);
+    alloc((void**)&c->part_o, units * c->max_splits_cap * group * D * sizeof(float));
+    alloc((void**)&c->part_ml, units * c->max_splits_cap * group * 2 * sizeof(float));
+    if (prefill_supported(k.head_dim, group)) {
+        // Largest segmented plan over every query length up to max_q_len (keys up to L_max).
+        for (int q_len = 32; q_len < k.max_q_len + 32; q_len += 32) {
+            const int ql = q_len < k.max_q_len ? q_len : k.max_q_len;
+            const PrefillPlan p = plan_prefill(ql, k.max_seq_len, group, k.n_kv_heads, kTargetPrefillWgs, kMaxPrefillSegs);
+            const size_t f = prefill_workspace_floats(p, ql, k.n_q_heads, k.head_dim);
+            if (f > c->pre_ws_floats) c->pre_ws_floats = f;
+        }
+        if (c->pre_ws_floats > 0) alloc((void**)&c->pre_ws, c->pre_ws_floats * sizeof(float));
+    }
+    alloc((void**)&c->q_dev, c->stage_words * 2);
+    alloc((void**)&c->o_dev, c->stage_words * 2);
+    alloc((void**)&c->lse_dev, c->lse_words * sizeof(float));
+    alloc((void**)&c->lens_dev, (size_t)k.batch * sizeof(int32_t));
+    alloc((void**)&c->zero_row, D * 2);
+    alloc((void**)&c->pos_dev, (size_t)k.batch * sizeof(int32_t));
+    alloc((void**)&c->rows_dev, 2 * units * D * 2);
+    alloc((void**)&c->new_dev, 2 * (size_t)k.n_kv_heads * k.max_q_len * D * 2);
+    if (c->paged) alloc((void**)&c->table_dev, (size_t)k.batch * c->max_pages * sizeof(int32_t));
+    if (rc == GQA_OK && hipHostMalloc((void**)&c->o_pinned, c->stage_words * 2, 0) != hipSuccess) rc = GQA_ERR_OOM;
+    if (rc == GQA_OK && hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) rc = GQA_ERR_HIP;
+    if (rc == GQA_OK) {
+        bool ok = hipEventCreate(&c->ev_begin) == hipSuccess && hipEventCreate(&c->ev_end) == hipSuccess;
+        for (int i = 0; i < 4 && ok; ++i) ok = hipEventCreate(&c->ev_t[i]) == hipSuccess;
+        if (!ok) rc = GQA_ERR_HIP;
+    }
+    // Zero the caches once so rows beyond every sequence's length hold finite words.
+    if (rc == GQA_OK && (hipMemsetAsync(c->zero_row, 0, D * 2, c->stream) != hipSuccess ||
+                         hipMemsetAsync(c->k_cache, 0, kv_words(c) * 2, c->stream) != hipSuccess ||
+                         hipMemsetAsync(c->v_cache, 0, kv_words(c) * 2, c->stream) != hipSuccess ||
+                         (c->paged && hipMemsetAsync(c->table_dev, 0xFF, (size_t)k.batch * c->max_pages * 4,
+                                                     c->stream) != hipSuccess) ||  // every entry -1: unmapped
+                         hipStreamSynchronize(c->stream) != hipSuccess))
+        rc = GQA_ERR_HIP;
+    if (rc != GQA_OK) {
+        gqa_destroy(c);
+        return rc;
+    }
+    *out_ctx = c;
+    return GQA_OK;
+}
+
+
+// Uploads sequence b's block-table row (host -> device, synchronous on the context stream).
+int upload_table_row(gqa_ctx* c, int b) {
+    HIP_TRY(hipMemcpyAsync(c->table_dev + (size_t)b * c->max_pages, c->pages.row(b),
+                           (size_t)c->max_pages * sizeof(int32_t), hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    return GQA_OK;
+}
+
+// Copies rows [start, start + n) of [H_kv][n][D] K and V between a caller buffer and a paged
+// cache, one strided copy (over the kv heads) per page the range touches.
+int copy_rows_paged(gqa_ctx* c, int b, int start, int n, const uint16_t* k_src, const uint16_t* v_src,
+                    uint16_t* k_dst, uint16_t* v_dst, hipMemcpyKind kind, hipStream_t s) {
+    const size_t D = c->cfg.head_dim;
+    const size_t pitch_pool = (size_t)c->page_size * D * 2;  // bytes between kv heads in a page
+    const size_t pitch_buf = (size_t)n * D * 2;              // bytes between kv heads in the buffer
+    for (int t = start; t < start + n;) {
+        const int t1 = std::min(start + n, ((t >> c->page_shift) + 1) << c->page_shift);
+        const int64_t row = cache_row(c, b, 0, t);
+        if (row < 0) return GQA_ERR_RANGE;
+        const size_t width = (size_t)(t1 - t) * D * 2;
+        const size_t buf = (size_t)(t - start) * D;
+        if (kind == hipMemcpyDeviceToHost) {
+            HIP_TRY(hipMemcpy2DAsync(k_dst + buf, pitch_buf, c->k_cache + row * D, pitch_pool, width,
+                                     c->cfg.n_kv_heads, kind, s));
+            HIP_TRY(hipMemcpy2DAsync(v_dst + buf, pitch_buf, c->v_cache + row * D, pitch_pool, width,
+                                     c->cfg.n_kv_heads, kind, s));
+        } else {
+            HIP_TRY(hipMemcpy2DAsync(c->k_cache + row * D, pitch_pool, k_src + buf, pitch_buf, width,
+                                     c->cfg.n_kv_heads, kind, s));
+            HIP_TRY(hipMemcpy2DAsync(c->v_cache + row * D, pitch_pool, v_src + buf, pitch_buf, width,
+                                     c->cfg.n_kv_heads, kind, s));
+        }
+        t = t1;
     }
     return GQA_OK;
 }
@@ -444,83 +603,14 @@ int gqa_device_count(int32_t* out_count) {
     return GQA_OK;
 }
 
-int gqa_create(const gqa_config* cfg, gqa_ctx** out_ctx) {
+int gqa_create(const gqa_config* cfg, gqa_ctx** out_ctx) { return create_ctx(cfg, 0, 0, out_ctx); }
+
+int gqa_create_paged(const gqa_config* cfg, int32_t page_size, int32_t n_pages, gqa_ctx** out_ctx) {
     if (!cfg || !out_ctx) return GQA_ERR_NULL;
     *out_ctx = nullptr;
-    const gqa_config& k = *cfg;
-    if (k.batch < 1 || k.n_q_heads < 1 || k.n_kv_heads < 1 || k.n_q_heads % k.n_kv_heads != 0 ||
-        k.max_seq_len < 1 || k.max_q_len < 1 || !(k.scale >= 0.f) || !isfinite(k.scale))
+    if (page_size < 64 || page_size > (1 << 16) || (page_size & (page_size - 1)) != 0 || n_pages < 1)
         return GQA_ERR_BAD_CFG;
-    const int group = k.n_q_heads / k.n_kv_heads;
-    if (!decode_supported(k.head_dim, group) && !prefill_supported(k.head_dim, group)) return GQA_ERR_UNSUPPORTED;
-
-    int n = 0;
-    if (hipGetDeviceCount(&n) != hipSuccess || n < 1) return GQA_ERR_NO_DEVICE;
-    if (k.device < 0 || k.device >= n) return GQA_ERR_NO_DEVICE;
-    hipDeviceProp_t prop;
-    if (hipGetDeviceProperties(&prop, k.device) != hipSuccess) return GQA_ERR_NO_DEVICE;
-    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) return GQA_ERR_NO_DEVICE;
-    HIP_TRY(hipSetDevice(k.device));
-
-    gqa_ctx* c = new gqa_ctx();
-    c->cfg = k;
-    c->group = group;
-    c->l_cap = ((k.max_seq_len + 63) / 64) * 64;
-    c->max_splits_cap = (c->l_cap + kMinChunk - 1) / kMinChunk;
-    c->scale = k.scale > 0.f ? k.scale : (float)(1.0 / sqrt((double)k.head_dim));
-    c->cfg.scale = c->scale;
-    c->clock_mhz = prop.clockRate / 1000.0;
-    const size_t D = (size_t)k.head_dim;
-    const size_t units = (size_t)k.batch * k.n_kv_heads;
-    c->stage_words = (size_t)k.n_q_heads * D * (size_t)(k.batch > k.max_q_len ? k.batch : k.max_q_len);
-    c->lse_words = (size_t)k.n_q_heads * (size_t)(k.batch > k.max_q_len ? k.batch : k.max_q_len);
-
-    int rc = GQA_OK;
-    auto alloc = [&](void** p, size_t bytes) {
-        if (rc != GQA_OK) return;
-        if (hipMalloc(p, bytes) != hipSuccess) rc = GQA_ERR_OOM;
-    };
-    alloc((void**)&c->k_cache, kv_words(c) * 2);
-    alloc((void**)&c->v_cache, kv_words(c) * 2);
-    alloc((void**)&c->part_o, units * c->max_splits_cap * group * D * sizeof(float));
-    alloc((void**)&c->part_ml, units * c->max_splits_cap * group * 2 * sizeof(float));
-    if (prefill_supported(k.head_dim, group)) {
-        // Largest segmented plan over every query length up to max_q_len (keys up to L_max).
-        for (int q_len = 32; q_len < k.max_q_len + 32; q_len += 32) {
-            const int ql = q_len < k.max_q_len ? q_len : k.max_q_len;
-            const PrefillPlan p = plan_prefill(ql, k.max_seq_len, group, k.n_kv_heads, kTargetPrefillWgs, kMaxPrefillSegs);
-            const size_t f = prefill_workspace_floats(p, ql, k.n_q_heads, k.head_dim);
-            if (f > c->pre_ws_floats) c->pre_ws_floats = f;
-        }
-        if (c->pre_ws_floats > 0) alloc((void**)&c->pre_ws, c->pre_ws_floats * sizeof(float));
-    }
-    alloc((void**)&c->q_dev, c->stage_words * 2);
-    alloc((void**)&c->o_dev, c->stage_words * 2);
-    alloc((void**)&c->lse_dev, c->lse_words * sizeof(float));
-    alloc((void**)&c->lens_dev, (size_t)k.batch * sizeof(int32_t));
-    alloc((void**)&c->zero_row, D * 2);
-    alloc((void**)&c->pos_dev, (size_t)k.batch * sizeof(int32_t));
-    alloc((void**)&c->rows_dev, 2 * units * D * 2);
-    alloc((void**)&c->new_dev, 2 * (size_t)k.n_kv_heads * k.max_q_len * D * 2);
-    if (rc == GQA_OK && hipHostMalloc((void**)&c->o_pinned, c->stage_words * 2, 0) != hipSuccess) rc = GQA_ERR_OOM;
-    if (rc == GQA_OK && hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) rc = GQA_ERR_HIP;
-    if (rc == GQA_OK) {
-        bool ok = hipEventCreate(&c->ev_begin) == hipSuccess && hipEventCreate(&c->ev_end) == hipSuccess;
-        for (int i = 0; i < 4 && ok; ++i) ok = hipEventCreate(&c->ev_t[i]) == hipSuccess;
-        if (!ok) rc = GQA_ERR_HIP;
-    }
-    // Zero the caches once so rows beyond every sequence's length hold finite words.
-    if (rc == GQA_OK && (hipMemsetAsync(c->zero_row, 0, D * 2, c->stream) != hipSuccess ||
-                         hipMemsetAsync(c->k_cache, 0, kv_words(c) * 2, c->stream) != hipSuccess ||
-                         hipMemsetAsync(c->v_cache, 0, kv_words(c) * 2, c->stream) != hipSuccess ||
-                         hipStreamSynchronize(c->stream) != hipSuccess))
-        rc = GQA_ERR_HIP;
-    if (rc != GQA_OK) {
-        gqa_destroy(c);
-        return rc;
-    }
-    *out_ctx = c;
-    return GQA_OK;
+    return create_ctx(cfg, page_size, n_pages, out_ctx);
 }
 
 int gqa_destroy(gqa_ctx* c) {
@@ -540,6 +630,7 @@ int gqa_destroy(gqa_ctx* c) {
     (void)hipFree(c->pos_dev);
     (void)hipFree(c->rows_dev);
     (void)hipFree(c->new_dev);
+    (void)hipFree(c->table_dev);
     if (c->o_pinned) (void)hipHostFree(c->o_pinned);
     if (c->ev_begin) (void)hipEventDestroy(c->ev_begin);
     if (c->ev_end) (void)hipEventDestroy(c->ev_end);
@@ -579,7 +670,7 @@ int gqa_set_option(gqa_ctx* c, int32_t option, int64_t value) {
             return profile_enable(c, value ? 1 : 0);
         case GQA_OPT_NUMERICS:
             if (value != GQA_NUMERICS_EXACT && value != GQA_NUMERICS_KV260) return GQA_ERR_RANGE;
-            if (value == GQA_NUMERICS_KV260 && c->cfg.head_dim != 64 && c->cfg.head_dim != 128)
+            if (value == GQA_NUMERICS_KV260 && ((c->cfg.head_dim != 64 && c->cfg.head_dim != 128) || c->paged))
                 return GQA_ERR_UNSUPPORTED;
             c->numerics = (int)value;
             return GQA_OK;
@@ -596,7 +687,77 @@ int gqa_cache_pointers(gqa_ctx* c, void** k, void** v, int32_t* l_cap) {
     if (!c) return GQA_ERR_NULL;
     if (k) *k = c->k_cache;
     if (v) *v = c->v_cache;
-    if (l_cap) *l_cap = c->l_cap;
+    if (l_cap) *l_cap = c->paged ? c->page_size : c->l_cap;
+    return GQA_OK;
+}
+
+// ---- paged cache management ------------------------------------------------------------
+
+int gqa_paged_reserve(gqa_ctx* c, int32_t b, int32_t n_rows) {
+    if (!c) return GQA_ERR_NULL;
+    if (!c->paged) return GQA_ERR_UNSUPPORTED;
+    if (b < 0 || b >= c->cfg.batch) return GQA_ERR_STREAM_DEST;
+    if (n_rows < 0 || n_rows > c->cfg.max_seq_len) return GQA_ERR_RANGE;
+    const int before = c->pages.mapped(b);
+    if (!c->pages.reserve(b, n_rows, c->page_size)) return GQA_ERR_OOM;
+    if (c->pages.mapped(b) == before) return GQA_OK;
+    HIP_TRY(hipSetDevice(c->cfg.device));
+    return upload_table_row(c, b);
+}
+
+int gqa_paged_release(gqa_ctx* c, int32_t b) {
+    if (!c) return GQA_ERR_NULL;
+    if (!c->paged) return GQA_ERR_UNSUPPORTED;
+    if (b < 0 || b >= c->cfg.batch) return GQA_ERR_STREAM_DEST;
+    int rc = txn_idle(c);
+    if (rc != GQA_OK) return rc;
+    HIP_TRY(hipSetDevice(c->cfg.device));
+    HIP_TRY(hipStreamSynchronize(c->stream));  // no launch on the context stream still reads the pages
+    c->pages.release(b);
+    return upload_table_row(c, b);
+}
+
+int gqa_paged_evict_lru(gqa_ctx* c, int32_t n_free_pages, const int32_t* pinned, int32_t n_pinned,
+                        int32_t* evicted, int32_t max_evicted, int32_t* n_evicted) {
+    if (!c || (n_pinned > 0 && !pinned)) return GQA_ERR_NULL;
+    if (!c->paged) return GQA_ERR_UNSUPPORTED;
+    if (n_free_pages < 0 || n_free_pages > c->n_pages || n_pinned < 0 || max_evicted < 0) return GQA_ERR_RANGE;
+    std::vector<char> pin(c->cfg.batch, 0);
+    for (int i = 0; i < n_pinned; ++i) {
+        if (pinned[i] < 0 || pinned[i] >= c->cfg.batch) return GQA_ERR_STREAM_DEST;
+        pin[pinned[i]] = 1;
+    }
+    int rc = txn_idle(c);
+    if (rc != GQA_OK) return rc;
+    HIP_TRY(hipSetDevice(c->cfg.device));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    std::vector<int> out;
+    if (!c->pages.evict_lru(n_free_pages, pin, &out)) return GQA_ERR_OOM;
+    for (int b : out) {
+        rc = upload_table_row(c, b);
+        if (rc != GQA_OK) return rc;
+    }
+    if (n_evicted) *n_evicted = (int32_t)out.size();
+    for (int i = 0; i < (int)out.size() && i < max_evicted && evicted; ++i) evicted[i] = out[i];
+    return GQA_OK;
+}
+
+int gqa_paged_info(gqa_ctx* c, int32_t* page_size, int32_t* n_pages, int32_t* n_free, int32_t* max_pages) {
+    if (!c) return GQA_ERR_NULL;
+    if (!c->paged) return GQA_ERR_UNSUPPORTED;
+    if (page_size) *page_size = c->page_size;
+    if (n_pages) *n_pages = c->n_pages;
+    if (n_free) *n_free = c->pages.free_pages();
+    if (max_pages) *max_pages = c->max_pages;
+    return GQA_OK;
+}
+
+int gqa_paged_table(gqa_ctx* c, int32_t b, int32_t* out, int32_t n) {
+    if (!c || !out) return GQA_ERR_NULL;
+    if (!c->paged) return GQA_ERR_UNSUPPORTED;
+    if (b < 0 || b >= c->cfg.batch) return GQA_ERR_STREAM_DEST;
+    if (n < 0 || n > c->max_pages) return GQA_ERR_RANGE;
+    memcpy(out, c->pages.row(b), (size_t)n * sizeof(int32_t));
     return GQA_OK;
 }
 
@@ -608,6 +769,14 @@ int gqa_load_kv(gqa_ctx* c, int32_t b, int32_t start_pos, int32_t n, const uint1
     if (rc != GQA_OK) return rc;
     if (n == 0) return GQA_OK;
     HIP_TRY(hipSetDevice(c->cfg.device));
+    if (c->paged) {
+        if (!rows_backed(c, b, start_pos, n)) return GQA_ERR_RANGE;
+        c->pages.touch(b);
+        HIP_TRY(hipEventRecord(c->ev_begin, c->stream));
+        rc = copy_rows_paged(c, b, start_pos, n, k, v, nullptr, nullptr, hipMemcpyHostToDevice, c->stream);
+        if (rc != GQA_OK) return rc;
+        return finish_sync(c);
+    }
     const size_t D = c->cfg.head_dim;
     const size_t row_bytes = D * 2;
     HIP_TRY(hipEventRecord(c->ev_begin, c->stream));
@@ -627,6 +796,12 @@ int gqa_load_kv_device(gqa_ctx* c, int32_t b, int32_t start_pos, int32_t n, cons
     if (n < 0 || start_pos < 0 || (int64_t)start_pos + n > c->cfg.max_seq_len) return GQA_ERR_RANGE;
     if (n == 0) return GQA_OK;
     hipStream_t s = pick_stream(c, stream);
+    if (c->paged) {
+        if (!rows_backed(c, b, start_pos, n)) return GQA_ERR_RANGE;
+        c->pages.touch(b);
+        return copy_rows_paged(c, b, start_pos, n, (const uint16_t*)k, (const uint16_t*)v, nullptr, nullptr,
+                               hipMemcpyDeviceToDevice, s);
+    }
     const size_t D = c->cfg.head_dim;
     const size_t pitch_dst = (size_t)c->l_cap * D * 2;   // bytes between kv heads in the cache
     const size_t pitch_src = (size_t)n * D * 2;          // bytes between kv heads in the source
@@ -646,6 +821,13 @@ int gqa_read_kv(gqa_ctx* c, int32_t b, int32_t start_pos, int32_t n, uint16_t* k
     if (rc != GQA_OK) return rc;
     if (n == 0) return GQA_OK;
     HIP_TRY(hipSetDevice(c->cfg.device));
+    if (c->paged) {
+        if (!rows_backed(c, b, start_pos, n)) return GQA_ERR_RANGE;
+        rc = copy_rows_paged(c, b, start_pos, n, nullptr, nullptr, k, v, hipMemcpyDeviceToHost, c->stream);
+        if (rc != GQA_OK) return rc;
+        HIP_TRY(hipStreamSynchronize(c->stream));
+        return GQA_OK;
+    }
     const size_t D = c->cfg.head_dim;
     for (int h = 0; h < c->cfg.n_kv_heads; ++h) {
         const size_t src = (((size_t)b * c->cfg.n_kv_heads + h) * c->l_cap + start_pos) * D;
@@ -659,8 +841,10 @@ int gqa_read_kv(gqa_ctx* c, int32_t b, int32_t start_pos, int32_t n, uint16_t* k
 
 int gqa_append_kv(gqa_ctx* c, const uint16_t* k_rows, const uint16_t* v_rows, const int32_t* positions) {
     if (!c || !k_rows || !v_rows || !positions) return GQA_ERR_NULL;
-    for (int b = 0; b < c->cfg.batch; ++b)
+    for (int b = 0; b < c->cfg.batch; ++b) {
         if (positions[b] < -1 || positions[b] >= c->cfg.max_seq_len) return GQA_ERR_RANGE;
+        if (positions[b] >= 0 && !rows_backed(c, b, positions[b], 1)) return GQA_ERR_RANGE;
+    }
     int rc = txn_idle(c);
     if (rc != GQA_OK) return rc;
     HIP_TRY(hipSetDevice(c->cfg.device));
@@ -681,7 +865,8 @@ int gqa_append_kv_device(gqa_ctx* c, const void* k_rows, const void* v_rows, con
     hipStream_t s = pick_stream(c, stream);
     timer_begin(c, GQA_TIMER_APPEND, s);
     HIP_TRY(launch_append((const uint16_t*)k_rows, (const uint16_t*)v_rows, positions, c->k_cache, c->v_cache,
-                          c->cfg.batch, c->cfg.n_kv_heads, c->cfg.head_dim, c->l_cap, c->cfg.max_seq_len, s));
+                          c->cfg.batch, c->cfg.n_kv_heads, c->cfg.head_dim, c->l_cap, c->cfg.max_seq_len,
+                          c->paged ? c->table_dev : nullptr, c->page_shift, c->max_pages, s));
     timer_end(c, GQA_TIMER_APPEND, s);
     return GQA_OK;
 }
@@ -691,11 +876,15 @@ int gqa_decode(gqa_ctx* c, const uint16_t* q, const int32_t* ctx_lens, uint16_t*
     int max_len = 0;
     for (int b = 0; b < c->cfg.batch; ++b) {
         if (ctx_lens[b] < 0 || ctx_lens[b] > c->cfg.max_seq_len) return GQA_ERR_RANGE;
+        if (!rows_backed(c, b, 0, ctx_lens[b])) return GQA_ERR_RANGE;
         if (ctx_lens[b] > max_len) max_len = ctx_lens[b];
     }
     int rc = txn_idle(c);
     if (rc != GQA_OK) return rc;
     HIP_TRY(hipSetDevice(c->cfg.device));
+    if (c->paged)
+        for (int b = 0; b < c->cfg.batch; ++b)
+            if (ctx_lens[b] > 0) c->pages.touch(b);
     const size_t qwords = (size_t)c->cfg.batch * c->cfg.n_q_heads * c->cfg.head_dim;
     HIP_TRY(hipEventRecord(c->ev_begin, c->stream));
     HIP_TRY(hipMemcpyAsync(c->q_dev, q, qwords * 2, hipMemcpyHostToDevice, c->stream));
@@ -722,11 +911,16 @@ int gqa_decode_append(gqa_ctx* c, const uint16_t* q, const uint16_t* k_rows, con
     for (int b = 0; b < c->cfg.batch; ++b) {
         if (ctx_lens[b] < 0 || ctx_lens[b] > c->cfg.max_seq_len) return GQA_ERR_RANGE;
         if (positions[b] < -1 || positions[b] >= c->cfg.max_seq_len) return GQA_ERR_RANGE;
+        if (!rows_backed(c, b, 0, ctx_lens[b]) || (positions[b] >= 0 && !rows_backed(c, b, positions[b], 1)))
+            return GQA_ERR_RANGE;
         if (ctx_lens[b] > max_len) max_len = ctx_lens[b];
     }
     int rc = txn_idle(c);
     if (rc != GQA_OK) return rc;
     HIP_TRY(hipSetDevice(c->cfg.device));
+    if (c->paged)
+        for (int b = 0; b < c->cfg.batch; ++b)
+            if (ctx_lens[b] > 0 || positions[b] >= 0) c->pages.touch(b);
     const size_t qwords = (size_t)c->cfg.batch * c->cfg.n_q_heads * c->cfg.head_dim;
     const size_t row_words = (size_t)c->cfg.batch * c->cfg.n_kv_heads * c->cfg.head_dim;
     const size_t i32 = (size_t)c->cfg.batch * sizeof(int32_t);
@@ -758,6 +952,7 @@ int gqa_prefill(gqa_ctx* c, int32_t b, const uint16_t* q, int32_t q_len, int32_t
     if (!c || !q || !o) return GQA_ERR_NULL;
     int rc = check_prefill_args(c, b, q_len, q_pos_base, kv_len, kv_pos_base);
     if (rc != GQA_OK) return rc;
+    if (!rows_backed(c, b, 0, kv_len)) return GQA_ERR_RANGE;
     rc = txn_idle(c);
     if (rc != GQA_OK) return rc;
     HIP_TRY(hipSetDevice(c->cfg.device));
@@ -780,6 +975,7 @@ int gqa_prefill_append(gqa_ctx* c, int32_t b, const uint16_t* q, const uint16_t*
     if (!c || !q || !k_rows || !v_rows || !o) return GQA_ERR_NULL;
     int rc = check_prefill_args(c, b, q_len, q_pos_base, kv_len, kv_pos_base);
     if (rc != GQA_OK) return rc;
+    if (!rows_backed(c, b, 0, kv_len)) return GQA_ERR_RANGE;
     if (n_new < 1 || n_new > kv_len || n_new > c->cfg.max_q_len) return GQA_ERR_RANGE;
     rc = txn_idle(c);
     if (rc != GQA_OK) return rc;
@@ -806,6 +1002,7 @@ int gqa_prefill_append_device(gqa_ctx* c, int32_t b, const void* q, const void* 
     if (!c || !q || !k_rows || !v_rows || !o) return GQA_ERR_NULL;
     int rc = check_prefill_args(c, b, q_len, q_pos_base, kv_len, kv_pos_base);
     if (rc != GQA_OK) return rc;
+    if (!rows_backed(c, b, 0, kv_len)) return GQA_ERR_RANGE;
     if (n_new < 1 || n_new > kv_len) return GQA_ERR_RANGE;
     return run_prefill(c, b, q, q_len, q_pos_base, kv_len, kv_pos_base, causal, o, lse, pick_stream(c, stream),
                        k_rows, v_rows, n_new);
@@ -816,6 +1013,7 @@ int gqa_prefill_device(gqa_ctx* c, int32_t b, const void* q, int32_t q_len, int3
     if (!c || !q || !o) return GQA_ERR_NULL;
     int rc = check_prefill_args(c, b, q_len, q_pos_base, kv_len, kv_pos_base);
     if (rc != GQA_OK) return rc;
+    if (!rows_backed(c, b, 0, kv_len)) return GQA_ERR_RANGE;
     return run_prefill(c, b, q, q_len, q_pos_base, kv_len, kv_pos_base, causal, o, lse, pick_stream(c, stream));
 }
 
@@ -828,6 +1026,7 @@ int gqa_submit(gqa_ctx* c, int32_t b, const uint16_t* q, int32_t q_len, int32_t 
     if (rc != GQA_OK) return rc;
     rc = check_prefill_args(c, b, q_len, q_pos_base, kv_len, kv_pos_base);
     if (rc != GQA_OK) return rc;
+    if (!rows_backed(c, b, 0, kv_len)) return GQA_ERR_RANGE;
     if (!prefill_supported(c->cfg.head_dim, c->group)) return GQA_ERR_UNSUPPORTED;
     HIP_TRY(hipSetDevice(c->cfg.device));
     c->txn = Txn();
@@ -854,6 +1053,7 @@ int gqa_layer_qkv_device(gqa_ctx* c, int32_t b, const void* x, int32_t n_tokens,
     if (rc != GQA_OK) return rc;
     rc = check_layer_args(c, b, n_tokens, hidden, q_pos_base, kv_pos_base, kv_row0);
     if (rc != GQA_OK) return rc;
+    if (!rows_backed(c, b, kv_row0, n_tokens)) return GQA_ERR_RANGE;
     if (!(rms_eps >= 0.f) || !isfinite(rms_eps)) return GQA_ERR_RANGE;
     HIP_TRY(hipSetDevice(c->cfg.device));
     return run_layer_qkv(c, b, x, n_tokens, hidden, wq, wk, wv, rms_weight, rms_eps, q_pos_base, kv_pos_base, kv_row0,
@@ -870,6 +1070,7 @@ int gqa_submit_layer(gqa_ctx* c, int32_t b, const uint16_t* x, int32_t n_tokens,
     if (rc != GQA_OK) return rc;
     rc = check_prefill_args(c, b, n_tokens, q_pos_base, n_tokens, kv_pos_base);
     if (rc != GQA_OK) return rc;
+    if (!rows_backed(c, b, 0, n_tokens)) return GQA_ERR_RANGE;
     if (!(rms_eps >= 0.f) || !isfinite(rms_eps)) return GQA_ERR_RANGE;
     if (!prefill_supported(c->cfg.head_dim, c->group)) return GQA_ERR_UNSUPPORTED;
     HIP_TRY(hipSetDevice(c->cfg.device));

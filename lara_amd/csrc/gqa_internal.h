@@ -28,6 +28,13 @@ struct DecodeArgs {
     float* part_ml;         // [B*H_kv][max_splits][G][2] (running max in log2 units, sum)
     uint16_t* out;          // [B][H_q][D] bf16
     float* lse;             // [B][H_q] natural-log LSE, or nullptr
+    // Paged cache (block_table != nullptr): kc/vc are the page pools [n_pages][H_kv][P][D] and
+    // row t of (b, h) is row t % P of page block_table[b * max_pages + t / P] (P = 2^page_shift,
+    // a multiple of 64); rows of an unmapped page (-1) read as zero_row and are never written.
+    const int32_t* block_table;
+    int32_t page_shift;
+    int32_t max_pages;
+    const uint16_t* zero_row;
 };
 
 // Chunked prefill / full-transaction launch description (one sequence b).
@@ -55,7 +62,20 @@ struct PrefillArgs {
     float* part_o;          // [n_segs][H_q][q_len][D] fp32 un-normalised partial O
     float* part_ml;         // [n_segs][H_q][q_len][2] (running max in log2 units, sum)
     const uint16_t* zero_row;  // >= D zero words: the source of K/V rows past kv_len
+    // Paged cache: block_table is sequence b's row of page indices (-1 = unmapped, read as
+    // zero_row, never written), kc/vc the pools [n_pages][H_kv][2^page_shift][D]; nullptr =
+    // contiguous cache of sequence b as above.
+    const int32_t* block_table;
+    int32_t page_shift;
 };
+
+// Row index (in units of D elements) of token row t of (sequence-relative) kv head h in a paged
+// pool, or -1 when its page is unmapped.
+__device__ __forceinline__ int64_t paged_row(const int32_t* table_row, int page_shift, int n_kv_heads, int h, int t) {
+    const int page = table_row[t >> page_shift];
+    if (page < 0) return -1;
+    return (((int64_t)page * n_kv_heads + h) << page_shift) + (t & ((1 << page_shift) - 1));
+}
 
 // KV segmentation of a prefill launch: (seg_len, n_segs) for q_len query rows whose
 // attended key span is kv_span, sized so the launch has about target_wgs work-groups.
@@ -99,10 +119,12 @@ hipError_t launch_prefill(int head_dim, int group, const PrefillArgs& a, hipStre
 // Merges the KV segments of a prefill launch with n_segs > 1.
 hipError_t launch_prefill_combine(int head_dim, const PrefillArgs& a, hipStream_t s);
 
-// K/V row append: rows [B][H_kv][D] -> cache row positions[b] (skipped if < 0 or >= l_max).
+// K/V row append: rows [B][H_kv][D] -> cache row positions[b] (skipped if < 0 or >= l_max, or,
+// in a paged cache (block_table != nullptr, [B][max_pages]), if the row's page is unmapped).
 hipError_t launch_append(const uint16_t* k_rows, const uint16_t* v_rows, const int32_t* positions,
                          uint16_t* kc, uint16_t* vc, int batch, int n_kv_heads, int head_dim,
-                         int l_cap, int l_max, hipStream_t s);
+                         int l_cap, int l_max, const int32_t* block_table, int page_shift, int max_pages,
+                         hipStream_t s);
 
 // Layer input stage of run_layer (sw/attn_driver.py:552-576): RMSNorm of the hidden states
 // and, after the QKV projection GEMM, RoPE plus the head-major scatter of Q and of K/V into
@@ -124,8 +146,10 @@ struct RopeArgs {
     int q_pos_base, kv_pos_base, rope;
     uint16_t* q_out;       // [n_q_heads][n_tokens][D]
     uint16_t* kc;          // cache of one sequence: [n_kv_heads][l_cap][D], rows row0 ..
-    uint16_t* vc;
+    uint16_t* vc;          //   (paged: the pools, addressed through block_table)
     int l_cap, row0;
+    const int32_t* block_table;  // paged: the sequence's page indices; nullptr = contiguous
+    int page_shift;
     float theta[kMaxRopePairs];  // rotation frequency of pair (2p, 2p+1)
 };
 hipError_t launch_rope_scatter(const RopeArgs& a, hipStream_t s);

@@ -147,7 +147,12 @@ __global__ __launch_bounds__(kMaxRopePairs) void rope_scatter_kernel(RopeArgs a)
             dst = a.q_out + ((size_t)h * a.n_tokens + t) * D;
         } else {
             const int g = is_k ? h - a.n_q_heads : h - a.n_q_heads - a.n_kv_heads;
-            dst = (is_k ? a.kc : a.vc) + ((size_t)g * a.l_cap + a.row0 + t) * D;
+            int64_t r = (int64_t)g * a.l_cap + a.row0 + t;
+            if (a.block_table != nullptr) {
+                r = paged_row(a.block_table, a.page_shift, a.n_kv_heads, g, a.row0 + t);
+                if (r < 0) continue;  // unmapped page: nothing to write
+            }
+            dst = (is_k ? a.kc : a.vc) + (size_t)r * D;
         }
         *(uint32_t*)(dst + 2 * p) = out;
     }

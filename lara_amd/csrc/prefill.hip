@@ -115,7 +115,7 @@ __device__ __forceinline__ int v_swz(int key) {
 // addresses key (lane%16)/4 of the four, dims d_g + 4*(lane%4) .. +3, and receives one dim of
 // four keys.
 
-template <int D, int G>
+template <int D, int G, bool PAGED>
 __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
     constexpr int NCH = D / 8;                   // 16-byte chunks per K/V row
     constexpr int KSTEPS = D / 16;               // QK k-steps
@@ -155,12 +155,22 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
     if (has_new && blockIdx.x == 0) {
         const u32x4* ks = reinterpret_cast<const u32x4*>(a.k_new) + (size_t)h * a.n_new * NCH;
         const u32x4* vs = reinterpret_cast<const u32x4*>(a.v_new) + (size_t)h * a.n_new * NCH;
-        u32x4* kd = reinterpret_cast<u32x4*>(a.kc + ((size_t)h * a.l_cap + a.new_begin) * D);
-        u32x4* vd = reinterpret_cast<u32x4*>(a.vc + ((size_t)h * a.l_cap + a.new_begin) * D);
         const int words = a.n_new * NCH;
-        for (int i = blockIdx.z * (kWaves * 64) + tid; i < words; i += gridDim.z * (kWaves * 64)) {
-            kd[i] = ks[i];
-            vd[i] = vs[i];
+        if constexpr (PAGED) {
+            for (int i = blockIdx.z * (kWaves * 64) + tid; i < words; i += gridDim.z * (kWaves * 64)) {
+                const int64_t r = paged_row(a.block_table, a.page_shift, a.n_kv_heads, h, a.new_begin + i / NCH);
+                if (r < 0) continue;  // unmapped page: nothing to write
+                const size_t dst = (size_t)r * NCH + (i % NCH);
+                reinterpret_cast<u32x4*>(a.kc)[dst] = ks[i];
+                reinterpret_cast<u32x4*>(a.vc)[dst] = vs[i];
+            }
+        } else {
+            u32x4* kd = reinterpret_cast<u32x4*>(a.kc + ((size_t)h * a.l_cap + a.new_begin) * D);
+            u32x4* vd = reinterpret_cast<u32x4*>(a.vc + ((size_t)h * a.l_cap + a.new_begin) * D);
+            for (int i = blockIdx.z * (kWaves * 64) + tid; i < words; i += gridDim.z * (kWaves * 64)) {
+                kd[i] = ks[i];
+                vd[i] = vs[i];
+            }
         }
     }
     const int last_task = min(n_tasks, (int)(blockIdx.x + 1) * kWaves) - 1;
@@ -198,8 +208,8 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
     float m_run = -INFINITY;  // running max (log2 units) of this lane's row
     float l_lane = 0.f;       // this lane's half of the running sum
 
-    const u32x4* kg = reinterpret_cast<const u32x4*>(a.kc + (size_t)h * a.l_cap * D);
-    const u32x4* vg = reinterpret_cast<const u32x4*>(a.vc + (size_t)h * a.l_cap * D);
+    const u32x4* kg = reinterpret_cast<const u32x4*>(a.kc + (PAGED ? 0 : (size_t)h * a.l_cap * D));
+    const u32x4* vg = reinterpret_cast<const u32x4*>(a.vc + (PAGED ? 0 : (size_t)h * a.l_cap * D));
     const u32x4* kn = has_new ? reinterpret_cast<const u32x4*>(a.k_new) + (size_t)h * a.n_new * NCH : nullptr;
     const u32x4* vn = has_new ? reinterpret_cast<const u32x4*>(a.v_new) + (size_t)h * a.n_new * NCH : nullptr;
     const u32x4* zero = reinterpret_cast<const u32x4*>(a.zero_row);
@@ -220,11 +230,28 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
     auto issue = [&](int j0, int st) {
         const bool special = (j0 + kBN > a.kv_len) ||
                              (has_new && j0 + kBN > a.new_begin && j0 < a.new_begin + a.n_new);
+        // Row j0's first word and the row stride; a paged block (j0 and the page size are
+        // multiples of 64) lies in one page, looked up once (stride 0: unmapped, zero row).
+        const u32x4* kb0 = kg;
+        const u32x4* vb0 = vg;
+        int stride = NCH;
+        if constexpr (PAGED) {
+            const int64_t pr = paged_row(a.block_table, a.page_shift, a.n_kv_heads, h, j0);
+            if (pr < 0) {
+                kb0 = zero;
+                vb0 = zero;
+                stride = 0;
+            } else {
+                kb0 = kg + (size_t)pr * NCH;
+                vb0 = vg + (size_t)pr * NCH;
+            }
+        }
 #pragma unroll
         for (int i = 0; i < DMA; ++i) {
             const int row_idx = j0 + sl_key[i];
-            const u32x4* sk = kg + (size_t)row_idx * NCH + sl_ck[i];
-            const u32x4* sv = vg + (size_t)row_idx * NCH + sl_cv[i];
+            const size_t roff = PAGED ? (size_t)sl_key[i] * stride : (size_t)row_idx * NCH;
+            const u32x4* sk = kb0 + roff + sl_ck[i];
+            const u32x4* sv = vb0 + roff + sl_cv[i];
             if (special) {
                 const unsigned r_new = (unsigned)(row_idx - a.new_begin);
                 if (row_idx >= a.kv_len) {
@@ -454,7 +481,10 @@ hipError_t launch_prefill_t(const PrefillArgs& a, hipStream_t s) {
     const int n_rb = (a.q_len + kRows - 1) / kRows;
     const int n_tasks = n_rb * G;
     dim3 grid((n_tasks + kWaves - 1) / kWaves, a.n_kv_heads, a.n_segs);
-    hipLaunchKernelGGL((prefill_kernel<D, G>), grid, dim3(kWaves * 64), 0, s, a);
+    if (a.block_table != nullptr)
+        hipLaunchKernelGGL((prefill_kernel<D, G, true>), grid, dim3(kWaves * 64), 0, s, a);
+    else
+        hipLaunchKernelGGL((prefill_kernel<D, G, false>), grid, dim3(kWaves * 64), 0, s, a);
     return hipGetLastError();
 }
 
