@@ -47,7 +47,7 @@ def log(msg: str) -> None:
 class DecodeBench:
     """Owns one libgqa context and HBM-resident inputs for a decode workload."""
 
-    def __init__(self, w, device: int = 0, chunk: int = 0):
+    def __init__(self, w, device: int = 0, chunk: int = 0, page_size: int = 0):
         import torch
         from lara_amd import _lib
 
@@ -59,7 +59,19 @@ class DecodeBench:
         L = int(self.lens.max())
         cfg = _lib.GqaConfig(w.batch, w.n_q_heads, w.n_kv_heads, w.head_dim, L, 1, float(w.scale or 0.0), device)
         self.ctx = ctypes.c_void_p()
-        _lib.check(self.lib.gqa_create(ctypes.byref(cfg), ctypes.byref(self.ctx)), "gqa_create")
+        if page_size:
+            # Paged cache: pages handed out round robin, one page per sequence in turn, so every
+            # sequence's rows are scattered over the pool.
+            pages = [-(-int(n) // page_size) for n in self.lens]
+            _lib.check(self.lib.gqa_create_paged(ctypes.byref(cfg), page_size, sum(pages), ctypes.byref(self.ctx)),
+                       "gqa_create_paged")
+            for p in range(1, max(pages) + 1):
+                for b in range(w.batch):
+                    if p <= pages[b]:
+                        _lib.check(self.lib.gqa_paged_reserve(self.ctx, b, min(int(self.lens[b]), p * page_size)),
+                                   "reserve")
+        else:
+            _lib.check(self.lib.gqa_create(ctypes.byref(cfg), ctypes.byref(self.ctx)), "gqa_create")
         if chunk:
             _lib.check(self.lib.gqa_set_option(self.ctx, _lib.GQA_OPT_DECODE_CHUNK, chunk), "chunk")
         dev = torch.device("cuda", device)
@@ -135,12 +147,17 @@ class DecodeBench:
         self.ctx = ctypes.c_void_p()
 
 
+PAGED_SUFFIX = "_paged"  # a decode workload over a paged cache of 64-row pages
+PAGE_ROWS = 64
+
+
 def measure(name: str, steps: int, warmup: int, chunk: int = 0) -> dict:
     from lara_amd.benchmark import WORKLOADS, decode_kernel_bytes, decode_step_bytes, HBM_PEAK_GBPS
 
-    w = WORKLOADS[name]
+    paged = name.endswith(PAGED_SUFFIX)
+    w = WORKLOADS[name[: -len(PAGED_SUFFIX)] if paged else name]
     log(f"{name}: filling HBM cache")
-    bench = DecodeBench(w, chunk=chunk)
+    bench = DecodeBench(w, chunk=chunk, page_size=PAGE_ROWS if paged else 0)
     try:
         log(f"{name}: warmup {warmup}, timing {steps} steps")
         r = bench.run(steps, warmup)
@@ -617,7 +634,7 @@ def main() -> int:
     parser.add_argument("--chunk", type=int, default=0, help="keys per split-KV work-group (0 = auto)")
     parser.add_argument("--prefill-wgs", type=int, default=0,
                         help="work-groups the prefill KV segmentation aims for (0 = auto, 1 = no segments)")
-    parser.add_argument("--others", default="c2,c3,c4,c5,layer", help="extra decode workloads to report ('' = none)")
+    parser.add_argument("--others", default="c2,c3,c4,c5,layer,ns_paged", help="extra decode workloads to report ('' = none)")
     parser.add_argument("--cpu-seconds", type=float, default=12.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--calibrate-copy-mib", type=int, default=0,

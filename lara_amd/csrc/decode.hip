@@ -195,10 +195,24 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
         const u32x4* v;
         int stride;
     };
+    // Paged: 64 consecutive block-table entries of the sequence, one per lane, from page
+    // pc_first on; a round reads its page with v_readlane (no memory access and no wait), and
+    // the window moves once every 64 pages.
+    int pc_first = -(1 << 30), pc_val = -1;
+    auto page_of = [&](int page_idx) -> int {  // page_idx is wave-uniform
+        if (page_idx - pc_first >= 64 || page_idx < pc_first) {
+            pc_first = page_idx;
+            const int i = page_idx + lane;
+            pc_val = i < a.max_pages ? trow[i] : -1;
+        }
+        return __builtin_amdgcn_readlane(pc_val, page_idx - pc_first);
+    };
     auto round_src = [&](int key0) -> RoundSrc {
         if constexpr (PAGED) {
-            const int64_t r = paged_row(trow, a.page_shift, a.n_kv_heads, h, __builtin_amdgcn_readfirstlane(key0));
-            if (r < 0) return {zero, zero, 0};
+            const int k0 = __builtin_amdgcn_readfirstlane(key0);
+            const int page = page_of(k0 >> a.page_shift);
+            if (page < 0) return {zero, zero, 0};
+            const int64_t r = (((int64_t)page * a.n_kv_heads + h) << a.page_shift) + (k0 & ((1 << a.page_shift) - 1));
             return {kbase + (size_t)r * NCH, vbase + (size_t)r * NCH, NCH};
         } else {
             return {kbase + (size_t)key0 * NCH, vbase + (size_t)key0 * NCH, NCH};
