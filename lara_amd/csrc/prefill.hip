@@ -36,6 +36,8 @@
 // the S^T result leaves them, and V^T is stored in LDS with the matching key order.
 #include "gqa_internal.h"
 
+#include <type_traits>
+
 #include <math.h>
 
 namespace lara {
@@ -91,6 +93,43 @@ __device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_addr) {
                  : "memory", "m0");
 }
 #pragma clang diagnostic pop
+
+// 16-byte LDS read issued from inline assembly, so it stays where it is written: the
+// compiler's scheduler, short of registers, would otherwise move every read next to its use
+// and make each MFMA wait for its own read.  The result is valid only after lgkm_wait.
+__device__ __forceinline__ u32x4 lds_read128(uint32_t addr) {
+    u32x4 v;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr) : "memory");
+    return v;
+}
+
+// s_waitcnt lgkmcnt(N) (vm and export counters untouched) that the compiler sees as
+// producing a and b, so no use of them can move above it.  Only this kernel's own LDS reads
+// are outstanding when it is used (the stage DMA counts on vmcnt).
+template <int N, typename T>
+__device__ __forceinline__ void lgkm_wait(T& a, T& b) {
+    static_assert(N >= 0 && N < 16, "lgkmcnt range");
+    asm volatile("s_waitcnt %2" : "+v"(a), "+v"(b) : "i"(0xF | (0x3 << 14) | (0x7 << 4) | (N << 8)));
+}
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Calls f(std::integral_constant<int, i>) for i = 0 .. N-1 (compile-time indices).
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<N, I + 1>(f);
+    }
+}
+
+// Transposing 8-byte LDS read (ds_read_b64_tr_b16) from inline assembly, at addr + OFF.
+template <int OFF>
+__device__ __forceinline__ u32x2 lds_read_tr64(uint32_t addr) {
+    u32x2 v;
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF) : "memory");
+    return v;
+}
 
 // Work-group barrier for the stage ring: LDS traffic is ordered by the explicit waits, so no
 // memory fence (which would wait for every load in flight) is attached.
@@ -314,14 +353,26 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
             for (int i = 0; i < 16; ++i) sacc[kt][i] = 0.f;
+        // K fragments are double-buffered: step ks+1's LDS reads are in flight while step ks's
+        // MFMAs run, so no MFMA waits for the read it consumes.
+        // Fully unrolled, every fragment is its own value: none is copied while its read is in
+        // flight.
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // nothing else outstanding on lgkm
+        constexpr uint32_t kKt = 32 * NCH * 16;                  // bytes between the two key tiles
+        u32x4 kf[KSTEPS][2];
+        kf[0][0] = lds_read128(kaddr[0] + stage_off);
+        kf[0][1] = lds_read128(kaddr[0] + stage_off + kKt);
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks) {
-            const uint32_t ka = kaddr[ks] + stage_off;
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt) {
-                const u32x4 kw = *(const __attribute__((address_space(3))) u32x4*)(uintptr_t)(ka + kt * 32 * NCH * 16);
-                sacc[kt] = mfma32(kw, qb[ks], sacc[kt]);
+            if (ks + 1 < KSTEPS) {
+                kf[ks + 1][0] = lds_read128(kaddr[ks + 1] + stage_off);
+                kf[ks + 1][1] = lds_read128(kaddr[ks + 1] + stage_off + kKt);
+                lgkm_wait<2>(kf[ks][0], kf[ks][1]);
+            } else {
+                lgkm_wait<0>(kf[ks][0], kf[ks][1]);
             }
+            sacc[0] = mfma32(kf[ks][0], qb[ks], sacc[0]);
+            sacc[1] = mfma32(kf[ks][1], qb[ks], sacc[1]);
         }
 
         // ---- online softmax (log2 domain, scale folded into the exponent) ----
@@ -379,24 +430,30 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
         l_lane += psum;
 
         // ---- O^T += V^T . P^T ----
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-            const uint32_t va = vaddr[mt] + stage_off;
-#pragma unroll
-            for (int st_i = 0; st_i < 4; ++st_i) {
-                const int kb = 32 * (st_i >> 1) + 16 * (st_i & 1);  // step's key base (half adds 4)
-                u32x4 vw;
-#pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                    const v4i16_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (__attribute__((address_space(3))) v4i16_t*)(uintptr_t)(va + (uint32_t)((kb + 8 * e) * (D * 2))));
-                    const uint2 w = __builtin_bit_cast(uint2, r);
-                    vw[2 * e] = w.x;
-                    vw[2 * e + 1] = w.y;
-                }
-                o[mt] = mfma32(vw, pb[st_i], o[mt]);
+        // Step i = (mt, st_i): the two transposing reads of step i+1 are issued before step i's
+        // MFMA, as in the S^T phase.
+        constexpr int PV = MT * 4;
+        u32x2 vf[PV][2];
+        auto read_v = [&](auto step_c) {
+            constexpr int i = decltype(step_c)::value;
+            constexpr int st_i = i % 4;
+            constexpr int kb = 32 * (st_i >> 1) + 16 * (st_i & 1);  // step's key base (half adds 4)
+            const uint32_t va = vaddr[i / 4] + stage_off;
+            vf[i][0] = lds_read_tr64<kb * (D * 2)>(va);
+            vf[i][1] = lds_read_tr64<(kb + 8) * (D * 2)>(va);
+        };
+        read_v(std::integral_constant<int, 0>{});
+        static_for<PV>([&](auto step_c) {
+            constexpr int i = decltype(step_c)::value;
+            if constexpr (i + 1 < PV) {
+                read_v(std::integral_constant<int, i + 1>{});
+                lgkm_wait<2>(vf[i][0], vf[i][1]);
+            } else {
+                lgkm_wait<0>(vf[i][0], vf[i][1]);
             }
-        }
+            const u32x4 vw = {vf[i][0].x, vf[i][0].y, vf[i][1].x, vf[i][1].y};
+            o[i / 4] = mfma32(vw, pb[i % 4], o[i / 4]);
+        });
     }
 
     if (!row_ok) return;
