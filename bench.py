@@ -290,7 +290,7 @@ class LayerBench:
     """run_layer on the device: RMSNorm -> QKV GEMM -> RoPE/scatter (gqa_layer_qkv_device), then
     causal attention of the whole prompt (gqa_prefill_device)."""
 
-    def __init__(self, w, device: int = 0):
+    def __init__(self, w, device: int = 0, target_wgs: int = 0):
         import torch
         from lara_amd import _lib
 
@@ -301,6 +301,8 @@ class LayerBench:
         cfg = _lib.GqaConfig(1, w.n_q_heads, w.n_kv_heads, w.head_dim, w.tokens, w.tokens, 0.0, device)
         self.ctx = ctypes.c_void_p()
         _lib.check(self.lib.gqa_create(ctypes.byref(cfg), ctypes.byref(self.ctx)), "gqa_create")
+        if target_wgs:
+            _lib.check(self.lib.gqa_set_option(self.ctx, _lib.GQA_OPT_PREFILL_WGS, target_wgs), "prefill wgs")
         dev = torch.device("cuda", device)
         self.sptr = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
         g = torch.Generator(device=dev)
@@ -359,13 +361,13 @@ class LayerBench:
         self.lib.gqa_destroy(self.ctx)
 
 
-def measure_layer(name: str, steps: int, warmup: int) -> dict:
+def measure_layer(name: str, steps: int, warmup: int, target_wgs: int = 0) -> dict:
     from lara_amd.benchmark import BF16_DENSE_TFLOPS, LAYER_WORKLOADS, layer_projection_flops, prefill_flops, \
         valid_pairs
 
     w = LAYER_WORKLOADS[name]
     log(f"{name}: layer set-up")
-    bench = LayerBench(w)
+    bench = LayerBench(w, target_wgs=target_wgs)
     try:
         r = bench.run(steps, warmup)
     finally:
@@ -680,7 +682,7 @@ def main() -> int:
             others[name] = measure_prefill(name, max(10, args.steps // 2), max(2, args.warmup // 2), args.prefill_wgs)
             continue
         if name == "layer":
-            others[name] = measure_layer(name, max(10, args.steps // 4), max(2, args.warmup // 2))
+            others[name] = measure_layer(name, max(10, args.steps // 4), max(2, args.warmup // 2), args.prefill_wgs)
             continue
         r = measure(name, max(10, args.steps // 2), max(2, args.warmup // 2))
         others[name] = {k: r[k] for k in ("us_per_step", "step_gbps", "step_frac_of_peak", "decode_us",

@@ -443,6 +443,20 @@ int layer_times(gqa_ctx* c) {
     return GQA_OK;
 }
 
+// Largest segmented-plan workspace (floats) over every query length up to max_q_len, keys up
+// to max_seq_len, for a work-group target.
+size_t prefill_workspace_need(const gqa_ctx* c, int target_wgs) {
+    const gqa_config& k = c->cfg;
+    size_t need = 0;
+    for (int q_len = 32; q_len < k.max_q_len + 32; q_len += 32) {
+        const int ql = q_len < k.max_q_len ? q_len : k.max_q_len;
+        const PrefillPlan p = plan_prefill(ql, k.max_seq_len, c->group, k.n_kv_heads, target_wgs, kMaxPrefillSegs);
+        const size_t f = prefill_workspace_floats(p, ql, k.n_q_heads, k.head_dim);
+        if (f > need) need = f;
+    }
+    return need;
+}
+
 int create_ctx(const gqa_config* cfg, int32_t page_size, int32_t n_pages, gqa_ctx** out_ctx) {
     if (!cfg || !out_ctx) return GQA_ERR_NULL;
     *out_ctx = nullptr;
@@ -492,13 +506,7 @@ int create_ctx(const gqa_config* cfg, int32_t page_size, int32_t n_pages, gqa_ct
     alloc((void**)&c->part_o, units * c->max_splits_cap * group * D * sizeof(float));
     alloc((void**)&c->part_ml, units * c->max_splits_cap * group * 2 * sizeof(float));
     if (prefill_supported(k.head_dim, group)) {
-        // Largest segmented plan over every query length up to max_q_len (keys up to L_max).
-        for (int q_len = 32; q_len < k.max_q_len + 32; q_len += 32) {
-            const int ql = q_len < k.max_q_len ? q_len : k.max_q_len;
-            const PrefillPlan p = plan_prefill(ql, k.max_seq_len, group, k.n_kv_heads, kTargetPrefillWgs, kMaxPrefillSegs);
-            const size_t f = prefill_workspace_floats(p, ql, k.n_q_heads, k.head_dim);
-            if (f > c->pre_ws_floats) c->pre_ws_floats = f;
-        }
+        c->pre_ws_floats = prefill_workspace_need(c, kTargetPrefillWgs);
         if (c->pre_ws_floats > 0) alloc((void**)&c->pre_ws, c->pre_ws_floats * sizeof(float));
     }
     alloc((void**)&c->q_dev, c->stage_words * 2);
@@ -674,10 +682,28 @@ int gqa_set_option(gqa_ctx* c, int32_t option, int64_t value) {
                 return GQA_ERR_UNSUPPORTED;
             c->numerics = (int)value;
             return GQA_OK;
-        case GQA_OPT_PREFILL_WGS:
+        case GQA_OPT_PREFILL_WGS: {
             if (value < 0 || value > (1 << 20)) return GQA_ERR_RANGE;
+            if (!prefill_supported(c->cfg.head_dim, c->group)) {
+                c->prefill_wgs_opt = (int)value;
+                return GQA_OK;
+            }
+            // Grow the segment workspace for the new target (kept if it already suffices).
+            const size_t need = prefill_workspace_need(c, value > 0 ? (int)value : kTargetPrefillWgs);
+            if (need > c->pre_ws_floats) {
+                int rc = txn_idle(c);
+                if (rc != GQA_OK) return rc;
+                HIP_TRY(hipSetDevice(c->cfg.device));
+                HIP_TRY(hipDeviceSynchronize());
+                float* ws = nullptr;
+                if (hipMalloc(&ws, need * sizeof(float)) != hipSuccess) return GQA_ERR_OOM;
+                (void)hipFree(c->pre_ws);
+                c->pre_ws = ws;
+                c->pre_ws_floats = need;
+            }
             c->prefill_wgs_opt = (int)value;
             return GQA_OK;
+        }
         default:
             return GQA_ERR_BAD_CFG;
     }

@@ -173,7 +173,10 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
     const int h = blockIdx.y;  // kv head
     const int n_rb = (a.q_len + kRows - 1) / kRows;
     const int n_tasks = n_rb * G;
-    const int task = blockIdx.x * kWaves + wave;
+    // Causal row blocks grow in work with their index: the largest go to the work-groups the
+    // dispatcher starts first (longest first), so a grid larger than the GPU balances.
+    const int wg_x = a.causal ? (int)(gridDim.x - 1 - blockIdx.x) : (int)blockIdx.x;
+    const int task = wg_x * kWaves + wave;
     const bool active = task < n_tasks;
     const int g = task % G;
     const int rb = task / G;
@@ -212,7 +215,7 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
             }
         }
     }
-    const int last_task = min(n_tasks, (int)(blockIdx.x + 1) * kWaves) - 1;
+    const int last_task = min(n_tasks, (wg_x + 1) * kWaves) - 1;
     const int wg_hi = kv_limit(last_task / G);  // row blocks grow with the task index
     const int wave_hi = active ? kv_limit(rb) : 0;
     const int seg_begin = blockIdx.z * a.seg_len;
