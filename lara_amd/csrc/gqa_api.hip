@@ -20,7 +20,7 @@ namespace {
 constexpr int kMinChunk = 256;     // smallest split (keys); multiple of every decode round size
 constexpr int kTargetPrefillWgs = kPrefillTargetWgs;
 constexpr int kMaxPrefillSegs = 16;
-constexpr int kTargetDecodeWgs = 512;  // 2 per CU: one split per (sequence, kv head) once that fills the GPU
+constexpr int kTargetDecodeWaves = 2048;  // 8 waves per CU; one split per (sequence, kv head) once that fills the GPU
 
 struct Txn {
     int valid = 0;     // a transaction has been submitted (configure + Q staged)
@@ -124,7 +124,8 @@ hipStream_t pick_stream(gqa_ctx* c, void* s) { return s ? (hipStream_t)s : c->st
 int choose_chunk(const gqa_ctx* c, int max_len) {
     if (c->chunk_opt > 0) return c->chunk_opt;
     const int units = c->cfg.batch * c->cfg.n_kv_heads;
-    int splits = (kTargetDecodeWgs + units - 1) / units;
+    const int target_wgs = kTargetDecodeWaves / decode_waves(c->group);
+    int splits = (target_wgs + units - 1) / units;
     if (splits < 1) splits = 1;
     int chunk = (max_len + splits - 1) / splits;
     chunk = ((chunk + kMinChunk - 1) / kMinChunk) * kMinChunk;

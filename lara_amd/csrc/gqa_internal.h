@@ -109,6 +109,8 @@ struct RtlArgs {
 hipError_t launch_rtl_transaction(int head_dim, const RtlArgs& a, hipStream_t s);
 
 bool decode_supported(int head_dim, int group);
+// Waves per split work-group of the decode kernel for a group size.
+int decode_waves(int group);
 // Split-KV attention with an optional fused row append; sequences longer than one split
 // leave fp32 partials that launch_combine merges.
 hipError_t launch_decode(int head_dim, int group, const DecodeArgs& a, hipStream_t s);
