@@ -696,7 +696,7 @@ def main() -> int:
     achieved = main_r["decode_kernel_gbps"]
     roofline = {
         "bound": "hbm",
-        "kernel": "decode_split_kernel<128,4>" if w.head_dim == 128 and w.group == 4 else "decode_split_kernel",
+        "kernel": "decode_split_kernel<128,4,8>" if w.head_dim == 128 and w.group == 4 else "decode_split_kernel",
         "achieved": achieved,
         "peak": HBM_PEAK_GBPS,
         "unit": "GB/s",
