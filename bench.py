@@ -142,11 +142,34 @@ class DecodeBench:
             "decode_launches": int(counts[_lib.GQA_TIMER_DECODE]),
         }
 
+    def run_graph(self, steps: int, warmup: int) -> float:
+        """The same step captured once into a HIP graph and replayed: wall us per step."""
+        torch = self.torch
+        c = ctypes.c_void_p
+        graph = c()
+        self._lib.check(self.lib.gqa_graph_capture_decode_append(
+            self.ctx, c(self.q.data_ptr()), c(self.k_new.data_ptr()), c(self.v_new.data_ptr()), c(self.pos.data_ptr()),
+            c(self.lens_dev.data_ptr()), c(self.o.data_ptr()), None, ctypes.byref(graph)), "graph capture")
+        try:
+            for _ in range(warmup):
+                self.lib.gqa_graph_launch(graph, self.sptr)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                rc = self.lib.gqa_graph_launch(graph, self.sptr)
+                if rc:
+                    self._lib.check(rc, "graph launch")
+            torch.cuda.synchronize()
+            return (time.perf_counter() - t0) * 1e6 / steps
+        finally:
+            self.lib.gqa_graph_destroy(graph)
+
     def close(self) -> None:
         self.lib.gqa_destroy(self.ctx)
         self.ctx = ctypes.c_void_p()
 
 
+LAUNCH_BOUND = ("c1", "c2")  # workloads whose step is also timed as a replayed HIP graph
 PAGED_SUFFIX = "_paged"  # a decode workload over a paged cache of 64-row pages
 PAGE_ROWS = 64
 
@@ -161,6 +184,8 @@ def measure(name: str, steps: int, warmup: int, chunk: int = 0) -> dict:
     try:
         log(f"{name}: warmup {warmup}, timing {steps} steps")
         r = bench.run(steps, warmup)
+        if name in LAUNCH_BOUND:
+            r["graph_us_per_step"] = bench.run_graph(steps, warmup)
     finally:
         bench.close()
     lens = w.lengths()
@@ -180,7 +205,8 @@ def measure(name: str, steps: int, warmup: int, chunk: int = 0) -> dict:
     if r["decode_kernel_gbps"]:
         r["decode_kernel_frac_of_peak"] = r["decode_kernel_gbps"] / HBM_PEAK_GBPS
     log(f"{name}: {r['us_per_step']:.1f} us/step, step {r['step_gbps']:.0f} GB/s, decode kernel "
-        f"{r['decode_us']:.1f} us = {r.get('decode_kernel_gbps') or 0:.0f} GB/s")
+        f"{r['decode_us']:.1f} us = {r.get('decode_kernel_gbps') or 0:.0f} GB/s"
+        + (f", replayed graph {r['graph_us_per_step']:.1f} us/step" if "graph_us_per_step" in r else ""))
     return r
 
 
@@ -686,7 +712,7 @@ def main() -> int:
             continue
         r = measure(name, max(10, args.steps // 2), max(2, args.warmup // 2))
         others[name] = {k: r[k] for k in ("us_per_step", "step_gbps", "step_frac_of_peak", "decode_us",
-                                           "decode_kernel_gbps", "tokens_per_s")}
+                                           "decode_kernel_gbps", "tokens_per_s", "graph_us_per_step") if k in r}
     cpu = None
     if not args.no_cpu_baseline:
         log(f"cpu baseline ({args.cpu_seconds:.0f} s budget)")

@@ -246,6 +246,22 @@ int gqa_layer_qkv_device(gqa_ctx* ctx, int32_t b, const void* x, int32_t n_token
                          int32_t rope, void* q_out, void* stream);
 int gqa_layer_times(gqa_ctx* ctx, float* out_us, int32_t n);
 
+/* ---- HIP graphs -------------------------------------------------------------------
+ * No reference counterpart (the board's transaction is driven by CSR writes).  For
+ * launch-bound serving loops (small batches): gqa_graph_capture_decode_append records one
+ * gqa_decode_append_device step (k_rows = v_rows = positions = NULL: gqa_decode_device) with
+ * these device pointers into a HIP graph; gqa_graph_launch replays it on `stream` (NULL = the
+ * context stream), reading q, rows, positions and ctx_lens and writing o, lse and the cache at
+ * the captured addresses, so the caller updates those buffers in place between replays.  The
+ * split plan is fixed at capture (sized for max_seq_len).  A graph must be destroyed before
+ * its context; profiling timers do not record replays. */
+typedef struct gqa_graph gqa_graph;
+int gqa_graph_capture_decode_append(gqa_ctx* ctx, const void* q, const void* k_rows, const void* v_rows,
+                                    const int32_t* positions, const int32_t* ctx_lens, void* o,
+                                    float* lse, gqa_graph** out_graph);
+int gqa_graph_launch(gqa_graph* graph, void* stream);
+int gqa_graph_destroy(gqa_graph* graph);
+
 /* ---- timing ---------------------------------------------------------------------
  * gqa_last_elapsed_us: elapsed time of the last synchronous call (HIP events on the ctx
  * stream).  With GQA_OPT_PROFILE on, every kernel launch is bracketed by HIP events on

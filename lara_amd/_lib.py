@@ -116,6 +116,10 @@ _SIGNATURES = {
     "gqa_layer_qkv_device": [_CTX, c_int32, c_void_p, c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p,
                              c_float, c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p],
     "gqa_layer_times": [_CTX, _PF, c_int32],
+    "gqa_graph_capture_decode_append": [_CTX, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                        POINTER(c_void_p)],
+    "gqa_graph_launch": [c_void_p, c_void_p],
+    "gqa_graph_destroy": [c_void_p],
     "gqa_last_elapsed_us": [_CTX, _PF],
     "gqa_kernel_times": [_CTX, _PF, c_int32],
     "gqa_kernel_launch_counts": [_CTX, _P32, c_int32],

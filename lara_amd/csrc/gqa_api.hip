@@ -82,6 +82,14 @@ struct gqa_ctx {
     int page_size = 0, page_shift = 0, n_pages = 0, max_pages = 0;
     int32_t* table_dev = nullptr;
     PageTable pages;
+    int capturing = 0;  // a HIP graph capture is recording this context's launches (no timer events)
+};
+
+// A captured decode step (gqa_graph_capture_decode_append) and the context it reads.
+struct gqa_graph {
+    gqa_ctx* ctx = nullptr;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
 };
 
 namespace {
@@ -136,12 +144,12 @@ int choose_chunk(const gqa_ctx* c, int max_len) {
 constexpr int kProfileLaunches = 512;  // event pairs kept per timer slot
 
 void timer_begin(gqa_ctx* c, int slot, hipStream_t s) {
-    if (c->profile && c->ev_count[slot] < kProfileLaunches)
+    if (c->profile && !c->capturing && c->ev_count[slot] < kProfileLaunches)
         (void)hipEventRecord(c->ev_pool[slot][2 * c->ev_count[slot]], s);
 }
 
 void timer_end(gqa_ctx* c, int slot, hipStream_t s) {
-    if (c->profile && c->ev_count[slot] < kProfileLaunches) {
+    if (c->profile && !c->capturing && c->ev_count[slot] < kProfileLaunches) {
         (void)hipEventRecord(c->ev_pool[slot][2 * c->ev_count[slot] + 1], s);
         c->ev_count[slot] += 1;
     }
@@ -1142,6 +1150,67 @@ int gqa_layer_times(gqa_ctx* c, float* out_us, int32_t n) {
     int rc = layer_times(c);
     if (rc != GQA_OK) return rc;
     for (int i = 0; i < n; ++i) out_us[i] = c->layer_us[i];
+    return GQA_OK;
+}
+
+// ---- HIP graphs ------------------------------------------------------------------------
+
+int gqa_graph_capture_decode_append(gqa_ctx* c, const void* q, const void* k_rows, const void* v_rows,
+                                    const int32_t* positions, const int32_t* ctx_lens, void* o, float* lse,
+                                    gqa_graph** out) {
+    if (!c || !q || !ctx_lens || !o || !out) return GQA_ERR_NULL;
+    if ((k_rows == nullptr) != (v_rows == nullptr) || (k_rows != nullptr && positions == nullptr))
+        return GQA_ERR_NULL;
+    *out = nullptr;
+    int rc = txn_idle(c);
+    if (rc != GQA_OK) return rc;
+    HIP_TRY(hipSetDevice(c->cfg.device));
+    hipStream_t cap = nullptr;
+    HIP_TRY(hipStreamCreateWithFlags(&cap, hipStreamNonBlocking));
+    gqa_graph* g = new gqa_graph();
+    g->ctx = c;
+    hipError_t e = hipStreamBeginCapture(cap, hipStreamCaptureModeThreadLocal);
+    if (e == hipSuccess) {
+        c->capturing = 1;
+        rc = run_decode(c, q, ctx_lens, k_rows, v_rows, positions, o, lse, cap, c->cfg.max_seq_len);
+        c->capturing = 0;
+        const hipError_t e2 = hipStreamEndCapture(cap, &g->graph);
+        if (rc == GQA_OK && e2 != hipSuccess) {
+            last_hip_error(e2, "hipStreamEndCapture");
+            rc = GQA_ERR_HIP;
+        }
+    } else {
+        last_hip_error(e, "hipStreamBeginCapture");
+        rc = GQA_ERR_HIP;
+    }
+    if (rc == GQA_OK) {
+        e = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
+        if (e != hipSuccess) {
+            last_hip_error(e, "hipGraphInstantiate");
+            rc = GQA_ERR_HIP;
+        }
+    }
+    (void)hipStreamDestroy(cap);
+    if (rc != GQA_OK) {
+        gqa_graph_destroy(g);
+        return rc;
+    }
+    *out = g;
+    return GQA_OK;
+}
+
+int gqa_graph_launch(gqa_graph* g, void* stream) {
+    if (!g || !g->exec) return GQA_ERR_NULL;
+    HIP_TRY(hipSetDevice(g->ctx->cfg.device));
+    HIP_TRY(hipGraphLaunch(g->exec, pick_stream(g->ctx, stream)));
+    return GQA_OK;
+}
+
+int gqa_graph_destroy(gqa_graph* g) {
+    if (!g) return GQA_ERR_NULL;
+    if (g->exec) (void)hipGraphExecDestroy(g->exec);
+    if (g->graph) (void)hipGraphDestroy(g->graph);
+    delete g;
     return GQA_OK;
 }
 
