@@ -421,6 +421,58 @@ def measure_layer(name: str, steps: int, warmup: int, target_wgs: int = 0) -> di
     return out
 
 
+ONESHOT_PREFILL = {"p8k": 8192}  # one causal prefill launch of this many tokens (32 q / 8 kv heads, D 128)
+
+
+def measure_prefill_oneshot(name: str, steps: int, warmup: int) -> dict:
+    """One causal prefill launch over a whole prompt already in the cache (gqa_prefill_device)."""
+    import torch
+    from lara_amd import _lib
+    from lara_amd.benchmark import BF16_DENSE_TFLOPS, prefill_flops, valid_pairs
+
+    L = ONESHOT_PREFILL[name]
+    lib = _lib.lib()
+    log(f"{name}: one-shot causal prefill of {L} tokens")
+    cfg = _lib.GqaConfig(1, 32, 8, 128, L, L, 0.0, 0)
+    ctx = ctypes.c_void_p()
+    _lib.check(lib.gqa_create(ctypes.byref(cfg), ctypes.byref(ctx)), "gqa_create")
+    try:
+        g = torch.Generator(device="cuda")
+        g.manual_seed(9)
+        q = torch.randn((32, L, 128), generator=g, device="cuda").to(torch.bfloat16)
+        k = torch.randn((8, L, 128), generator=g, device="cuda").to(torch.bfloat16)
+        v = torch.randn((8, L, 128), generator=g, device="cuda").to(torch.bfloat16)
+        o = torch.empty_like(q)
+        c = ctypes.c_void_p
+        sptr = c(torch.cuda.current_stream().cuda_stream)
+        _lib.check(lib.gqa_load_kv_device(ctx, 0, 0, L, c(k.data_ptr()), c(v.data_ptr()), sptr), "load")
+
+        def step():
+            _lib.check(lib.gqa_prefill_device(ctx, 0, c(q.data_ptr()), L, 0, L, 0, 1, c(o.data_ptr()), None, sptr),
+                       "prefill")
+
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        _lib.check(lib.gqa_set_option(ctx, _lib.GQA_OPT_PROFILE, 1), "profile on")
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        wall_us = (time.perf_counter() - t0) * 1e6 / steps
+        t = (ctypes.c_float * _lib.GQA_TIMER_COUNT)()
+        _lib.check(lib.gqa_kernel_times(ctx, t, _lib.GQA_TIMER_COUNT), "kernel times")
+    finally:
+        lib.gqa_destroy(ctx)
+    kern_us = t[_lib.GQA_TIMER_PREFILL] + t[_lib.GQA_TIMER_COMBINE]
+    flops = prefill_flops(32, 128, valid_pairs(L, L, causal=True))
+    out = {"tokens": L, "us_per_prompt": wall_us, "kernel_us": kern_us,
+           "kernel_tflops": flops / (kern_us * 1e-6) / 1e12 if kern_us > 0 else None}
+    out["mfma_frac_of_bf16_peak"] = out["kernel_tflops"] / BF16_DENSE_TFLOPS if out["kernel_tflops"] else None
+    log(f"{name}: {wall_us:.1f} us/prompt, kernel {kern_us:.1f} us = {out['kernel_tflops'] or 0:.0f} TFLOP/s")
+    return out
+
+
 def read_traffic():
     """HBM bytes per decode launch from the committed rocprofv3 PMC summary, if present."""
     if not PROFILE_TRAFFIC.is_file():
@@ -662,7 +714,7 @@ def main() -> int:
     parser.add_argument("--chunk", type=int, default=0, help="keys per split-KV work-group (0 = auto)")
     parser.add_argument("--prefill-wgs", type=int, default=0,
                         help="work-groups the prefill KV segmentation aims for (0 = auto, 1 = no segments)")
-    parser.add_argument("--others", default="c2,c3,c4,c5,layer,ns_paged", help="extra decode workloads to report ('' = none)")
+    parser.add_argument("--others", default="c2,c3,c4,c5,p8k,layer,ns_paged", help="extra decode workloads to report ('' = none)")
     parser.add_argument("--cpu-seconds", type=float, default=12.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--calibrate-copy-mib", type=int, default=0,
@@ -706,6 +758,9 @@ def main() -> int:
     for name in [x for x in args.others.split(",") if x and x != args.workload]:
         if name == "c5":
             others[name] = measure_prefill(name, max(10, args.steps // 2), max(2, args.warmup // 2), args.prefill_wgs)
+            continue
+        if name in ONESHOT_PREFILL:
+            others[name] = measure_prefill_oneshot(name, max(5, args.steps // 10), 2)
             continue
         if name == "layer":
             others[name] = measure_layer(name, max(10, args.steps // 4), max(2, args.warmup // 2), args.prefill_wgs)
