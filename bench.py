@@ -732,7 +732,7 @@ def main() -> int:
     parser.add_argument("--board-warmup", type=int, default=1)
     parser.add_argument("--board-repeats", type=int, default=5)
     parser.add_argument("--cpu-threads", type=int, default=int(os.environ.get("LARA_CPU_THREADS", "1")))
-    parser.add_argument("--output-dir", default="gpurun_out/board_performance")
+    parser.add_argument("--output-dir", default="board_performance_results")
     args = parser.parse_args()
     args.lengths_given = args.lengths is not None
     if args.lengths is None:
