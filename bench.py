@@ -3,16 +3,19 @@
 
 Default workload: Llama-3-8B-shape GQA decode, batch 64, 32 query / 8 KV heads,
 head_dim 128, bf16, 8192 attended keys per sequence.  One step appends one K/V row per
-sequence (bit-exact row copy into the HBM cache) and then attends every cached row:
-split-KV decode kernel + log-sum-exp combine kernel.  Inputs are synthetic N(0, 1) bf16
-generated on the GPU and resident in HBM before the timed region; the cache (2 GiB) is
-far larger than the 256 MB Infinity Cache, so the rate is an HBM rate.
+sequence (bit-exact row copy into the HBM cache) and then attends every cached row, in one
+split-KV decode launch (plus a log-sum-exp merge launch when a sequence spans several
+splits).  Inputs are synthetic N(0, 1) bf16 generated on the GPU and resident in HBM before
+the timed region; the cache (2 GiB) is far larger than the 256 MB Infinity Cache, so the
+rate is an HBM rate.
 
-Printed: ONE JSON line.  ``value`` is the whole-step algorithmic byte rate in GB/s;
-``roofline`` describes the dominant kernel (the split-KV decode kernel) from its HIP-event
-average over the timed steps; ``cpu_baseline`` times the fp32 NumPy oracle on the host on
-a bounded sample of the same workload.  Other decode workloads (C2, C3, C4) are measured
-the same way and reported under ``other_workloads``.
+Printed: ONE JSON line.  ``value`` is the whole-step algorithmic byte rate in GB/s over the
+timed steps (no per-launch events in them); ``roofline`` describes the dominant kernel (the
+split-KV decode kernel) from the average of per-launch HIP events on its stream over a second
+pass of the same steps; ``cpu_baseline`` times the fp32 NumPy oracle on the host on a bounded
+sample of the same workload.  Other workloads (decode C2, C3, C4, paged NS; chunked prefill;
+one-shot prefill; the layer input stage) are measured the same way and reported under
+``other_workloads``.
 """
 from __future__ import annotations
 
@@ -42,6 +45,54 @@ WORKLOAD_NAMES = {
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def bench_stream(dev):
+    """A stream of the bench's own (default priority) for the library's launches: the timing
+    events are recorded on the stream the kernels run on.  Inputs made on torch's stream are
+    synchronised before the library reads them."""
+    import torch
+
+    return torch.cuda.Stream(device=dev)
+
+
+def timed_passes(lib, _lib, ctx, stream, step, steps: int, warmup: int) -> dict:
+    """Warm-up, then two passes of `steps` calls of `step` on `stream`.
+
+    The timed pass runs the steps alone between two synchronisations (wall clock) and one pair
+    of events on the stream (device time per step).  The kernel pass repeats them with the
+    library's per-launch HIP events on the same stream (GQA_OPT_PROFILE) and returns each
+    kernel's average launch duration.  Every recorded event pair leaves the GPU idle for
+    several microseconds between launches on this runtime, which is why it stays out of the
+    timed pass.
+    """
+    import torch
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(steps):
+        step()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    gpu_ms = ev0.elapsed_time(ev1) / steps
+    _lib.check(lib.gqa_set_option(ctx, _lib.GQA_OPT_PROFILE, 1), "profile on")
+    try:
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        times = (ctypes.c_float * _lib.GQA_TIMER_COUNT)()
+        counts = (ctypes.c_int32 * _lib.GQA_TIMER_COUNT)()
+        _lib.check(lib.gqa_kernel_times(ctx, times, _lib.GQA_TIMER_COUNT), "kernel times")
+        _lib.check(lib.gqa_kernel_launch_counts(ctx, counts, _lib.GQA_TIMER_COUNT), "counts")
+    finally:
+        _lib.check(lib.gqa_set_option(ctx, _lib.GQA_OPT_PROFILE, 0), "profile off")
+    return {"wall_ms": wall_ms, "gpu_ms": gpu_ms, "times": list(times), "counts": list(counts)}
 
 
 class DecodeBench:
@@ -75,7 +126,7 @@ class DecodeBench:
         if chunk:
             _lib.check(self.lib.gqa_set_option(self.ctx, _lib.GQA_OPT_DECODE_CHUNK, chunk), "chunk")
         dev = torch.device("cuda", device)
-        self.stream = torch.cuda.current_stream(dev)
+        self.stream = bench_stream(dev)
         sptr = ctypes.c_void_p(self.stream.cuda_stream)
         self.sptr = sptr
         g = torch.Generator(device=dev)
@@ -90,8 +141,10 @@ class DecodeBench:
                 k[rows] *= w.outlier_scale
             k = k.to(torch.bfloat16)
             v = (torch.randn((w.n_kv_heads, n, w.head_dim), generator=g, device=dev) * amp).to(torch.bfloat16)
+            torch.cuda.synchronize(dev)  # k, v are written on torch's stream; the copy runs on the bench stream
             _lib.check(self.lib.gqa_load_kv_device(self.ctx, b, 0, n, ctypes.c_void_p(k.data_ptr()),
                                                    ctypes.c_void_p(v.data_ptr()), sptr), "load_kv_device")
+            torch.cuda.synchronize(dev)
             del k, v
         self.q = (torch.randn((w.batch, w.n_q_heads, w.head_dim), generator=g, device=dev) * amp).to(torch.bfloat16)
         self.k_new = (torch.randn((w.batch, w.n_kv_heads, w.head_dim), generator=g, device=dev) * amp).to(
@@ -112,34 +165,15 @@ class DecodeBench:
             self._lib.check(rc, "decode_append")
 
     def run(self, steps: int, warmup: int) -> dict:
-        torch = self.torch
         _lib = self._lib
-        for _ in range(warmup):
-            self.step()
-        torch.cuda.synchronize()
-        # Per-kernel HIP events on the stream the kernels run on, over the timed steps.
-        _lib.check(self.lib.gqa_set_option(self.ctx, _lib.GQA_OPT_PROFILE, 1), "profile on")
-        ev0 = torch.cuda.Event(enable_timing=True)
-        ev1 = torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        ev0.record(self.stream)
-        for _ in range(steps):
-            self.step()
-        ev1.record(self.stream)
-        torch.cuda.synchronize()
-        wall_ms = (time.perf_counter() - t0) * 1e3 / steps
-        gpu_ms = ev0.elapsed_time(ev1) / steps
-        times = (ctypes.c_float * _lib.GQA_TIMER_COUNT)()
-        counts = (ctypes.c_int32 * _lib.GQA_TIMER_COUNT)()
-        _lib.check(self.lib.gqa_kernel_times(self.ctx, times, _lib.GQA_TIMER_COUNT), "kernel times")
-        _lib.check(self.lib.gqa_kernel_launch_counts(self.ctx, counts, _lib.GQA_TIMER_COUNT), "counts")
-        _lib.check(self.lib.gqa_set_option(self.ctx, _lib.GQA_OPT_PROFILE, 0), "profile off")
+        t = timed_passes(self.lib, _lib, self.ctx, self.stream, self.step, steps, warmup)
         return {
-            "wall_ms_per_step": wall_ms,
-            "gpu_ms_per_step": gpu_ms,
-            "decode_us": times[_lib.GQA_TIMER_DECODE],
-            "decode_launches": int(counts[_lib.GQA_TIMER_DECODE]),
+            "wall_ms_per_step": t["wall_ms"],
+            "gpu_ms_per_step": t["gpu_ms"],
+            "decode_us": t["times"][_lib.GQA_TIMER_DECODE],
+            "decode_launches": int(t["counts"][_lib.GQA_TIMER_DECODE]),
+            "combine_us": t["times"][_lib.GQA_TIMER_COMBINE],
+            "combine_launches": int(t["counts"][_lib.GQA_TIMER_COMBINE]),
         }
 
     def run_graph(self, steps: int, warmup: int) -> float:
@@ -227,7 +261,7 @@ class PrefillBench:
         if target_wgs:
             _lib.check(self.lib.gqa_set_option(self.ctx, _lib.GQA_OPT_PREFILL_WGS, target_wgs), "prefill wgs")
         dev = torch.device("cuda", device)
-        self.stream = torch.cuda.current_stream(dev)
+        self.stream = bench_stream(dev)
         self.sptr = ctypes.c_void_p(self.stream.cuda_stream)
         g = torch.Generator(device=dev)
         g.manual_seed(w.seed)
@@ -256,25 +290,12 @@ class PrefillBench:
                 self._lib.check(rc, "prefill_append_device")
 
     def run(self, steps: int, warmup: int) -> dict:
-        torch = self.torch
         _lib = self._lib
-        for _ in range(warmup):
-            self.step()
-        torch.cuda.synchronize()
-        _lib.check(self.lib.gqa_set_option(self.ctx, _lib.GQA_OPT_PROFILE, 1), "profile on")
-        t0 = time.perf_counter()
-        for _ in range(steps):
-            self.step()
-        torch.cuda.synchronize()
-        wall_ms = (time.perf_counter() - t0) * 1e3 / steps
-        times = (ctypes.c_float * _lib.GQA_TIMER_COUNT)()
-        _lib.check(self.lib.gqa_kernel_times(self.ctx, times, _lib.GQA_TIMER_COUNT), "kernel times")
-        counts = (ctypes.c_int32 * _lib.GQA_TIMER_COUNT)()
-        _lib.check(self.lib.gqa_kernel_launch_counts(self.ctx, counts, _lib.GQA_TIMER_COUNT), "counts")
-        _lib.check(self.lib.gqa_set_option(self.ctx, _lib.GQA_OPT_PROFILE, 0), "profile off")
-        merges = counts[_lib.GQA_TIMER_COMBINE] / max(1, counts[_lib.GQA_TIMER_PREFILL])
-        return {"wall_ms_per_prompt": wall_ms, "prefill_us_per_launch": times[_lib.GQA_TIMER_PREFILL],
-                "merge_us_per_launch": times[_lib.GQA_TIMER_COMBINE] * merges}
+        t = timed_passes(self.lib, _lib, self.ctx, self.stream, self.step, steps, warmup)
+        merges = t["counts"][_lib.GQA_TIMER_COMBINE] / max(1, t["counts"][_lib.GQA_TIMER_PREFILL])
+        return {"wall_ms_per_prompt": t["wall_ms"], "gpu_ms_per_prompt": t["gpu_ms"],
+                "prefill_us_per_launch": t["times"][_lib.GQA_TIMER_PREFILL],
+                "merge_us_per_launch": t["times"][_lib.GQA_TIMER_COMBINE] * merges}
 
     def close(self) -> None:
         self.lib.gqa_destroy(self.ctx)
@@ -330,7 +351,8 @@ class LayerBench:
         if target_wgs:
             _lib.check(self.lib.gqa_set_option(self.ctx, _lib.GQA_OPT_PREFILL_WGS, target_wgs), "prefill wgs")
         dev = torch.device("cuda", device)
-        self.sptr = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        self.stream = bench_stream(dev)
+        self.sptr = ctypes.c_void_p(self.stream.cuda_stream)
         g = torch.Generator(device=dev)
         g.manual_seed(w.seed)
         nq, nkv = w.n_q_heads * w.head_dim, w.n_kv_heads * w.head_dim
@@ -356,32 +378,24 @@ class LayerBench:
         self._lib.check(rc, "gqa_prefill_device")
 
     def run(self, steps: int, warmup: int) -> dict:
-        torch = self.torch
         _lib = self._lib
-        for _ in range(warmup):
-            self.step()
-        torch.cuda.synchronize()
+        t = timed_passes(self.lib, _lib, self.ctx, self.stream, self.step, steps, warmup)
+        # Stage times: a few more calls with the library's stage events on (profiling on), each
+        # read back after its own synchronisation.
         _lib.check(self.lib.gqa_set_option(self.ctx, _lib.GQA_OPT_PROFILE, 1), "profile on")
-        t0 = time.perf_counter()
-        for _ in range(steps):
-            self.step()
-        torch.cuda.synchronize()
-        wall_ms = (time.perf_counter() - t0) * 1e3 / steps
-        # stage times of one more (synchronised) call: the library's events on its stream
         stage = np.zeros(3)
-        for _ in range(5):
-            self.step()
-            stage_us = (ctypes.c_float * 3)()
-            _lib.check(self.lib.gqa_layer_times(self.ctx, stage_us, 3), "layer times")
-            stage += np.array(stage_us[:]) / 5
-        times = (ctypes.c_float * _lib.GQA_TIMER_COUNT)()
-        _lib.check(self.lib.gqa_kernel_times(self.ctx, times, _lib.GQA_TIMER_COUNT), "kernel times")
-        counts = (ctypes.c_int32 * _lib.GQA_TIMER_COUNT)()
-        _lib.check(self.lib.gqa_kernel_launch_counts(self.ctx, counts, _lib.GQA_TIMER_COUNT), "counts")
-        _lib.check(self.lib.gqa_set_option(self.ctx, _lib.GQA_OPT_PROFILE, 0), "profile off")
-        merges = counts[_lib.GQA_TIMER_COMBINE] / max(1, counts[_lib.GQA_TIMER_PREFILL])
-        return {"wall_ms": wall_ms, "stage_us": stage, "prefill_us": times[_lib.GQA_TIMER_PREFILL],
-                "merge_us": times[_lib.GQA_TIMER_COMBINE] * merges}
+        try:
+            for _ in range(5):
+                self.step()
+                stage_us = (ctypes.c_float * 3)()
+                _lib.check(self.lib.gqa_layer_times(self.ctx, stage_us, 3), "layer times")
+                stage += np.array(stage_us[:]) / 5
+        finally:
+            _lib.check(self.lib.gqa_set_option(self.ctx, _lib.GQA_OPT_PROFILE, 0), "profile off")
+        merges = t["counts"][_lib.GQA_TIMER_COMBINE] / max(1, t["counts"][_lib.GQA_TIMER_PREFILL])
+        return {"wall_ms": t["wall_ms"], "gpu_ms": t["gpu_ms"], "stage_us": stage,
+                "prefill_us": t["times"][_lib.GQA_TIMER_PREFILL],
+                "merge_us": t["times"][_lib.GQA_TIMER_COMBINE] * merges}
 
     def close(self) -> None:
         self.lib.gqa_destroy(self.ctx)
@@ -444,24 +458,18 @@ def measure_prefill_oneshot(name: str, steps: int, warmup: int) -> dict:
         v = torch.randn((8, L, 128), generator=g, device="cuda").to(torch.bfloat16)
         o = torch.empty_like(q)
         c = ctypes.c_void_p
-        sptr = c(torch.cuda.current_stream().cuda_stream)
+        stream = bench_stream(torch.device("cuda", 0))
+        sptr = c(stream.cuda_stream)
+        torch.cuda.synchronize()
         _lib.check(lib.gqa_load_kv_device(ctx, 0, 0, L, c(k.data_ptr()), c(v.data_ptr()), sptr), "load")
 
         def step():
             _lib.check(lib.gqa_prefill_device(ctx, 0, c(q.data_ptr()), L, 0, L, 0, 1, c(o.data_ptr()), None, sptr),
                        "prefill")
 
-        for _ in range(warmup):
-            step()
-        torch.cuda.synchronize()
-        _lib.check(lib.gqa_set_option(ctx, _lib.GQA_OPT_PROFILE, 1), "profile on")
-        t0 = time.perf_counter()
-        for _ in range(steps):
-            step()
-        torch.cuda.synchronize()
-        wall_us = (time.perf_counter() - t0) * 1e6 / steps
-        t = (ctypes.c_float * _lib.GQA_TIMER_COUNT)()
-        _lib.check(lib.gqa_kernel_times(ctx, t, _lib.GQA_TIMER_COUNT), "kernel times")
+        r = timed_passes(lib, _lib, ctx, stream, step, steps, warmup)
+        wall_us = r["wall_ms"] * 1e3
+        t = r["times"]
     finally:
         lib.gqa_destroy(ctx)
     kern_us = t[_lib.GQA_TIMER_PREFILL] + t[_lib.GQA_TIMER_COMBINE]

@@ -197,7 +197,10 @@ int gqa_read_perf(gqa_ctx* ctx, uint64_t* total_ticks, uint64_t* kernel_ticks,
 
 /* ---- device-pointer forms (inputs already in HBM; stream may be NULL = ctx stream) --
  * Same semantics as the host forms; all pointers are device pointers.  They enqueue
- * and return without synchronising. */
+ * and return without synchronising.  The context stream is a blocking HIP stream: work
+ * on it is ordered both ways with the legacy default stream (handle 0, PyTorch's default
+ * stream), so passing NULL from code that uses the default stream needs no extra sync.
+ * A non-default caller stream gets no such ordering: pass that stream itself. */
 int gqa_append_kv_device(gqa_ctx* ctx, const void* k_rows, const void* v_rows,
                          const int32_t* positions, void* stream);
 int gqa_decode_device(gqa_ctx* ctx, const void* q, const int32_t* ctx_lens,
@@ -235,7 +238,10 @@ int gqa_cache_pointers(gqa_ctx* ctx, void** k_cache, void** v_cache, int32_t* l_
  * gqa_layer_qkv_device does the same from device memory without a transaction: Q goes to
  * q_out ([H_q][n_tokens][D]), K/V to rows [kv_row0, kv_row0 + n_tokens) of sequence b; it
  * allocates its workspace on first use.  gqa_layer_times returns the device time in us of
- * the last call's RMSNorm, projection and RoPE stages (n <= 3; synchronises). */
+ * the RMSNorm, projection and RoPE stages (n <= 3; synchronises) of the last gqa_submit_layer
+ * call, or of the last gqa_layer_qkv_device call made while GQA_OPT_PROFILE is on (stage events
+ * idle the GPU between launches, so device calls record none otherwise);
+ * GQA_ERR_NO_TRANSACTION when the last call recorded none. */
 int gqa_submit_layer(gqa_ctx* ctx, int32_t b, const uint16_t* x, int32_t n_tokens, int32_t hidden,
                      const uint16_t* wq, const uint16_t* wk, const uint16_t* wv,
                      const uint16_t* rms_weight, float rms_eps, int32_t q_pos_base,

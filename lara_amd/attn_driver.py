@@ -930,7 +930,8 @@ class AttentionAccelerator:
                    ctypes.c_void_p(stream) if stream else None)
 
     def layer_stage_us(self) -> tuple[float, float, float]:
-        """Device time (us) of the last layer call's RMSNorm, projection and RoPE stages."""
+        """Device time (us) of the RMSNorm, projection and RoPE stages of the last ``run_layer``
+        call, or of the last ``layer_qkv_device`` call made while profiling is on."""
         self._ensure_open()
         out = (ctypes.c_float * 3)()
         self._call("gqa_layer_times", out, 3)

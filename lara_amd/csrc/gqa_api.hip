@@ -68,7 +68,9 @@ struct gqa_ctx {
     double clock_mhz = 0.0;
     Txn txn;
     // Layer input stage (run_layer): rocBLAS handle and grow-only device workspaces, created on
-    // first use; ev_layer brackets RMSNorm, projection and RoPE of the last layer call.
+    // first use; ev_layer brackets RMSNorm, projection and RoPE of the last timed layer call
+    // (every host-pointer call; a device call only while profiling is on, since each recorded
+    // event leaves the GPU idle for several microseconds between the launches it separates).
     rocblas_handle blas = nullptr;
     uint8_t* layer_in = nullptr;   // host-entry uploads: x, Wq, Wk, Wv, gamma
     size_t layer_in_bytes = 0;
@@ -76,6 +78,7 @@ struct gqa_ctx {
     size_t layer_tmp_bytes = 0;
     hipEvent_t ev_layer[4] = {};
     float layer_us[3] = {};
+    bool layer_timed = false;  // ev_layer holds a recorded call
     // Paged cache (gqa_create_paged): k_cache/v_cache are page pools [n_pages][H_kv][P][D], the
     // block tables [B][max_pages] live on the device (table_dev) and in `pages` on the host.
     int paged = 0;
@@ -363,7 +366,7 @@ int check_layer_args(const gqa_ctx* c, int32_t b, int32_t n_tokens, int32_t hidd
 // (if rope) and scatter: Q to q_out [H_q][n_tokens][D], K/V to rows row0.. of sequence b.
 int run_layer_qkv(gqa_ctx* c, int32_t b, const void* x, int32_t n_tokens, int32_t hidden, const void* wq,
                   const void* wk, const void* wv, const void* gamma, float eps, int32_t q_pos_base,
-                  int32_t kv_pos_base, int32_t row0, int32_t rope, void* q_out, hipStream_t s) {
+                  int32_t kv_pos_base, int32_t row0, int32_t rope, void* q_out, hipStream_t s, bool timed) {
     const int D = c->cfg.head_dim, nq = c->cfg.n_q_heads * D, nkv = c->cfg.n_kv_heads * D;
     const int ld = nq + 2 * nkv;
     const size_t y_bytes = gamma ? ((size_t)n_tokens * hidden * 2 + 255) / 256 * 256 : 0;
@@ -377,9 +380,11 @@ int run_layer_qkv(gqa_ctx* c, int32_t b, const void* x, int32_t n_tokens, int32_
             return GQA_ERR_HIP;
         }
     }
-    if (!c->ev_layer[0])
+    if (timed && !c->ev_layer[0])
         for (int i = 0; i < 4; ++i) HIP_TRY(hipEventCreate(&c->ev_layer[i]));
-    HIP_TRY(hipEventRecord(c->ev_layer[0], s));
+    c->layer_timed = false;
+    auto mark = [&](int i) { return timed ? hipEventRecord(c->ev_layer[i], s) : hipSuccess; };
+    HIP_TRY(mark(0));
     const uint16_t* src = (const uint16_t*)x;
     if (gamma) {
         NormArgs na{};
@@ -392,7 +397,7 @@ int run_layer_qkv(gqa_ctx* c, int32_t b, const void* x, int32_t n_tokens, int32_
         HIP_TRY(launch_rms_norm(na, s));
         src = na.y;
     }
-    HIP_TRY(hipEventRecord(c->ev_layer[1], s));
+    HIP_TRY(mark(1));
     uint16_t* qkv = (uint16_t*)(c->layer_tmp + y_bytes);
     rocblas_status st = rocblas_set_stream(c->blas, s);
     const float one = 1.f, zero = 0.f;
@@ -417,7 +422,7 @@ int run_layer_qkv(gqa_ctx* c, int32_t b, const void* x, int32_t n_tokens, int32_
         snprintf(g_last_error, sizeof(g_last_error), "rocblas_gemm_ex: %s", rocblas_status_to_string(st));
         return GQA_ERR_HIP;
     }
-    HIP_TRY(hipEventRecord(c->ev_layer[2], s));
+    HIP_TRY(mark(2));
     RopeArgs ra{};
     ra.qkv = qkv;
     ra.ld = ld;
@@ -438,7 +443,8 @@ int run_layer_qkv(gqa_ctx* c, int32_t b, const void* x, int32_t n_tokens, int32_
     ra.row0 = row0;
     for (int p = 0; p < D / 2; ++p) ra.theta[p] = (float)pow(kRopeBase, -2.0 * p / D);
     HIP_TRY(launch_rope_scatter(ra, s));
-    HIP_TRY(hipEventRecord(c->ev_layer[3], s));
+    HIP_TRY(mark(3));
+    c->layer_timed = timed;
     return GQA_OK;
 }
 
@@ -528,7 +534,10 @@ int create_ctx(const gqa_config* cfg, int32_t page_size, int32_t n_pages, gqa_ct
     alloc((void**)&c->new_dev, 2 * (size_t)k.n_kv_heads * k.max_q_len * D * 2);
     if (c->paged) alloc((void**)&c->table_dev, (size_t)k.batch * c->max_pages * sizeof(int32_t));
     if (rc == GQA_OK && hipHostMalloc((void**)&c->o_pinned, c->stage_words * 2, 0) != hipSuccess) rc = GQA_ERR_OOM;
-    if (rc == GQA_OK && hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) rc = GQA_ERR_HIP;
+    // A blocking stream: ordered both ways with the legacy default stream, so a caller that
+    // passes NULL (for instance PyTorch's default stream, whose handle is 0) sees its own
+    // earlier default-stream work finish before the library reads it, and vice versa.
+    if (rc == GQA_OK && hipStreamCreateWithFlags(&c->stream, hipStreamDefault) != hipSuccess) rc = GQA_ERR_HIP;
     if (rc == GQA_OK) {
         bool ok = hipEventCreate(&c->ev_begin) == hipSuccess && hipEventCreate(&c->ev_end) == hipSuccess;
         for (int i = 0; i < 4 && ok; ++i) ok = hipEventCreate(&c->ev_t[i]) == hipSuccess;
@@ -1092,7 +1101,7 @@ int gqa_layer_qkv_device(gqa_ctx* c, int32_t b, const void* x, int32_t n_tokens,
     if (!(rms_eps >= 0.f) || !isfinite(rms_eps)) return GQA_ERR_RANGE;
     HIP_TRY(hipSetDevice(c->cfg.device));
     return run_layer_qkv(c, b, x, n_tokens, hidden, wq, wk, wv, rms_weight, rms_eps, q_pos_base, kv_pos_base, kv_row0,
-                         rope, q_out, pick_stream(c, stream));
+                         rope, q_out, pick_stream(c, stream), c->profile && !c->capturing);
 }
 
 int gqa_submit_layer(gqa_ctx* c, int32_t b, const uint16_t* x, int32_t n_tokens, int32_t hidden, const uint16_t* wq,
@@ -1134,7 +1143,7 @@ int gqa_submit_layer(gqa_ctx* c, int32_t b, const uint16_t* x, int32_t n_tokens,
     HIP_TRY(hipMemcpyAsync(dwv, wv, wkb, hipMemcpyHostToDevice, c->stream));
     if (rms_weight) HIP_TRY(hipMemcpyAsync(dg, rms_weight, gb, hipMemcpyHostToDevice, c->stream));
     rc = run_layer_qkv(c, b, dx, n_tokens, hidden, dwq, dwk, dwv, rms_weight ? dg : nullptr, rms_eps, q_pos_base,
-                       kv_pos_base, 0, rope, c->q_dev, c->stream);
+                       kv_pos_base, 0, rope, c->q_dev, c->stream, true);
     if (rc != GQA_OK) return rc;
     HIP_TRY(hipStreamSynchronize(c->stream));
     rc = layer_times(c);
@@ -1146,7 +1155,7 @@ int gqa_submit_layer(gqa_ctx* c, int32_t b, const uint16_t* x, int32_t n_tokens,
 int gqa_layer_times(gqa_ctx* c, float* out_us, int32_t n) {
     if (!c || !out_us) return GQA_ERR_NULL;
     if (n < 0 || n > 3) return GQA_ERR_RANGE;
-    if (!c->ev_layer[0]) return GQA_ERR_NO_TRANSACTION;
+    if (!c->layer_timed) return GQA_ERR_NO_TRANSACTION;
     int rc = layer_times(c);
     if (rc != GQA_OK) return rc;
     for (int i = 0; i < n; ++i) out_us[i] = c->layer_us[i];

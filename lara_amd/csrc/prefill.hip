@@ -192,14 +192,18 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
         return max(hi, 0);
     };
 
-    // Fused append: the copy into the cache, before any early exit.
+    // Fused append: the new rows are copied into the cache by every work-group of this kv
+    // head, an equal share each, so no work-group carries the whole copy.  Blocks that hold
+    // these rows read them from k_new/v_new (issue below), so no work-group waits for the copy.
     const bool has_new = a.k_new != nullptr && a.n_new > 0;
-    if (has_new && blockIdx.x == 0) {
+    auto append_share = [&]() {
         const u32x4* ks = reinterpret_cast<const u32x4*>(a.k_new) + (size_t)h * a.n_new * NCH;
         const u32x4* vs = reinterpret_cast<const u32x4*>(a.v_new) + (size_t)h * a.n_new * NCH;
         const int words = a.n_new * NCH;
+        const int n_threads = gridDim.x * gridDim.z * (kWaves * 64);
+        const int first = (blockIdx.z * gridDim.x + blockIdx.x) * (kWaves * 64) + tid;
         if constexpr (PAGED) {
-            for (int i = blockIdx.z * (kWaves * 64) + tid; i < words; i += gridDim.z * (kWaves * 64)) {
+            for (int i = first; i < words; i += n_threads) {
                 const int64_t r = paged_row(a.block_table, a.page_shift, a.n_kv_heads, h, a.new_begin + i / NCH);
                 if (r < 0) continue;  // unmapped page: nothing to write
                 const size_t dst = (size_t)r * NCH + (i % NCH);
@@ -209,19 +213,22 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
         } else {
             u32x4* kd = reinterpret_cast<u32x4*>(a.kc + ((size_t)h * a.l_cap + a.new_begin) * D);
             u32x4* vd = reinterpret_cast<u32x4*>(a.vc + ((size_t)h * a.l_cap + a.new_begin) * D);
-            for (int i = blockIdx.z * (kWaves * 64) + tid; i < words; i += gridDim.z * (kWaves * 64)) {
+            for (int i = first; i < words; i += n_threads) {
                 kd[i] = ks[i];
                 vd[i] = vs[i];
             }
         }
-    }
+    };
     const int last_task = min(n_tasks, (wg_x + 1) * kWaves) - 1;
     const int wg_hi = kv_limit(last_task / G);  // row blocks grow with the task index
     const int wave_hi = active ? kv_limit(rb) : 0;
     const int seg_begin = blockIdx.z * a.seg_len;
     // With several segments, one that no row of this work-group reaches is not read by the
     // merge; a single segment always reaches the epilogue (rows without keys output 0).
-    if (a.n_segs > 1 && seg_begin >= wg_hi) return;
+    if (a.n_segs > 1 && seg_begin >= wg_hi) {
+        if (has_new) append_share();
+        return;
+    }
     const int seg_end = min(wg_hi, seg_begin + a.seg_len);
     const int n_blocks = seg_end > seg_begin ? (seg_end - seg_begin + kBN - 1) / kBN : 0;
 
@@ -230,17 +237,6 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
     const int row = rb * kRows + col;
     const bool row_ok = active && row < a.q_len;
     const int q_pos = a.q_pos_base + row;
-
-    // Q^T operand: row `row`, dims 16*ks + 8*half .. +7.
-    u32x4 qb[KSTEPS];
-    {
-        const u32x4* qp = reinterpret_cast<const u32x4*>(a.q + ((size_t)hq * a.q_len + row) * D);
-#pragma unroll
-        for (int ks = 0; ks < KSTEPS; ++ks) qb[ks] = row_ok ? qp[2 * ks + half] : u32x4{0u, 0u, 0u, 0u};
-    }
-    // Retire the Q loads now: with none of its own loads pending, the compiler inserts no
-    // wait-for-everything inside the loop, where the stage ring's loads are in flight.
-    wait_vmcnt<0>();
 
     f32x16 o[MT];
 #pragma unroll
@@ -337,13 +333,29 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
     constexpr float kLazyLog2 = 8.0f;
     const float c = a.scale_log2;
 
+    // Q^T operand: row `row`, dims 16*ks + 8*half .. +7.  The Q loads, the first two blocks'
+    // K/V loads and the append share's loads are all in flight before the first wait.
+    u32x4 qb[KSTEPS];
+    {
+        const u32x4* qp = reinterpret_cast<const u32x4*>(a.q + ((size_t)hq * a.q_len + row) * D);
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks) qb[ks] = row_ok ? qp[2 * ks + half] : u32x4{0u, 0u, 0u, 0u};
+    }
     if (n_blocks > 0) issue(seg_begin, 0);
     if (n_blocks > 1) issue(seg_begin + kBN, 1);
+    if (has_new) append_share();
+    // Retire everything now (Q, the append and the first blocks, issued together): with none of
+    // its own loads pending, the compiler inserts no wait-for-everything inside the loop, where
+    // the stage ring's loads are in flight.
+    wait_vmcnt<0>();
     for (int blk = 0; blk < n_blocks; ++blk) {
         const int st = blk % kStages;
         const int j0 = seg_begin + blk * kBN;
-        // This thread's loads of block blk are done once at most the next block's remain.
-        if (blk + 1 < n_blocks) wait_vmcnt<LPB>(); else wait_vmcnt<0>();
+        // This thread's loads of block blk are done once at most the next block's remain
+        // (blocks 0 and 1 were retired before the loop).
+        if (blk >= 1) {
+            if (blk + 1 < n_blocks) wait_vmcnt<LPB>(); else wait_vmcnt<0>();
+        }
         stage_barrier();  // every wave's block blk landed; block blk-1's stage is free
         if (blk + 2 < n_blocks) issue(j0 + 2 * kBN, (blk + 2) % kStages);
         if (j0 >= wave_hi) continue;  // this wave's rows see no key of the block
@@ -493,8 +505,10 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
 // Merge of a row's KV segments.  Segment s holds keys [s*seg_len, (s+1)*seg_len); a row
 // reads the segments below its own key limit, which are exactly the ones prefill_kernel
 // wrote for it.  A work-group merges kMergeRows rows of one query head; each row is handled
-// by D/4 threads owning four dims (16-byte loads), which all read the row's (m, l) pairs.
+// by D/4 threads owning four dims (16-byte loads).  The (m, l) pairs and O slices of up to
+// kMergeBatch segments are loaded together, so a row pays one memory latency per batch.
 constexpr int kMergeRows = 8;
+constexpr int kMergeBatch = 8;
 
 template <int D>
 __global__ __launch_bounds__(kMergeRows * D / 4) void prefill_combine_kernel(PrefillArgs a) {
@@ -509,24 +523,44 @@ __global__ __launch_bounds__(kMergeRows * D / 4) void prefill_combine_kernel(Pre
     const int n_valid = min(a.n_segs, (hi + a.seg_len - 1) / a.seg_len);
     const size_t seg_stride = (size_t)a.n_q_heads * a.q_len;
     const size_t prow = (size_t)hq * a.q_len + row;
-    const float2* ml = reinterpret_cast<const float2*>(a.part_ml);
-    float M = -INFINITY;
-    for (int sp = 0; sp < n_valid; ++sp) M = fmaxf(M, ml[sp * seg_stride + prow].x);
+    const float2* ml = reinterpret_cast<const float2*>(a.part_ml) + prow;
+    const float4* po = reinterpret_cast<const float4*>(a.part_o) + prow * TPR + d4;
+    float M = -INFINITY;  // running max over the merged segments (log2 units)
     float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
     float Ls = 0.f;
-    if (M != -INFINITY) {
-        const float4* po = reinterpret_cast<const float4*>(a.part_o) + prow * TPR + d4;
-#pragma unroll 4
-        for (int sp = 0; sp < n_valid; ++sp) {
-            const float2 e = ml[sp * seg_stride + prow];
-            const float w = __builtin_amdgcn_exp2f(e.x - M);
-            const float4 v = po[sp * seg_stride * TPR];
-            O.x = fmaf(w, v.x, O.x);
-            O.y = fmaf(w, v.y, O.y);
-            O.z = fmaf(w, v.z, O.z);
-            O.w = fmaf(w, v.w, O.w);
-            Ls = fmaf(w, e.y, Ls);
+    for (int s0 = 0; s0 < n_valid; s0 += kMergeBatch) {
+        float2 e[kMergeBatch];
+        float4 v[kMergeBatch];
+#pragma unroll
+        for (int j = 0; j < kMergeBatch; ++j) {
+            if (s0 + j < n_valid) {
+                e[j] = ml[(size_t)(s0 + j) * seg_stride];
+                v[j] = po[(size_t)(s0 + j) * seg_stride * TPR];
+            } else {
+                e[j] = make_float2(-INFINITY, 0.f);
+                v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
         }
+        float bm = M;
+#pragma unroll
+        for (int j = 0; j < kMergeBatch; ++j) bm = fmaxf(bm, e[j].x);
+        if (bm == -INFINITY) continue;  // no valid key in the segments so far
+        const float corr = __builtin_amdgcn_exp2f(M - bm);  // 0 while M = -inf
+        O.x *= corr;
+        O.y *= corr;
+        O.z *= corr;
+        O.w *= corr;
+        Ls *= corr;
+#pragma unroll
+        for (int j = 0; j < kMergeBatch; ++j) {
+            const float w = __builtin_amdgcn_exp2f(e[j].x - bm);  // 0 for a segment past n_valid
+            O.x = fmaf(w, v[j].x, O.x);
+            O.y = fmaf(w, v[j].y, O.y);
+            O.z = fmaf(w, v[j].z, O.z);
+            O.w = fmaf(w, v[j].w, O.w);
+            Ls = fmaf(w, e[j].y, Ls);
+        }
+        M = bm;
     }
     const float inv = Ls > 0.f ? 1.f / Ls : 0.f;
     uint2 w;
