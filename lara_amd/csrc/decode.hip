@@ -432,13 +432,14 @@ __global__ __launch_bounds__(D) void decode_combine_kernel(DecodeArgs a) {
     if (d == 0 && a.lse != nullptr) a.lse[row] = Ls > 0.f ? (M + log2f(Ls)) * kLn2 : -INFINITY;
 }
 
-// Waves per split work-group.  Up to G = 4 a wave fits in 256 registers, so 8-wave
+// Waves per split work-group.  Up to G = 8 a wave fits in 256 registers, so 8-wave
 // work-groups keep two waves per SIMD and give one (sequence, kv head) twice the loads in
-// flight of a 4-wave one (ragged batches finish their long sequences sooner); G >= 8 needs
-// more than 256 registers per wave and keeps 4 waves.
+// flight of a 4-wave one (ragged batches finish their long sequences sooner, and a long
+// context is cut into half as many splits); G = 16 needs more than 256 registers per wave
+// and keeps 4 waves.
 template <int G>
 constexpr int decode_waves_t() {
-    return G <= 4 ? 8 : 4;
+    return G <= 8 ? 8 : 4;
 }
 
 template <int D, int G>
@@ -461,7 +462,9 @@ hipError_t launch_combine_t(const DecodeArgs& a, hipStream_t s) {
 
 }  // namespace
 
-int decode_waves(int group) { return group <= 4 ? decode_waves_t<4>() : decode_waves_t<8>(); }
+int decode_waves(int group) {
+    return group <= 4 ? decode_waves_t<4>() : group <= 8 ? decode_waves_t<8>() : decode_waves_t<16>();
+}
 
 bool decode_supported(int head_dim, int group) {
     return (head_dim == 64 || head_dim == 128) && (group == 2 || group == 4 || group == 8 || group == 16);
