@@ -297,8 +297,8 @@ int run_prefill(gqa_ctx* c, int32_t b, const void* q, int32_t q_len, int32_t q_p
     a.seg_len = plan.seg_len;
     a.n_segs = plan.n_segs;
     a.zero_row = c->zero_row;
-    a.part_o = c->pre_ws;
-    a.part_ml = c->pre_ws + (size_t)plan.n_segs * c->cfg.n_q_heads * q_len * c->cfg.head_dim;
+    a.part_o = reinterpret_cast<uint16_t*>(c->pre_ws);
+    a.part_ml = c->pre_ws + (size_t)plan.n_segs * c->cfg.n_q_heads * q_len * (c->cfg.head_dim / 2);
     timer_begin(c, GQA_TIMER_PREFILL, s);
     HIP_TRY(launch_prefill(c->cfg.head_dim, c->group, a, s));
     timer_end(c, GQA_TIMER_PREFILL, s);

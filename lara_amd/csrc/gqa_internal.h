@@ -59,8 +59,8 @@ struct PrefillArgs {
     float* lse;             // [H_q][q_len] or nullptr
     int32_t seg_len;        // keys per KV segment (multiple of 64)
     int32_t n_segs;         // KV segments (grid z); 1 = write the output directly
-    float* part_o;          // [n_segs][H_q][q_len][D] fp32 un-normalised partial O
-    float* part_ml;         // [n_segs][H_q][q_len][2] (running max in log2 units, sum)
+    uint16_t* part_o;       // [n_segs][H_q][q_len][D] fp16 words: the segment's O / l divided by `scale`
+    float* part_ml;         // [n_segs][H_q][q_len][4] (running max in log2 units, sum l, scale, unused)
     const uint16_t* zero_row;  // >= D zero words: the source of K/V rows past kv_len
     // Paged cache: block_table is sequence b's row of page indices (-1 = unmapped, read as
     // zero_row, never written), kc/vc the pools [n_pages][H_kv][2^page_shift][D]; nullptr =

@@ -46,6 +46,7 @@ namespace {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBN = 64;     // keys per block
 constexpr int kRows = 32;   // query rows per wave
@@ -56,6 +57,14 @@ constexpr float kLn2 = 0.693147180559945309f;
 __device__ __forceinline__ f32x16 mfma32(const u32x4& a, const u32x4& b, const f32x16& c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
                                                    c, 0, 0, 0);
+}
+
+// The value lane l ^ 32 holds (the other half-wave of the row), without an LDS round trip:
+// v_permlane32_swap leaves lanes 0-31 of its second result and lanes 32-63 of its first
+// holding the opposite half's values.  `half` is the lane's half-wave (lane / 32).
+__device__ __forceinline__ float half_swap(float x, int half) {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(half ? sw[0] : sw[1]);
 }
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
@@ -472,19 +481,34 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
     }
 
     if (!row_ok) return;
-    const float l_row = l_lane + __shfl_xor(l_lane, 32);
+    const float l_row = l_lane + half_swap(l_lane, half);
     if (a.n_segs > 1) {
         // Rows this wave never reached in the segment are not read by the merge.
         if (seg_begin >= wave_hi) return;
+        // The segment's O / l in fp16, divided by the row's largest |O / l| so every dim keeps
+        // 11 significant bits relative to the row (a bf16 ulp is 8), and (m, l, scale) in fp32:
+        // half the bytes of an fp32 partial, written here and read once by the merge.
         const size_t prow = ((size_t)blockIdx.z * a.n_q_heads + hq) * a.q_len + row;
-        float* po = a.part_o + prow * D;
+        float amax = 0.f;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-            for (int r4 = 0; r4 < 4; ++r4)
-                *reinterpret_cast<float4*>(po + mt * 32 + 8 * r4 + 4 * half) =
-                    make_float4(o[mt][4 * r4 + 0], o[mt][4 * r4 + 1], o[mt][4 * r4 + 2], o[mt][4 * r4 + 3]);
-        if (half == 0) *reinterpret_cast<float2*>(a.part_ml + prow * 2) = make_float2(m_run, l_row);
+            for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(o[mt][i]));
+        amax = fmaxf(amax, half_swap(amax, half));  // the row's other half-wave
+        // The merge rebuilds O_s as l * scale * (o * k) = o * amax * k: k only has to be close
+        // to 1 / amax (so o * k stays within fp16 range), not exact.
+        const float k = amax > 0.f ? __builtin_amdgcn_rcpf(amax) : 0.f;
+        const float scale = l_row > 0.f && amax > 0.f ? amax / l_row : 1.f;
+        uint16_t* po = a.part_o + prow * D;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const f16x4 w = {(_Float16)(o[mt][4 * r4 + 0] * k), (_Float16)(o[mt][4 * r4 + 1] * k),
+                                 (_Float16)(o[mt][4 * r4 + 2] * k), (_Float16)(o[mt][4 * r4 + 3] * k)};
+                *reinterpret_cast<uint2*>(po + mt * 32 + 8 * r4 + 4 * half) = __builtin_bit_cast(uint2, w);
+            }
+        if (half == 0) *reinterpret_cast<float4*>(a.part_ml + prow * 4) = make_float4(m_run, l_row, scale, 0.f);
         return;
     }
     const float inv = l_row > 0.f ? 1.f / l_row : 0.f;
@@ -505,8 +529,8 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
 // Merge of a row's KV segments.  Segment s holds keys [s*seg_len, (s+1)*seg_len); a row
 // reads the segments below its own key limit, which are exactly the ones prefill_kernel
 // wrote for it.  A work-group merges kMergeRows rows of one query head; each row is handled
-// by D/4 threads owning four dims (16-byte loads).  The (m, l) pairs and O slices of up to
-// kMergeBatch segments are loaded together, so a row pays one memory latency per batch.
+// by D/4 threads owning four dims (8-byte fp16 loads).  The (m, l, scale) rows and O slices of
+// up to kMergeBatch segments are loaded together, so a row pays one memory latency per batch.
 constexpr int kMergeRows = 8;
 constexpr int kMergeBatch = 8;
 
@@ -523,21 +547,22 @@ __global__ __launch_bounds__(kMergeRows * D / 4) void prefill_combine_kernel(Pre
     const int n_valid = min(a.n_segs, (hi + a.seg_len - 1) / a.seg_len);
     const size_t seg_stride = (size_t)a.n_q_heads * a.q_len;
     const size_t prow = (size_t)hq * a.q_len + row;
-    const float2* ml = reinterpret_cast<const float2*>(a.part_ml) + prow;
-    const float4* po = reinterpret_cast<const float4*>(a.part_o) + prow * TPR + d4;
+    const float4* ml = reinterpret_cast<const float4*>(a.part_ml) + prow;
+    const uint2* po = reinterpret_cast<const uint2*>(a.part_o) + prow * TPR + d4;
     float M = -INFINITY;  // running max over the merged segments (log2 units)
     float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
     float Ls = 0.f;
     for (int s0 = 0; s0 < n_valid; s0 += kMergeBatch) {
-        float2 e[kMergeBatch];
-        float4 v[kMergeBatch];
+        float4 e[kMergeBatch];  // (m, l, scale, -) of the segment
+        float4 v[kMergeBatch];  // four dims of the segment's O / l / scale
 #pragma unroll
         for (int j = 0; j < kMergeBatch; ++j) {
             if (s0 + j < n_valid) {
                 e[j] = ml[(size_t)(s0 + j) * seg_stride];
-                v[j] = po[(size_t)(s0 + j) * seg_stride * TPR];
+                const f16x4 h = __builtin_bit_cast(f16x4, po[(size_t)(s0 + j) * seg_stride * TPR]);
+                v[j] = make_float4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
             } else {
-                e[j] = make_float2(-INFINITY, 0.f);
+                e[j] = make_float4(-INFINITY, 0.f, 0.f, 0.f);
                 v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
             }
         }
@@ -553,12 +578,13 @@ __global__ __launch_bounds__(kMergeRows * D / 4) void prefill_combine_kernel(Pre
         Ls *= corr;
 #pragma unroll
         for (int j = 0; j < kMergeBatch; ++j) {
-            const float w = __builtin_amdgcn_exp2f(e[j].x - bm);  // 0 for a segment past n_valid
+            const float wl = __builtin_amdgcn_exp2f(e[j].x - bm) * e[j].y;  // 0 for a segment past n_valid
+            const float w = wl * e[j].z;                                    // O_s = l * scale * v
             O.x = fmaf(w, v[j].x, O.x);
             O.y = fmaf(w, v[j].y, O.y);
             O.z = fmaf(w, v[j].z, O.z);
             O.w = fmaf(w, v[j].w, O.w);
-            Ls = fmaf(w, e[j].y, Ls);
+            Ls += wl;
         }
         M = bm;
     }
@@ -599,7 +625,7 @@ PrefillPlan plan_prefill(int q_len, int kv_span, int group, int n_kv_heads, int 
 
 size_t prefill_workspace_floats(const PrefillPlan& p, int q_len, int n_q_heads, int head_dim) {
     if (p.n_segs <= 1) return 0;
-    return (size_t)p.n_segs * n_q_heads * q_len * (head_dim + 2);
+    return (size_t)p.n_segs * n_q_heads * q_len * (head_dim / 2 + 4);  // fp16 O row + (m, l, scale, -)
 }
 
 hipError_t launch_prefill_combine(int head_dim, const PrefillArgs& a, hipStream_t s) {
