@@ -220,3 +220,28 @@ def test_prefill_segmentation_invariance(wgs):
         out, lse = acc.prefill_chunk(q, q_pos_base=kv_len - q_len, kv_len=kv_len, return_lse=True)
     ref, ref_lse = oracle_for(q, k, v, causal=True, q_pos_base=kv_len - q_len)
     check_rows(out, lse, ref, ref_lse)
+
+
+@pytest.mark.parametrize("v_scale", [1e30, 1e-30, "mixed"])
+def test_segment_partials_at_extreme_magnitudes(v_scale):
+    """KV segments hand their rows to the merge as fp16 O / l divided by the row's largest
+    |O / l|: outputs of very large or very small magnitude, and rows mixing both, keep the
+    2-ulp bound with many segments."""
+    rng = np.random.default_rng(500 if v_scale == "mixed" else int(np.log10(v_scale)) + 600)
+    q_len, kv_len = 128, 1024
+    q = bf16_normal(rng, (32, q_len, 128))
+    k = bf16_normal(rng, (8, kv_len, 128))
+    if v_scale == "mixed":
+        v32 = rng.standard_normal((8, kv_len, 128), dtype=np.float32)
+        v32[:, ::7] *= np.float32(1e20)  # every 7th key's row dominates the rows that see it
+        v = orc.fp32_to_bf16_u16(v32)
+    else:
+        v = bf16_normal(rng, (8, kv_len, 128), v_scale)
+    with AttentionAccelerator(max_seq_len=kv_len, max_q_len=q_len) as acc:
+        from lara_amd import _lib
+        _lib.check(acc._lib.gqa_set_option(acc._ctx, _lib.GQA_OPT_PREFILL_WGS, 1024), "prefill wgs")
+        acc.load_kv(k, v)
+        out, lse = acc.prefill_chunk(q, q_pos_base=kv_len - q_len, kv_len=kv_len, return_lse=True)
+    assert np.all(np.isfinite(drv.bf16_u16_to_fp32(out)))
+    ref, ref_lse = oracle_for(q, k, v, causal=True, q_pos_base=kv_len - q_len)
+    check_rows(out, lse, ref, ref_lse)
