@@ -54,13 +54,14 @@ extern "C" {
 /* Per-kernel timer slots reported by gqa_kernel_times. */
 #define GQA_TIMER_APPEND  0
 #define GQA_TIMER_DECODE  1
-#define GQA_TIMER_COMBINE 2 /* split-KV merge launched on its own (prefill); decode merges in-kernel */
+#define GQA_TIMER_COMBINE 2 /* log-sum-exp merge launch of split-KV decode or segmented prefill */
 #define GQA_TIMER_PREFILL 3
 #define GQA_TIMER_COUNT   4
 
 /* Tunables for gqa_set_option. */
 #define GQA_OPT_DECODE_CHUNK 1 /* keys per split-KV work-group (multiple of 64; 0 = auto) */
-#define GQA_OPT_PROFILE      2 /* 1 = time every kernel launch with HIP events (restarts the record) */
+#define GQA_OPT_PROFILE      2 /* 1 = time every kernel launch with HIP events (restarts the record);
+                                  each event pair idles the GPU ~10 us between launches */
 #define GQA_OPT_PREFILL_WGS  3 /* prefill work-groups the KV segmentation aims for (0 = auto, 1 = none) */
 #define GQA_OPT_NUMERICS     4 /* GQA_NUMERICS_*: arithmetic of prefill / transactions (decode: EXACT only) */
 
