@@ -825,7 +825,7 @@ class AttentionAccelerator:
         ``rms_weight`` (gamma, [hidden]) or None for no normalisation.  All are packed to bf16
         words like the transaction inputs (uint16 passes through).  The reference runs these
         steps on the host through its ``host_attention`` module; here they run on the GPU
-        (RMSNorm and RoPE kernels around a rocBLAS bf16 GEMM with fp32 accumulation) and write
+        (RMSNorm and RoPE kernels around a hipBLASLt bf16 GEMM with fp32 accumulation) and write
         Q and the cache directly.  ``rms_eps`` and ``rope`` extend the reference signature.
         Returns fp32 [L, H_q*D] (``bf16_u16_to_fp32(o).transpose(1, 0, 2).reshape(L, -1)``).
         The RunProfile fields host_rms_norm_ms / host_qkv_projection_ms / host_rope_ms hold

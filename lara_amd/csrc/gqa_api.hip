@@ -5,7 +5,7 @@
 #include "page_table.h"
 
 #include <math.h>
-#include <rocblas/rocblas.h>
+#include <hipblaslt/hipblaslt.h>
 
 #include <algorithm>
 #include <stdio.h>
@@ -30,6 +30,18 @@ struct Txn {
 };
 
 }  // namespace
+
+// One projection GEMM shape, D[rows x n_tokens] (leading dimension ld) = W^T X with W stored
+// [rows][hidden] and X [n_tokens][hidden] (column-major: W is hidden x rows, X hidden x
+// n_tokens), bf16 in and out, fp32 accumulation: the hipBLASLt descriptors and the algorithm
+// its heuristic ranks first among those that need no workspace.
+struct ProjectionPlan {
+    int rows = 0, n_tokens = 0, hidden = 0, ld = 0;
+    hipblasLtMatmulDesc_t desc = nullptr;
+    hipblasLtMatrixLayout_t w = nullptr, x = nullptr, d = nullptr;
+    hipblasLtMatmulAlgo_t algo{};
+};
+constexpr int kProjectionPlans = 8;
 
 struct gqa_ctx {
     gqa_config cfg{};
@@ -67,11 +79,13 @@ struct gqa_ctx {
     float last_us = 0.f;
     double clock_mhz = 0.0;
     Txn txn;
-    // Layer input stage (run_layer): rocBLAS handle and grow-only device workspaces, created on
-    // first use; ev_layer brackets RMSNorm, projection and RoPE of the last timed layer call
+    // Layer input stage (run_layer): hipBLASLt handle, projection plans and grow-only device
+    // workspaces, created on first use; ev_layer brackets RMSNorm, projection and RoPE of the last timed layer call
     // (every host-pointer call; a device call only while profiling is on, since each recorded
     // event leaves the GPU idle for several microseconds between the launches it separates).
-    rocblas_handle blas = nullptr;
+    hipblasLtHandle_t lt = nullptr;
+    ProjectionPlan proj[kProjectionPlans];  // per GEMM shape, reused in turn
+    int proj_next = 0;
     uint8_t* layer_in = nullptr;   // host-entry uploads: x, Wq, Wk, Wv, gamma
     size_t layer_in_bytes = 0;
     uint8_t* layer_tmp = nullptr;  // normalised x, then the [n_tokens][Q|K|V] projection
@@ -362,8 +376,63 @@ int check_layer_args(const gqa_ctx* c, int32_t b, int32_t n_tokens, int32_t hidd
     return GQA_OK;
 }
 
-// RMSNorm (if gamma) -> [Q|K|V] = x W^T (three rocBLAS bf16 GEMMs, fp32 accumulate) -> RoPE
-// (if rope) and scatter: Q to q_out [H_q][n_tokens][D], K/V to rows row0.. of sequence b.
+void release_plan(ProjectionPlan& p) {
+    if (p.w) (void)hipblasLtMatrixLayoutDestroy(p.w);
+    if (p.x) (void)hipblasLtMatrixLayoutDestroy(p.x);
+    if (p.d) (void)hipblasLtMatrixLayoutDestroy(p.d);
+    if (p.desc) (void)hipblasLtMatmulDescDestroy(p.desc);
+    p = ProjectionPlan();
+}
+
+// The cached plan for this projection shape, or a new one (replacing the oldest of
+// kProjectionPlans): descriptors plus the first algorithm of hipBLASLt's heuristic.
+int projection_plan(gqa_ctx* c, int rows, int n_tokens, int hidden, int ld, const ProjectionPlan** out) {
+    for (const ProjectionPlan& p : c->proj)
+        if (p.desc && p.rows == rows && p.n_tokens == n_tokens && p.hidden == hidden && p.ld == ld) {
+            *out = &p;
+            return GQA_OK;
+        }
+    ProjectionPlan& p = c->proj[c->proj_next];
+    c->proj_next = (c->proj_next + 1) % kProjectionPlans;
+    release_plan(p);
+    hipblasLtMatmulPreference_t pref = nullptr;
+    const hipblasOperation_t tw = HIPBLAS_OP_T, tx = HIPBLAS_OP_N;
+    const uint64_t no_workspace = 0;
+    hipblasLtMatmulHeuristicResult_t best{};
+    int found = 0;
+    hipblasStatus_t st = hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F);
+    if (st == HIPBLAS_STATUS_SUCCESS)
+        st = hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &tw, sizeof(tw));
+    if (st == HIPBLAS_STATUS_SUCCESS)
+        st = hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tx, sizeof(tx));
+    if (st == HIPBLAS_STATUS_SUCCESS) st = hipblasLtMatrixLayoutCreate(&p.w, HIP_R_16BF, hidden, rows, hidden);
+    if (st == HIPBLAS_STATUS_SUCCESS) st = hipblasLtMatrixLayoutCreate(&p.x, HIP_R_16BF, hidden, n_tokens, hidden);
+    if (st == HIPBLAS_STATUS_SUCCESS) st = hipblasLtMatrixLayoutCreate(&p.d, HIP_R_16BF, rows, n_tokens, ld);
+    if (st == HIPBLAS_STATUS_SUCCESS) st = hipblasLtMatmulPreferenceCreate(&pref);
+    if (st == HIPBLAS_STATUS_SUCCESS)
+        st = hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &no_workspace,
+                                                   sizeof(no_workspace));
+    if (st == HIPBLAS_STATUS_SUCCESS)
+        st = hipblasLtMatmulAlgoGetHeuristic(c->lt, p.desc, p.w, p.x, p.d, p.d, pref, 1, &best, &found);
+    if (pref) (void)hipblasLtMatmulPreferenceDestroy(pref);
+    if (st != HIPBLAS_STATUS_SUCCESS || found < 1 || best.state != HIPBLAS_STATUS_SUCCESS) {
+        snprintf(g_last_error, sizeof(g_last_error), "hipBLASLt projection plan %dx%dx%d: status %d, %d algorithms",
+                 rows, n_tokens, hidden, (int)st, found);
+        release_plan(p);
+        return GQA_ERR_HIP;
+    }
+    p.algo = best.algo;
+    p.rows = rows;
+    p.n_tokens = n_tokens;
+    p.hidden = hidden;
+    p.ld = ld;
+    *out = &p;
+    return GQA_OK;
+}
+
+// RMSNorm (if gamma) -> [Q|K|V] = x W^T (one fused or three hipBLASLt bf16 GEMMs, fp32
+// accumulate) -> RoPE (if rope) and scatter: Q to q_out [H_q][n_tokens][D], K/V to rows
+// row0.. of sequence b.
 int run_layer_qkv(gqa_ctx* c, int32_t b, const void* x, int32_t n_tokens, int32_t hidden, const void* wq,
                   const void* wk, const void* wv, const void* gamma, float eps, int32_t q_pos_base,
                   int32_t kv_pos_base, int32_t row0, int32_t rope, void* q_out, hipStream_t s, bool timed) {
@@ -372,11 +441,11 @@ int run_layer_qkv(gqa_ctx* c, int32_t b, const void* x, int32_t n_tokens, int32_
     const size_t y_bytes = gamma ? ((size_t)n_tokens * hidden * 2 + 255) / 256 * 256 : 0;
     int rc = ensure_buffer(&c->layer_tmp, &c->layer_tmp_bytes, y_bytes + (size_t)n_tokens * ld * 2);
     if (rc != GQA_OK) return rc;
-    if (!c->blas) {
-        rocblas_status st = rocblas_create_handle(&c->blas);
-        if (st != rocblas_status_success) {
-            c->blas = nullptr;
-            snprintf(g_last_error, sizeof(g_last_error), "rocblas_create_handle: %s", rocblas_status_to_string(st));
+    if (!c->lt) {
+        const hipblasStatus_t st = hipblasLtCreate(&c->lt);
+        if (st != HIPBLAS_STATUS_SUCCESS) {
+            c->lt = nullptr;
+            snprintf(g_last_error, sizeof(g_last_error), "hipblasLtCreate: status %d", (int)st);
             return GQA_ERR_HIP;
         }
     }
@@ -399,7 +468,6 @@ int run_layer_qkv(gqa_ctx* c, int32_t b, const void* x, int32_t n_tokens, int32_
     }
     HIP_TRY(mark(1));
     uint16_t* qkv = (uint16_t*)(c->layer_tmp + y_bytes);
-    rocblas_status st = rocblas_set_stream(c->blas, s);
     const float one = 1.f, zero = 0.f;
     const void* ws[3] = {wq, wk, wv};
     int rows[3] = {nq, nkv, nkv}, off[3] = {0, nq, nq + nkv};
@@ -411,16 +479,16 @@ int run_layer_qkv(gqa_ctx* c, int32_t b, const void* x, int32_t n_tokens, int32_
         rows[0] = ld;
         n_gemm = 1;
     }
-    for (int i = 0; i < n_gemm && st == rocblas_status_success; ++i) {
-        // Column-major view: C[rows x n_tokens] (ld) = W[hidden x rows]^T . X[hidden x n_tokens].
-        st = rocblas_gemm_ex(c->blas, rocblas_operation_transpose, rocblas_operation_none, rows[i], n_tokens, hidden,
-                             &one, ws[i], rocblas_datatype_bf16_r, hidden, src, rocblas_datatype_bf16_r, hidden,
-                             &zero, qkv + off[i], rocblas_datatype_bf16_r, ld, qkv + off[i],
-                             rocblas_datatype_bf16_r, ld, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
-    }
-    if (st != rocblas_status_success) {
-        snprintf(g_last_error, sizeof(g_last_error), "rocblas_gemm_ex: %s", rocblas_status_to_string(st));
-        return GQA_ERR_HIP;
+    for (int i = 0; i < n_gemm; ++i) {
+        const ProjectionPlan* p = nullptr;
+        rc = projection_plan(c, rows[i], n_tokens, hidden, ld, &p);
+        if (rc != GQA_OK) return rc;
+        const hipblasStatus_t st = hipblasLtMatmul(c->lt, p->desc, &one, ws[i], p->w, src, p->x, &zero, qkv + off[i],
+                                                   p->d, qkv + off[i], p->d, &p->algo, nullptr, 0, s);
+        if (st != HIPBLAS_STATUS_SUCCESS) {
+            snprintf(g_last_error, sizeof(g_last_error), "hipblasLtMatmul: status %d", (int)st);
+            return GQA_ERR_HIP;
+        }
     }
     HIP_TRY(mark(2));
     RopeArgs ra{};
@@ -668,7 +736,8 @@ int gqa_destroy(gqa_ctx* c) {
     }
     for (int i = 0; i < 4; ++i)
         if (c->ev_t[i]) (void)hipEventDestroy(c->ev_t[i]);
-    if (c->blas) (void)rocblas_destroy_handle(c->blas);
+    for (ProjectionPlan& p : c->proj) release_plan(p);
+    if (c->lt) (void)hipblasLtDestroy(c->lt);
     (void)hipFree(c->layer_in);
     (void)hipFree(c->layer_tmp);
     for (int i = 0; i < 4; ++i)
