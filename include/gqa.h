@@ -237,7 +237,8 @@ int gqa_cache_pointers(gqa_ctx* ctx, void** k_cache, void** v_cache, int32_t* l_
  * the transaction's staging and K/V into rows [0, n_tokens) of sequence b, and leaves a
  * transaction (q_len = kv_len = n_tokens) for gqa_start / gqa_wait / gqa_read_output.
  * gqa_layer_qkv_device does the same from device memory without a transaction: Q goes to
- * q_out ([H_q][n_tokens][D]), K/V to rows [kv_row0, kv_row0 + n_tokens) of sequence b; it
+ * q_out ([H_q][n_tokens][D], 16-byte aligned, else GQA_ERR_RANGE), K/V to rows
+ * [kv_row0, kv_row0 + n_tokens) of sequence b; it
  * allocates its workspace on first use.  gqa_layer_times returns the device time in us of
  * the RMSNorm, projection and RoPE stages (n <= 3; synchronises) of the last gqa_submit_layer
  * call, or of the last gqa_layer_qkv_device call made while GQA_OPT_PROFILE is on (stage events

@@ -372,7 +372,7 @@ int check_layer_args(const gqa_ctx* c, int32_t b, int32_t n_tokens, int32_t hidd
     if (q_pos_base < 0 || kv_pos_base < 0 || (int64_t)q_pos_base + n_tokens > (1 << 24) ||
         (int64_t)kv_pos_base + n_tokens > (1 << 24))
         return GQA_ERR_RANGE;  // positions are exact in the fp32 phase product below 2^24
-    if (c->cfg.head_dim > 2 * kMaxRopePairs || (c->cfg.head_dim & 1)) return GQA_ERR_UNSUPPORTED;
+    if (c->cfg.head_dim > 2 * kMaxRopePairs || (c->cfg.head_dim & 7)) return GQA_ERR_UNSUPPORTED;
     return GQA_OK;
 }
 
@@ -1161,7 +1161,7 @@ int gqa_layer_qkv_device(gqa_ctx* c, int32_t b, const void* x, int32_t n_tokens,
                          const void* wk, const void* wv, const void* rms_weight, float rms_eps, int32_t q_pos_base,
                          int32_t kv_pos_base, int32_t kv_row0, int32_t rope, void* q_out, void* stream) {
     if (!c || !x || !wq || !wk || !wv || !q_out) return GQA_ERR_NULL;
-    if (reinterpret_cast<uintptr_t>(q_out) & 3) return GQA_ERR_RANGE;  // Q is written as bf16 pairs
+    if (reinterpret_cast<uintptr_t>(q_out) & 15) return GQA_ERR_RANGE;  // Q is written in 16-byte chunks
     int rc = txn_idle(c);
     if (rc != GQA_OK) return rc;
     rc = check_layer_args(c, b, n_tokens, hidden, q_pos_base, kv_pos_base, kv_row0);

@@ -95,52 +95,52 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(NormArgs a) {
     }
 }
 
-constexpr int kRopeHeadsPerBlock = 8;
+constexpr int kRopeThreads = 256;
 
 // grid (n_tokens, ceil((H_q + 2 H_kv) / 8)); one wave per block, one lane per (2p, 2p+1)
 // pair.  A lane evaluates cos/sin once for the Q position and once for the K position, loads
 // its pair of all 8 heads (each head row is D*2 contiguous bytes across the wave) before
 // rotating and storing them.
-__global__ __launch_bounds__(kMaxRopePairs) void rope_scatter_kernel(RopeArgs a) {
-    const int t = blockIdx.x, p = threadIdx.x;
-    const int D = a.head_dim;
+// One work-group per token: the (position, pair) cos/sin values are computed once into LDS,
+// then the token's H_q + 2 H_kv head rows move in 16-byte chunks (four pairs per thread and
+// chunk; a thread's pairs are the same in every head, as 256 is a multiple of D / 8).
+__global__ __launch_bounds__(kRopeThreads) void rope_scatter_kernel(RopeArgs a) {
+    __shared__ float cs[2][kMaxRopePairs][2];  // [Q position | K position][pair][cos, sin]
+    const int t = blockIdx.x;
+    const int D = a.head_dim, P = D / 2, CPH = D / 8;  // pairs and 16-byte chunks per head row
     const int H = a.n_q_heads + 2 * a.n_kv_heads;
-    const int h0 = blockIdx.y * kRopeHeadsPerBlock;
-    const uint32_t* src = (const uint32_t*)(a.qkv + (size_t)t * a.ld) + p;
-    uint32_t w[kRopeHeadsPerBlock];
-#pragma unroll
-    for (int i = 0; i < kRopeHeadsPerBlock; ++i)
-        w[i] = (h0 + i < H) ? __builtin_nontemporal_load(src + (size_t)(h0 + i) * (D / 2)) : 0u;
-    float cq = 1.f, sq = 0.f, ck = 1.f, sk = 0.f;
+    const bool same_pos = a.kv_pos_base == a.q_pos_base;
     if (a.rope) {
-        // Each product and sum is rounded to fp32 on its own: no fused multiply-add.
+        for (int i = threadIdx.x; i < 2 * P; i += kRopeThreads) {
+            const int which = i / P, p = i - which * P;  // 0: the Q position, 1: the K position
+            if (which == 1 && same_pos) continue;
+            {
 #pragma clang fp contract(off)
-        double sd, cd;
-        sincos((double)((float)(a.q_pos_base + t) * a.theta[p]), &sd, &cd);
-        sq = (float)sd;
-        cq = (float)cd;
-        if (a.kv_pos_base == a.q_pos_base) {
-            sk = sq;
-            ck = cq;
-        } else {
-            sincos((double)((float)(a.kv_pos_base + t) * a.theta[p]), &sd, &cd);
-            sk = (float)sd;
-            ck = (float)cd;
+                double sd, cd;
+                sincos((double)((float)((which ? a.kv_pos_base : a.q_pos_base) + t) * a.theta[p]), &sd, &cd);
+                cs[which][p][0] = (float)cd;
+                cs[which][p][1] = (float)sd;
+            }
         }
+        __syncthreads();
     }
-#pragma unroll
-    for (int i = 0; i < kRopeHeadsPerBlock; ++i) {
-        const int h = h0 + i;
-        if (h >= H) break;
-        uint32_t out = w[i];
+    const u32x4* src = reinterpret_cast<const u32x4*>(a.qkv + (size_t)t * a.ld);
+    for (int ci = threadIdx.x; ci < H * CPH; ci += kRopeThreads) {
+        const int h = ci / CPH, cw = ci - h * CPH;
+        u32x4 w = __builtin_nontemporal_load(src + ci);
         const bool is_q = h < a.n_q_heads, is_k = !is_q && h < a.n_q_heads + a.n_kv_heads;
         if (a.rope && (is_q || is_k)) {
+            const int which = (is_k && !same_pos) ? 1 : 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
 #pragma clang fp contract(off)
-            const float c = is_q ? cq : ck, s = is_q ? sq : sk;
-            const float x0 = bf16_to_f32(w[i] & 0xFFFFu), x1 = bf16_to_f32(w[i] >> 16);
-            const float r0 = x0 * c - x1 * s;
-            const float r1 = x0 * s + x1 * c;
-            out = (uint32_t)f32_to_bf16_rne(r0) | ((uint32_t)f32_to_bf16_rne(r1) << 16);
+                // Each product and sum is rounded to fp32 on its own: no fused multiply-add.
+                const float c = cs[which][4 * cw + j][0], s = cs[which][4 * cw + j][1];
+                const float x0 = bf16_to_f32(w[j] & 0xFFFFu), x1 = bf16_to_f32(w[j] >> 16);
+                const float r0 = x0 * c - x1 * s;
+                const float r1 = x0 * s + x1 * c;
+                w[j] = (uint32_t)f32_to_bf16_rne(r0) | ((uint32_t)f32_to_bf16_rne(r1) << 16);
+            }
         }
         uint16_t* dst;
         if (is_q) {
@@ -154,7 +154,7 @@ __global__ __launch_bounds__(kMaxRopePairs) void rope_scatter_kernel(RopeArgs a)
             }
             dst = (is_k ? a.kc : a.vc) + (size_t)r * D;
         }
-        *(uint32_t*)(dst + 2 * p) = out;
+        *reinterpret_cast<u32x4*>(dst + 8 * cw) = w;
     }
 }
 
@@ -168,10 +168,9 @@ hipError_t launch_rms_norm(const NormArgs& a, hipStream_t s) {
 
 hipError_t launch_rope_scatter(const RopeArgs& a, hipStream_t s) {
     if (a.n_tokens < 1) return hipSuccess;
-    if (a.head_dim < 2 || a.head_dim > 2 * kMaxRopePairs || (a.head_dim & 1)) return hipErrorInvalidValue;
-    const int heads = a.n_q_heads + 2 * a.n_kv_heads;
-    hipLaunchKernelGGL(rope_scatter_kernel, dim3(a.n_tokens, (heads + kRopeHeadsPerBlock - 1) / kRopeHeadsPerBlock),
-                       dim3(a.head_dim / 2), 0, s, a);
+    if (a.head_dim < 8 || a.head_dim > 2 * kMaxRopePairs || (a.head_dim & 7) || kRopeThreads % (a.head_dim / 8))
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rope_scatter_kernel, dim3(a.n_tokens), dim3(kRopeThreads), 0, s, a);
     return hipGetLastError();
 }
 
