@@ -55,14 +55,16 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(NormArgs a) {
                                                reinterpret_cast<uintptr_t>(a.y)) & 15) == 0;
     constexpr int kStep = kNormThreads * 8;
     float ss = 0.f;
-    u32x4 cache[kNormCached];
+    u32x4 cache[kNormCached], gcache[kNormCached];  // x and gamma chunks, gamma loaded with x
     if (vec) {
 #pragma unroll
         for (int c = 0; c < kNormCached; ++c) {
             const int i = c * kStep + threadIdx.x * 8;
             cache[c] = i < a.hidden ? __builtin_nontemporal_load((const u32x4*)(x + i)) : u32x4{0u, 0u, 0u, 0u};
-            ss += sum_squares(cache[c]);
+            gcache[c] = i < a.hidden ? *(const u32x4*)(a.gamma + i) : u32x4{0u, 0u, 0u, 0u};
         }
+#pragma unroll
+        for (int c = 0; c < kNormCached; ++c) ss += sum_squares(cache[c]);
         for (int i = kNormCached * kStep + threadIdx.x * 8; i < a.hidden; i += kStep)
             ss += sum_squares(*(const u32x4*)(x + i));
     } else {
@@ -85,7 +87,7 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(NormArgs a) {
 #pragma unroll
         for (int c = 0; c < kNormCached; ++c) {
             const int i = c * kStep + threadIdx.x * 8;
-            if (i < a.hidden) *(u32x4*)(y + i) = scale_row(cache[c], *(const u32x4*)(a.gamma + i), inv);
+            if (i < a.hidden) *(u32x4*)(y + i) = scale_row(cache[c], gcache[c], inv);
         }
         for (int i = kNormCached * kStep + threadIdx.x * 8; i < a.hidden; i += kStep)
             *(u32x4*)(y + i) = scale_row(*(const u32x4*)(x + i), *(const u32x4*)(a.gamma + i), inv);
