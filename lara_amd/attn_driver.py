@@ -920,8 +920,8 @@ class AttentionAccelerator:
                          kv_pos_base: int = 0, kv_row0: int = 0, rms_eps: float = RMS_NORM_EPS, rope: bool = True,
                          stream: int | None = None) -> None:
         """Device-pointer layer input stage (``gqa_layer_qkv_device``): Q to ``q_out_ptr``
-        ([H_q, n_tokens, D] bf16), K/V into rows kv_row0.. of sequence ``b``; enqueued, not
-        synchronised."""
+        ([H_q, n_tokens, D] bf16, 16-byte aligned), K/V into rows kv_row0.. of sequence ``b``;
+        enqueued, not synchronised."""
         self._ensure_open()
         self._call("gqa_layer_qkv_device", int(b), ctypes.c_void_p(x_ptr), int(n_tokens), int(hidden),
                    ctypes.c_void_p(wq_ptr), ctypes.c_void_p(wk_ptr), ctypes.c_void_p(wv_ptr),
