@@ -205,17 +205,17 @@ class DecodeBench:
 
 
 LAUNCH_BOUND = ("c1", "c2")  # workloads whose step is also timed as a replayed HIP graph
-PAGED_SUFFIX = "_paged"  # a decode workload over a paged cache of 64-row pages
+PAGED_SUFFIX = "_paged"  # a decode workload over a paged cache (64-row pages unless --page-rows)
 PAGE_ROWS = 64
 
 
-def measure(name: str, steps: int, warmup: int, chunk: int = 0) -> dict:
+def measure(name: str, steps: int, warmup: int, chunk: int = 0, page_rows: int = PAGE_ROWS) -> dict:
     from lara_amd.benchmark import WORKLOADS, decode_kernel_bytes, decode_step_bytes, HBM_PEAK_GBPS
 
     paged = name.endswith(PAGED_SUFFIX)
     w = WORKLOADS[name[: -len(PAGED_SUFFIX)] if paged else name]
     log(f"{name}: filling HBM cache")
-    bench = DecodeBench(w, chunk=chunk, page_size=PAGE_ROWS if paged else 0)
+    bench = DecodeBench(w, chunk=chunk, page_size=page_rows if paged else 0)
     try:
         log(f"{name}: warmup {warmup}, timing {steps} steps")
         r = bench.run(steps, warmup)
@@ -738,6 +738,8 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--workload", default="ns", choices=sorted(WORKLOAD_NAMES))
     parser.add_argument("--chunk", type=int, default=0, help="keys per split-KV work-group (0 = auto)")
+    parser.add_argument("--page-rows", type=int, default=PAGE_ROWS,
+                        help="rows per page of the paged-cache workloads (power of two, >= 64)")
     parser.add_argument("--prefill-wgs", type=int, default=0,
                         help="work-groups the prefill KV segmentation aims for (0 = auto, 1 = no segments)")
     parser.add_argument("--others", default="c2,c3,c4,c5,p8k,layer,ns_paged", help="extra decode workloads to report ('' = none)")
@@ -779,7 +781,7 @@ def main() -> int:
         return copy_calibration(args.calibrate_copy_mib)
     if args.board_matrix:
         return board_matrix(args)
-    main_r = measure(args.workload, args.steps, args.warmup, args.chunk)
+    main_r = measure(args.workload, args.steps, args.warmup, args.chunk, args.page_rows)
     others = {}
     for name in [x for x in args.others.split(",") if x and x != args.workload]:
         if name == "c5":
@@ -791,7 +793,7 @@ def main() -> int:
         if name == "layer":
             others[name] = measure_layer(name, max(10, args.steps // 4), max(2, args.warmup // 2), args.prefill_wgs)
             continue
-        r = measure(name, max(10, args.steps // 2), max(2, args.warmup // 2))
+        r = measure(name, max(10, args.steps // 2), max(2, args.warmup // 2), page_rows=args.page_rows)
         others[name] = {k: r[k] for k in ("us_per_step", "step_gbps", "step_frac_of_peak", "decode_us",
                                            "decode_kernel_gbps", "decode_isolated_us", "decode_launches_per_step",
                                            "tokens_per_s", "graph_us_per_step") if k in r}
