@@ -204,7 +204,7 @@ def test_fused_append_decode_matches_two_launches(hq, hkv, d):
     """decode_step with rows = append_kv + decode_step, bit for bit, over repeated steps.
 
     A small split size gives many splits per sequence, so every step exercises the
-    in-kernel merge and the reset of its arrival counters for the next launch.
+    combine launch and the split that reads the appended row from k_new/v_new.
     """
     rng = np.random.default_rng(200 + hq + d)
     B = 3
