@@ -14,8 +14,9 @@ timed steps (no per-launch events in them); ``roofline`` describes the dominant 
 split-KV decode kernel, the step's only launch) from the HIP events that bracket the timed
 steps on its stream, with the average of per-launch events over a second pass of the same
 steps beside it; ``cpu_baseline`` times the fp32 NumPy oracle on the host on a bounded
-sample of the same workload.  Other workloads (decode C2, C3, C4, paged NS; chunked prefill;
-one-shot prefill; the layer input stage) are measured the same way and reported under
+sample of the same workload.  Other workloads (batch-1 context-4097, ragged batch-64 and
+batch-4 context-131072 decode, the default decode on a paged cache; chunked prefill; one-shot
+prefill; the layer input stage) are measured the same way and reported under
 ``other_workloads``.
 """
 from __future__ import annotations
@@ -34,13 +35,13 @@ import numpy as np
 
 ROOT = Path(__file__).resolve().parent
 METRIC = "GQA decode µs/step + achieved HBM GB/s (% of peak) at 1 MI355X"
-PROFILE_TRAFFIC = ROOT / "profiles" / "decode_ns_hbm_traffic.txt"
+PROFILE_TRAFFIC = ROOT / "profiles" / "decode_b64_ctx8192_hbm_traffic.txt"
 WORKLOAD_NAMES = {
-    "ns": "llama3-8b-gqa-decode-b64-ctx8192",
-    "c2": "llama3-8b-gqa-decode-b1-ctx4096+1",
-    "c3": "llama3-8b-gqa-decode-b64-ragged-512..8192",
-    "c4": "long-context-gqa-decode-b4-64q8kv-ctx131072",
-    "c1": "board-shape-gqa-decode-b1-8q2kv-d64-ctx256",
+    "decode-b64-ctx8192": "llama3-8b-gqa-decode-b64-ctx8192",
+    "decode-b1-ctx4097": "llama3-8b-gqa-decode-b1-ctx4096+1",
+    "decode-b64-ragged": "llama3-8b-gqa-decode-b64-ragged-512..8192",
+    "decode-b4-ctx131072": "long-context-gqa-decode-b4-64q8kv-ctx131072",
+    "decode-b1-d64-ctx256": "board-shape-gqa-decode-b1-8q2kv-d64-ctx256",
 }
 
 
@@ -204,8 +205,8 @@ class DecodeBench:
         self.ctx = ctypes.c_void_p()
 
 
-LAUNCH_BOUND = ("c1", "c2")  # workloads whose step is also timed as a replayed HIP graph
-PAGED_SUFFIX = "_paged"  # a decode workload over a paged cache (64-row pages unless --page-rows)
+LAUNCH_BOUND = ("decode-b1-d64-ctx256", "decode-b1-ctx4097")  # workloads whose step is also timed as a replayed HIP graph
+PAGED_SUFFIX = "-paged"  # a decode workload over a paged cache (64-row pages unless --page-rows)
 PAGE_ROWS = 64
 
 
@@ -450,7 +451,9 @@ def measure_layer(name: str, steps: int, warmup: int, target_wgs: int = 0) -> di
     return out
 
 
-ONESHOT_PREFILL = {"p8k": 8192}  # one causal prefill launch of this many tokens (32 q / 8 kv heads, D 128)
+ONESHOT_PREFILL = {"prefill-8192": 8192}  # one causal prefill launch of this many tokens (32 q / 8 kv heads, D 128)
+DEFAULT_OTHERS = ("decode-b1-ctx4097", "decode-b64-ragged", "decode-b4-ctx131072", "prefill-chunked-2048",
+                  "prefill-8192", "layer-2048", "decode-b64-ctx8192" + PAGED_SUFFIX)
 
 
 def measure_prefill_oneshot(name: str, steps: int, warmup: int) -> dict:
@@ -736,13 +739,15 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=100)
     parser.add_argument("--warmup", type=int, default=10)
-    parser.add_argument("--workload", default="ns", choices=sorted(WORKLOAD_NAMES))
+    parser.add_argument("--workload", default="decode-b64-ctx8192", choices=sorted(WORKLOAD_NAMES))
     parser.add_argument("--chunk", type=int, default=0, help="keys per split-KV work-group (0 = auto)")
     parser.add_argument("--page-rows", type=int, default=PAGE_ROWS,
                         help="rows per page of the paged-cache workloads (power of two, >= 64)")
     parser.add_argument("--prefill-wgs", type=int, default=0,
                         help="work-groups the prefill KV segmentation aims for (0 = auto, 1 = no segments)")
-    parser.add_argument("--others", default="c2,c3,c4,c5,p8k,layer,ns_paged", help="extra decode workloads to report ('' = none)")
+    parser.add_argument("--others", default=",".join(DEFAULT_OTHERS),
+                        help="extra workloads to report, comma-separated ('' = none); decode workloads also run "
+                             "on a paged cache with the suffix " + PAGED_SUFFIX)
     parser.add_argument("--cpu-seconds", type=float, default=12.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--calibrate-copy-mib", type=int, default=0,
@@ -762,17 +767,24 @@ def main() -> int:
     parser.add_argument("--cpu-threads", type=int, default=int(os.environ.get("LARA_CPU_THREADS", "1")))
     parser.add_argument("--output-dir", default="board_performance_results")
     args = parser.parse_args()
+    from lara_amd.benchmark import LAYER_WORKLOADS, PREFILL_WORKLOADS
+
+    known = set(WORKLOAD_NAMES) | {n + PAGED_SUFFIX for n in WORKLOAD_NAMES} | set(PREFILL_WORKLOADS) | \
+        set(LAYER_WORKLOADS) | set(ONESHOT_PREFILL)
+    unknown = [x for x in args.others.split(",") if x and x not in known]
+    if unknown:
+        parser.error(f"--others: unknown workload(s) {', '.join(unknown)}; known: {', '.join(sorted(known))}")
     args.lengths_given = args.lengths is not None
     if args.lengths is None:
         args.lengths = "1,16,32,64,128,512"
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1).", file=sys.stderr)
+        print("bench.py measures one GPU: the engine has no multi-GPU path (run with --gpus 1).", file=sys.stderr)
         return 2
 
     import torch
 
-    from lara_amd.benchmark import HBM_PEAK_GBPS, WORKLOADS
+    from lara_amd.benchmark import HBM_PEAK_GBPS, LAYER_WORKLOADS, PREFILL_WORKLOADS, WORKLOADS
 
     if not torch.cuda.is_available():
         print("bench.py needs a GPU (gfx950)", file=sys.stderr)
@@ -784,13 +796,13 @@ def main() -> int:
     main_r = measure(args.workload, args.steps, args.warmup, args.chunk, args.page_rows)
     others = {}
     for name in [x for x in args.others.split(",") if x and x != args.workload]:
-        if name == "c5":
+        if name in PREFILL_WORKLOADS:
             others[name] = measure_prefill(name, max(10, args.steps // 2), max(2, args.warmup // 2), args.prefill_wgs)
             continue
         if name in ONESHOT_PREFILL:
             others[name] = measure_prefill_oneshot(name, max(5, args.steps // 10), 2)
             continue
-        if name == "layer":
+        if name in LAYER_WORKLOADS:
             others[name] = measure_layer(name, max(10, args.steps // 4), max(2, args.warmup // 2), args.prefill_wgs)
             continue
         r = measure(name, max(10, args.steps // 2), max(2, args.warmup // 2), page_rows=args.page_rows)
@@ -811,7 +823,7 @@ def main() -> int:
         "peak": HBM_PEAK_GBPS,
         "unit": "GB/s",
         "frac": achieved / HBM_PEAK_GBPS if achieved else None,
-        "traffic": read_traffic() if args.workload == "ns" else None,
+        "traffic": read_traffic() if args.workload == "decode-b64-ctx8192" else None,
         "algorithmic_bytes_per_launch": main_r["decode_kernel_bytes"],
         "avg_launch_us": main_r["decode_us"],
         "launches_averaged": main_r["decode_launches"],

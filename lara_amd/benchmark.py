@@ -85,18 +85,18 @@ class PrefillWorkload:
 
 
 # Configurations.  "attended" follows the byte counts of the measurement plan:
-# C2 caches 4096 rows and attends 4097 after the append; the others attend the stated
+# The batch-1 context-4096 decode caches 4096 rows and attends 4097 after the append; the others attend the stated
 # context (the appended row is the last of it).
 WORKLOADS = {
-    "c1": DecodeWorkload("c1", "board-shape decode: B1, 8q/2kv, D64, ctx 256, no mask", 1, 8, 2, 64,
+    "decode-b1-d64-ctx256": DecodeWorkload("decode-b1-d64-ctx256", "board-shape decode: B1, 8q/2kv, D64, ctx 256, no mask", 1, 8, 2, 64,
                          attended=256, scale=1.0 / 8.0, seed=1),
-    "c2": DecodeWorkload("c2", "Llama-3-8B decode: B1, 32q/8kv, D128, ctx 4096 + 1 appended", 1, 32, 8, 128,
+    "decode-b1-ctx4097": DecodeWorkload("decode-b1-ctx4097", "Llama-3-8B decode: B1, 32q/8kv, D128, ctx 4096 + 1 appended", 1, 32, 8, 128,
                          attended=4097, amplitude=0.5, seed=2),
-    "c3": DecodeWorkload("c3", "batched decode: B64, 32q/8kv, D128, L ~ U[512, 8192]", 64, 32, 8, 128,
+    "decode-b64-ragged": DecodeWorkload("decode-b64-ragged", "batched decode: B64, 32q/8kv, D128, L ~ U[512, 8192]", 64, 32, 8, 128,
                          ragged=(512, 8192), seed=3),
-    "c4": DecodeWorkload("c4", "long-context decode: B4, 64q/8kv, D128, L 131072, 1% K rows x8", 4, 64, 8, 128,
+    "decode-b4-ctx131072": DecodeWorkload("decode-b4-ctx131072", "long-context decode: B4, 64q/8kv, D128, L 131072, 1% K rows x8", 4, 64, 8, 128,
                          attended=131072, outlier_fraction=0.01, outlier_scale=8.0, seed=4),
-    "ns": DecodeWorkload("ns", "Llama-3-8B GQA decode: B64, 32q/8kv, D128, ctx 8192", 64, 32, 8, 128,
+    "decode-b64-ctx8192": DecodeWorkload("decode-b64-ctx8192", "Llama-3-8B GQA decode: B64, 32q/8kv, D128, ctx 8192", 64, 32, 8, 128,
                          attended=8192, seed=5),
 }
 
@@ -114,7 +114,7 @@ class LayerWorkload:
 
 
 LAYER_WORKLOADS = {
-    "layer": LayerWorkload("layer", "run_layer input stage + attention: Llama-3-8B shape (hidden 4096, 32q/8kv, D128), "
+    "layer-2048": LayerWorkload("layer-2048", "run_layer input stage + attention: Llama-3-8B shape (hidden 4096, 32q/8kv, D128), "
                                     "2048-token prompt, RMSNorm -> QKV GEMM -> RoPE -> causal attention",
                            32, 8, 128, hidden=4096, tokens=2048, seed=8),
 }
@@ -126,7 +126,7 @@ def layer_projection_flops(w: LayerWorkload) -> int:
 
 
 PREFILL_WORKLOADS = {
-    "c5": PrefillWorkload("c5", "chunked prefill: B1, 32q/8kv, D128, 2048 tokens in 256-token chunks, causal",
+    "prefill-chunked-2048": PrefillWorkload("prefill-chunked-2048", "chunked prefill: B1, 32q/8kv, D128, 2048 tokens in 256-token chunks, causal",
                           32, 8, 128, prompt=2048, chunk=256, seed=6),
 }
 
@@ -285,7 +285,7 @@ def compute_model(name: str) -> dict:
 
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
-    parser.add_argument("--workload", default="ns", choices=sorted(WORKLOADS) + sorted(PREFILL_WORKLOADS))
+    parser.add_argument("--workload", default="decode-b64-ctx8192", choices=sorted(WORKLOADS) + sorted(PREFILL_WORKLOADS))
     args = parser.parse_args()
     print(json.dumps(compute_model(args.workload), indent=2, sort_keys=True, default=str))
     return 0

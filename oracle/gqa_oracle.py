@@ -1,8 +1,8 @@
 """CPU oracle for the GQA streaming-attention path.
 
 TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
-``cpu_baseline`` leg of ``bench.py`` may import this module, and only as the checker or
-the timed CPU baseline.  The product path (``lara_amd``) never imports it and has no CPU
+``cpu_baseline`` leg of ``bench.py`` may import this module, and only as the parity
+reference or the timed CPU baseline.  The product path (``lara_amd``) never imports it and has no CPU
 fallback.
 
 What it restates (reference files, paths relative to the reference repository):

@@ -1,6 +1,6 @@
 """CPU oracle for the layer input stage of run_layer (RMSNorm, QKV projection, RoPE).
 
-TEST INFRASTRUCTURE ONLY.  Only ``tests/`` may import this module, as the checker.  The
+TEST INFRASTRUCTURE ONLY.  Only ``tests/`` may import this module, as the parity reference.  The
 product path (``lara_amd``) never imports it.
 
 The reference's ``run_layer`` (sw/attn_driver.py:552-586) imports ``rms_norm``,

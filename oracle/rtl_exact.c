@@ -1,7 +1,7 @@
 /*
  * rtl_exact.c -- CPU restatement of the KV260 datapath's bit-level arithmetic (TEST INFRASTRUCTURE).
  *
- * Only tests/ (through ctypes) use this library, as the checker of the engine's RTL-exact
+ * Only tests/ (through ctypes) use this library, as the oracle of the engine's RTL-exact
  * numerics mode; the product never links or loads it.
  *
  * It restates, bit for bit, the synthesis path of the reference RTL (paths relative to the

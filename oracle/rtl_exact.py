@@ -1,5 +1,5 @@
 """ctypes binding of oracle/librtl_exact.so, the C restatement of the KV260 bit-level
-arithmetic (TEST INFRASTRUCTURE: only tests/ use it, as the checker of the RTL-exact mode).
+arithmetic (TEST INFRASTRUCTURE: only tests/ use it, as the oracle of the RTL-exact mode).
 
 Build it with ``make -C oracle`` (``__graft_entry__.build()`` does).  The ROM tables come from
 ``lara_amd/data/*.hex`` (closed forms, pinned by SHA-256 to the board's ROM images).

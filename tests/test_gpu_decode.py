@@ -143,7 +143,7 @@ def test_decode_split_invariance():
 
 
 def test_decode_group8_outliers():
-    # C4-shaped (64q/8kv, 1% of K rows x8) at a length the oracle checks in seconds
+    # Long-context shape (64q/8kv, 1% of K rows x8) at a length the oracle checks in seconds
     rng = np.random.default_rng(104)
     B, hq, hkv, d, L = 2, 64, 8, 128, 20000
     with make_engine(B, hq, hkv, d, L) as eng:
@@ -188,15 +188,15 @@ def _full_size(name):
 
 
 def test_decode_full_size_ns():
-    _full_size("ns")
+    _full_size("decode-b64-ctx8192")
 
 
 def test_decode_full_size_c3_ragged():
-    _full_size("c3")
+    _full_size("decode-b64-ragged")
 
 
 def test_decode_full_size_c4_long_context():
-    _full_size("c4")
+    _full_size("decode-b4-ctx131072")
 
 
 @pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (64, 8, 128), (16, 8, 64)])

@@ -90,21 +90,21 @@ def test_tile_pairs_per_head_brute_force():
 
 
 def test_roofline_bytes_match_measurement_plan():
-    ns = bm.compute_model("ns")
+    ns = bm.compute_model("decode-b64-ctx8192")
     assert ns["decode_kernel_bytes"] == 2 ** 31 + 64 * 32 * 128 * 2
     assert ns["step_bytes"] == 2 ** 31 + int(1.25 * 2 ** 20)
-    c2 = bm.compute_model("c2")
+    c2 = bm.compute_model("decode-b1-ctx4097")
     assert c2["step_bytes"] - 2 * 8 * 128 * 2 - 2 * 32 * 128 * 2 == 16781312
-    c5 = bm.compute_model("c5")
+    c5 = bm.compute_model("prefill-chunked-2048")
     assert abs(c5["flops"] / 1e9 - 34.38) < 0.01
 
 
 def test_workload_lengths():
-    c3 = bm.WORKLOADS["c3"].lengths()
+    c3 = bm.WORKLOADS["decode-b64-ragged"].lengths()
     assert c3.shape == (64,) and c3.min() >= 512 and c3.max() <= 8192
-    assert np.array_equal(c3, bm.WORKLOADS["c3"].lengths())
-    assert np.all(bm.WORKLOADS["ns"].lengths() == 8192)
-    sched = bm.prefill_chunk_schedule(bm.PREFILL_WORKLOADS["c5"])
+    assert np.array_equal(c3, bm.WORKLOADS["decode-b64-ragged"].lengths())
+    assert np.all(bm.WORKLOADS["decode-b64-ctx8192"].lengths() == 8192)
+    sched = bm.prefill_chunk_schedule(bm.PREFILL_WORKLOADS["prefill-chunked-2048"])
     assert len(sched) == 8 and sched[-1] == (1792, 256, 2048)
 
 

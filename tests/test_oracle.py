@@ -1,4 +1,4 @@
-"""Pins the CPU oracle against independent references before it is trusted as the checker.
+"""Pins the CPU oracle against independent references before the parity tests rely on it.
 
 * bf16 packers: hand-derived words, the algebraic closed form of the reference packer
   over every low-half pattern, and torch's bfloat16 conversion (RNE) for bf16_rne.
