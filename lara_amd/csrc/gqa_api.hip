@@ -33,13 +33,19 @@ struct Txn {
 
 // One projection GEMM shape, D[rows x n_tokens] (leading dimension ld) = W^T X with W stored
 // [rows][hidden] and X [n_tokens][hidden] (column-major: W is hidden x rows, X hidden x
-// n_tokens), bf16 in and out, fp32 accumulation: the hipBLASLt descriptors and the algorithm
-// its heuristic ranks first among those that need no workspace.
+// n_tokens), bf16 in and out, fp32 accumulation: the hipBLASLt descriptors, the candidates its
+// heuristic ranks first (workspace up to kProjectionWorkspace bytes) and the one in use: the
+// heuristic's first until the first call outside a graph capture has timed them all.
+constexpr int kProjectionCandidates = 8;
+constexpr size_t kProjectionWorkspace = 32u << 20;
 struct ProjectionPlan {
     int rows = 0, n_tokens = 0, hidden = 0, ld = 0;
     hipblasLtMatmulDesc_t desc = nullptr;
     hipblasLtMatrixLayout_t w = nullptr, x = nullptr, d = nullptr;
-    hipblasLtMatmulAlgo_t algo{};
+    hipblasLtMatmulHeuristicResult_t cand[kProjectionCandidates] = {};
+    int n_cand = 0;
+    int pick = 0;        // index into cand of the algorithm in use
+    bool tuned = false;  // pick chosen by timing
 };
 constexpr int kProjectionPlans = 8;
 
@@ -90,6 +96,8 @@ struct gqa_ctx {
     size_t layer_in_bytes = 0;
     uint8_t* layer_tmp = nullptr;  // normalised x, then the [n_tokens][Q|K|V] projection
     size_t layer_tmp_bytes = 0;
+    uint8_t* lt_ws = nullptr;      // hipBLASLt workspace of the projection algorithms in use
+    size_t lt_ws_bytes = 0;
     hipEvent_t ev_layer[4] = {};
     float layer_us[3] = {};
     bool layer_timed = false;  // ev_layer holds a recorded call
@@ -385,9 +393,9 @@ void release_plan(ProjectionPlan& p) {
 }
 
 // The cached plan for this projection shape, or a new one (replacing the oldest of
-// kProjectionPlans): descriptors plus the first algorithm of hipBLASLt's heuristic.
-int projection_plan(gqa_ctx* c, int rows, int n_tokens, int hidden, int ld, const ProjectionPlan** out) {
-    for (const ProjectionPlan& p : c->proj)
+// kProjectionPlans): descriptors plus hipBLASLt's heuristic candidates.
+int projection_plan(gqa_ctx* c, int rows, int n_tokens, int hidden, int ld, ProjectionPlan** out) {
+    for (ProjectionPlan& p : c->proj)
         if (p.desc && p.rows == rows && p.n_tokens == n_tokens && p.hidden == hidden && p.ld == ld) {
             *out = &p;
             return GQA_OK;
@@ -397,8 +405,7 @@ int projection_plan(gqa_ctx* c, int rows, int n_tokens, int hidden, int ld, cons
     release_plan(p);
     hipblasLtMatmulPreference_t pref = nullptr;
     const hipblasOperation_t tw = HIPBLAS_OP_T, tx = HIPBLAS_OP_N;
-    const uint64_t no_workspace = 0;
-    hipblasLtMatmulHeuristicResult_t best{};
+    const uint64_t max_workspace = kProjectionWorkspace;
     int found = 0;
     hipblasStatus_t st = hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F);
     if (st == HIPBLAS_STATUS_SUCCESS)
@@ -410,23 +417,69 @@ int projection_plan(gqa_ctx* c, int rows, int n_tokens, int hidden, int ld, cons
     if (st == HIPBLAS_STATUS_SUCCESS) st = hipblasLtMatrixLayoutCreate(&p.d, HIP_R_16BF, rows, n_tokens, ld);
     if (st == HIPBLAS_STATUS_SUCCESS) st = hipblasLtMatmulPreferenceCreate(&pref);
     if (st == HIPBLAS_STATUS_SUCCESS)
-        st = hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &no_workspace,
-                                                   sizeof(no_workspace));
+        st = hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &max_workspace,
+                                                   sizeof(max_workspace));
     if (st == HIPBLAS_STATUS_SUCCESS)
-        st = hipblasLtMatmulAlgoGetHeuristic(c->lt, p.desc, p.w, p.x, p.d, p.d, pref, 1, &best, &found);
+        st = hipblasLtMatmulAlgoGetHeuristic(c->lt, p.desc, p.w, p.x, p.d, p.d, pref, kProjectionCandidates, p.cand,
+                                             &found);
     if (pref) (void)hipblasLtMatmulPreferenceDestroy(pref);
-    if (st != HIPBLAS_STATUS_SUCCESS || found < 1 || best.state != HIPBLAS_STATUS_SUCCESS) {
+    // Keep the usable candidates, in the heuristic's order.
+    p.n_cand = 0;
+    for (int i = 0; st == HIPBLAS_STATUS_SUCCESS && i < found && i < kProjectionCandidates; ++i)
+        if (p.cand[i].state == HIPBLAS_STATUS_SUCCESS && p.cand[i].workspaceSize <= kProjectionWorkspace)
+            p.cand[p.n_cand++] = p.cand[i];
+    if (st != HIPBLAS_STATUS_SUCCESS || p.n_cand < 1) {
         snprintf(g_last_error, sizeof(g_last_error), "hipBLASLt projection plan %dx%dx%d: status %d, %d algorithms",
                  rows, n_tokens, hidden, (int)st, found);
         release_plan(p);
         return GQA_ERR_HIP;
     }
-    p.algo = best.algo;
+    p.pick = 0;
+    p.tuned = p.n_cand == 1;
     p.rows = rows;
     p.n_tokens = n_tokens;
     p.hidden = hidden;
     p.ld = ld;
     *out = &p;
+    return GQA_OK;
+}
+
+// Picks the fastest of a plan's candidates on the caller's operands: each runs once untimed,
+// then three times between two events; the stream is synchronised once per candidate.  Every
+// candidate computes the same product (beta = 0), so the runs leave the destination as the
+// final call does.  A candidate that fails to launch is skipped.  Runs once per plan.
+template <typename Gemm>
+int tune_projection(gqa_ctx* c, ProjectionPlan* p, Gemm&& gemm, hipStream_t s) {
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    HIP_TRY(hipEventCreate(&e0));
+    if (hipEventCreate(&e1) != hipSuccess) {
+        (void)hipEventDestroy(e0);
+        return GQA_ERR_HIP;
+    }
+    int best = 0;
+    float best_ms = INFINITY;
+    hipError_t err = hipSuccess;
+    for (int k = 0; k < p->n_cand && err == hipSuccess; ++k) {
+        if (gemm(k) != HIPBLAS_STATUS_SUCCESS) continue;
+        bool ok = (err = hipEventRecord(e0, s)) == hipSuccess;
+        for (int r = 0; ok && r < 3; ++r) ok = gemm(k) == HIPBLAS_STATUS_SUCCESS;
+        if (err == hipSuccess) err = hipEventRecord(e1, s);
+        if (err == hipSuccess) err = hipEventSynchronize(e1);
+        float ms = 0.f;
+        if (err == hipSuccess) err = hipEventElapsedTime(&ms, e0, e1);
+        if (ok && err == hipSuccess && ms < best_ms) {
+            best_ms = ms;
+            best = k;
+        }
+    }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (err != hipSuccess) {
+        last_hip_error(err, "projection tuning");
+        return GQA_ERR_HIP;
+    }
+    p->pick = best;
+    p->tuned = true;
     return GQA_OK;
 }
 
@@ -480,11 +533,23 @@ int run_layer_qkv(gqa_ctx* c, int32_t b, const void* x, int32_t n_tokens, int32_
         n_gemm = 1;
     }
     for (int i = 0; i < n_gemm; ++i) {
-        const ProjectionPlan* p = nullptr;
+        ProjectionPlan* p = nullptr;
         rc = projection_plan(c, rows[i], n_tokens, hidden, ld, &p);
         if (rc != GQA_OK) return rc;
-        const hipblasStatus_t st = hipblasLtMatmul(c->lt, p->desc, &one, ws[i], p->w, src, p->x, &zero, qkv + off[i],
-                                                   p->d, qkv + off[i], p->d, &p->algo, nullptr, 0, s);
+        size_t ws_need = p->cand[p->pick].workspaceSize;
+        if (!p->tuned && !c->capturing)
+            for (int k = 0; k < p->n_cand; ++k) ws_need = std::max(ws_need, p->cand[k].workspaceSize);
+        rc = ensure_buffer(&c->lt_ws, &c->lt_ws_bytes, std::max<size_t>(ws_need, 256));
+        if (rc != GQA_OK) return rc;
+        auto gemm = [&](int k) {
+            return hipblasLtMatmul(c->lt, p->desc, &one, ws[i], p->w, src, p->x, &zero, qkv + off[i], p->d,
+                                   qkv + off[i], p->d, &p->cand[k].algo, c->lt_ws, p->cand[k].workspaceSize, s);
+        };
+        if (!p->tuned && !c->capturing) {
+            rc = tune_projection(c, p, gemm, s);
+            if (rc != GQA_OK) return rc;
+        }
+        const hipblasStatus_t st = gemm(p->pick);
         if (st != HIPBLAS_STATUS_SUCCESS) {
             snprintf(g_last_error, sizeof(g_last_error), "hipblasLtMatmul: status %d", (int)st);
             return GQA_ERR_HIP;
@@ -740,6 +805,7 @@ int gqa_destroy(gqa_ctx* c) {
     if (c->lt) (void)hipblasLtDestroy(c->lt);
     (void)hipFree(c->layer_in);
     (void)hipFree(c->layer_tmp);
+    (void)hipFree(c->lt_ws);
     for (int i = 0; i < 4; ++i)
         if (c->ev_layer[i]) (void)hipEventDestroy(c->ev_layer[i]);
     if (c->stream) (void)hipStreamDestroy(c->stream);
