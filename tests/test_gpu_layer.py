@@ -61,6 +61,26 @@ def weights(rng, nq, nkv, hidden):
 
 
 @pytest.mark.parametrize("fused", [False, True])
+def test_first_call_of_a_shape_equals_the_tuned_calls(fused):
+    # The first call of a projection shape times hipBLASLt's candidates (running each on the
+    # destination) and keeps the fastest; that call and the later ones (cached pick, no timing)
+    # must leave the same words, and a new shape in between must not disturb the cached plan.
+    print(f"[layer] tuned projection repeatability fused={fused}", flush=True)
+    rng = np.random.default_rng(77)
+    with AttentionAccelerator(n_q_heads=8, n_kv_heads=2, head_dim=128, max_seq_len=384) as acc:
+        x = bf16_normal(rng, (192, 2048))
+        wq, wk, wv = weights(rng, 1024, 256, 2048)
+        gamma = orc.fp32_to_bf16_u16(1 + 0.1 * rng.standard_normal(2048, dtype=np.float32))
+        first = stage(acc, x, wq, wk, wv, gamma, row0=5, fused=fused)
+        other = stage(acc, x[:64], wq, wk, wv, gamma, row0=200, fused=fused)  # another shape
+        second = stage(acc, x, wq, wk, wv, gamma, row0=5, fused=fused)
+        third = stage(acc, x, wq, wk, wv, gamma, row0=5, fused=fused)
+    assert other[0].shape[1] == 64
+    for a, b, c in zip(first, second, third):
+        assert np.array_equal(a, b) and np.array_equal(b, c)
+
+
+@pytest.mark.parametrize("fused", [False, True])
 @pytest.mark.parametrize("hidden,L", [(768, 37), (1001, 5), (4096, 64)])
 def test_projection_within_fp32_accumulation_bound(hidden, L, fused):
     print(f"[layer] projection hidden={hidden} L={L} fused={fused}", flush=True)
