@@ -117,6 +117,25 @@ __device__ __forceinline__ int clamp_len(int len, int l_max) {
 
 __device__ __forceinline__ u32x4 ld_stream(const u32x4* p) { return __builtin_nontemporal_load(p); }
 
+// The sequence of rank `rank` when the batch (at most 64 sequences, one per lane) is ordered
+// by attended length, longest first, ties in index order.  Every wave computes it for itself:
+// one load of the lengths, a wave min/max (a batch of equal lengths keeps its order and skips
+// the rest) and a batch-long loop of lane reads; no LDS and no barrier.
+__device__ int rank_to_sequence(const DecodeArgs& a, int rank) {
+    const int lane = threadIdx.x & 63;
+    const int mine = lane < a.batch ? clamp_len(a.lens[lane], a.l_max) : -1;
+    const int lo = __reduce_min_sync(~0ull, lane < a.batch ? mine : INT_MAX);
+    const int hi = __reduce_max_sync(~0ull, mine);
+    if (lo == hi) return rank;
+    int before = 0;  // sequences ordered ahead of this lane's
+    for (int j = 0; j < a.batch; ++j) {
+        const int other = __builtin_amdgcn_readlane(mine, j);
+        before += (other > mine) || (other == mine && j < lane);
+    }
+    const unsigned long long hit = __ballot(lane < a.batch && before == rank);
+    return hit ? (int)__builtin_ctzll(hit) : rank;
+}
+
 template <int D, int G, int NW, bool PAGED>
 __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
     constexpr int NCH = D / 8;               // 16-byte words per K/V row
@@ -133,9 +152,10 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
     static_assert(!PBF16 || (NSUB % 2 == 0 && NLD % 2 == 0), "key pairs (row, row + RK/2) share a lane");
 
     const int split = blockIdx.x;
-    const int unit = blockIdx.y;  // b * H_kv + h
-    const int b = unit / a.n_kv_heads;
-    const int h = unit - b * a.n_kv_heads;
+    const int h = blockIdx.y % a.n_kv_heads;
+    int b = blockIdx.y / a.n_kv_heads;
+    if (a.longest_first) b = rank_to_sequence(a, b);
+    const int unit = b * a.n_kv_heads + h;
     const int H_q = a.n_kv_heads * G;
     const int L = clamp_len(a.lens[b], a.l_max);
     const int n_splits = L > 0 ? (L + a.chunk - 1) / a.chunk : 1;

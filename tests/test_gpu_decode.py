@@ -123,6 +123,30 @@ def test_decode_ragged_edges(hq, hkv, d):
         assert not out[0].any()
 
 
+@pytest.mark.parametrize("B", [64, 65])
+def test_decode_longest_first_order_is_invisible(B):
+    # Batches of up to 64 sequences are dispatched longest first (ranked inside the kernel, ties
+    # in index order); above 64 the grid keeps index order.  Either way every sequence's output
+    # must be the oracle's, and word for word the same when the batch is listed in another order.
+    rng = np.random.default_rng(600 + B)
+    hq, hkv, d = 32, 8, 128
+    lens = rng.choice(np.array([0, 1, 16, 17, 100, 256, 257, 300, 511, 600], np.int32), size=B)
+    lens[:4] = 600  # ties at the top
+    with make_engine(B, hq, hkv, d, 640) as eng:
+        kc, vc = fill_cache(eng, rng, B, hkv, d, lens, lcap=640)
+        q = bf16_normal(rng, (B, hq, d))
+        out, lse = eng.decode_step(q, lens, return_lse=True)
+        check_decode(out, lse, q, kc, vc, lens, None)
+    perm = rng.permutation(B)
+    with make_engine(B, hq, hkv, d, 640) as eng:
+        for i, b in enumerate(perm):
+            if lens[b]:
+                eng.load_kv(kc[b, :, :lens[b]], vc[b, :, :lens[b]], b=i)
+        out_p, lse_p = eng.decode_step(q[perm], lens[perm], return_lse=True)
+    assert np.array_equal(out_p, out[perm])
+    assert np.array_equal(lse_p, lse[perm])
+
+
 def test_decode_split_invariance():
     rng = np.random.default_rng(103)
     B, hq, hkv, d = 2, 32, 8, 128
