@@ -81,8 +81,8 @@ typedef struct gqa_config {
     int32_t n_q_heads;   /* H_q  (N_Q_HEADS, attn_driver.py:65)                         */
     int32_t n_kv_heads;  /* H_kv (N_KV_HEADS, attn_driver.py:66); H_q % H_kv == 0        */
     int32_t head_dim;    /* D    (HEAD_DIM, attn_driver.py:63): 64 or 128               */
-    int32_t max_seq_len; /* cache rows per (b, kv head)  (MAX_SEQ_LEN generalised)      */
-    int32_t max_q_len;   /* largest prefill chunk / transaction length (>= 1)           */
+    int32_t max_seq_len; /* cache rows per (b, kv head), 1 .. 2^30 (MAX_SEQ_LEN generalised) */
+    int32_t max_q_len;   /* largest prefill chunk / transaction length, 1 .. 2^30       */
     float   scale;       /* softmax scale; 0 selects fp32(1/sqrt(D)) (attn_pkg.sv:241)   */
     int32_t device;      /* HIP device ordinal                                          */
 } gqa_config;

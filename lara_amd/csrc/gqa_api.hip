@@ -20,6 +20,7 @@ namespace {
 constexpr int kMinChunk = 256;     // smallest split (keys); multiple of every decode round size
 constexpr int kTargetPrefillWgs = kPrefillTargetWgs;
 constexpr int kMaxPrefillSegs = 16;
+constexpr int32_t kMaxRows = 1 << 30;  // max_seq_len / max_q_len limit: row counts rounded up stay in int32
 constexpr int kTargetDecodeWaves = 2048;  // 8 waves per CU; one split per (sequence, kv head) once that fills the GPU
 
 struct Txn {
@@ -611,7 +612,8 @@ int create_ctx(const gqa_config* cfg, int32_t page_size, int32_t n_pages, gqa_ct
     *out_ctx = nullptr;
     const gqa_config& k = *cfg;
     if (k.batch < 1 || k.n_q_heads < 1 || k.n_kv_heads < 1 || k.n_q_heads % k.n_kv_heads != 0 ||
-        k.max_seq_len < 1 || k.max_q_len < 1 || !(k.scale >= 0.f) || !isfinite(k.scale))
+        k.max_seq_len < 1 || k.max_q_len < 1 || k.max_seq_len > kMaxRows || k.max_q_len > kMaxRows ||
+        !(k.scale >= 0.f) || !isfinite(k.scale))
         return GQA_ERR_BAD_CFG;
     const int group = k.n_q_heads / k.n_kv_heads;
     if (!decode_supported(k.head_dim, group) && !prefill_supported(k.head_dim, group)) return GQA_ERR_UNSUPPORTED;

@@ -48,6 +48,9 @@ def test_create_rejects_bad_config_before_device():
     ctx = ctypes.c_void_p()
     assert lib.gqa_create(ctypes.byref(_cfg(n_q_heads=30)), ctypes.byref(ctx)) == _lib.GQA_ERR_BAD_CFG
     assert lib.gqa_create(ctypes.byref(_cfg(max_seq_len=0)), ctypes.byref(ctx)) == _lib.GQA_ERR_BAD_CFG
+    # row counts are rounded up inside int32: lengths above 2^30 are refused, not wrapped
+    assert lib.gqa_create(ctypes.byref(_cfg(max_seq_len=2**31 - 1)), ctypes.byref(ctx)) == _lib.GQA_ERR_BAD_CFG
+    assert lib.gqa_create(ctypes.byref(_cfg(max_q_len=2**30 + 1)), ctypes.byref(ctx)) == _lib.GQA_ERR_BAD_CFG
     assert lib.gqa_create(ctypes.byref(_cfg(scale=-1.0)), ctypes.byref(ctx)) == _lib.GQA_ERR_BAD_CFG
     assert lib.gqa_create(ctypes.byref(_cfg(head_dim=96)), ctypes.byref(ctx)) == _lib.GQA_ERR_UNSUPPORTED
     assert lib.gqa_create(ctypes.byref(_cfg(n_q_heads=96, n_kv_heads=3)), ctypes.byref(ctx)) == _lib.GQA_ERR_UNSUPPORTED
