@@ -1401,7 +1401,7 @@ int gqa_status(gqa_ctx* c, uint32_t* out_status) {
 
 int gqa_wait(gqa_ctx* c, int32_t timeout_ms) {
     if (!c) return GQA_ERR_NULL;
-    if (!c->txn.running) return c->txn.valid ? GQA_ERR_NO_TRANSACTION : GQA_ERR_NO_TRANSACTION;
+    if (!c->txn.running) return GQA_ERR_NO_TRANSACTION;  // nothing started (submitted or not)
     struct timespec t0;
     clock_gettime(CLOCK_MONOTONIC, &t0);
     for (;;) {
