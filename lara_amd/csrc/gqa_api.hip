@@ -18,10 +18,9 @@ using namespace lara;
 namespace {
 
 constexpr int kMinChunk = 256;     // smallest split (keys); multiple of every decode round size
-constexpr int kTargetPrefillWgs = kPrefillTargetWgs;
 constexpr int kMaxPrefillSegs = 16;
 constexpr int32_t kMaxRows = 1 << 30;  // max_seq_len / max_q_len limit: row counts rounded up stay in int32
-constexpr int kTargetDecodeWaves = 2048;  // 8 waves per CU; one split per (sequence, kv head) once that fills the GPU
+constexpr int kDecodeWavesPerCu = 8;  // split planner target; one split per (sequence, kv head) once that fills the GPU
 
 struct Txn {
     int valid = 0;     // a transaction has been submitted (configure + Q staged)
@@ -85,6 +84,7 @@ struct gqa_ctx {
     hipEvent_t ev_t[4] = {};     // transaction: copy-in start, kernel start, kernel end, done
     float last_us = 0.f;
     double clock_mhz = 0.0;
+    int n_cu = 256;  // compute units of the device (the planners' work-group targets scale with it)
     Txn txn;
     // Layer input stage (run_layer): hipBLASLt handle, projection plans and grow-only device
     // workspaces, created on first use; ev_layer brackets RMSNorm, projection and RoPE of the last timed layer call
@@ -158,7 +158,7 @@ hipStream_t pick_stream(gqa_ctx* c, void* s) { return s ? (hipStream_t)s : c->st
 int choose_chunk(const gqa_ctx* c, int max_len) {
     if (c->chunk_opt > 0) return c->chunk_opt;
     const int units = c->cfg.batch * c->cfg.n_kv_heads;
-    const int target_wgs = kTargetDecodeWaves / decode_waves(c->group);
+    const int target_wgs = kDecodeWavesPerCu * c->n_cu / decode_waves(c->group);
     int splits = (target_wgs + units - 1) / units;
     if (splits < 1) splits = 1;
     int chunk = (max_len + splits - 1) / splits;
@@ -292,7 +292,7 @@ int run_prefill(gqa_ctx* c, int32_t b, const void* q, int32_t q_len, int32_t q_p
     if (!prefill_supported(c->cfg.head_dim, c->group)) return GQA_ERR_UNSUPPORTED;
     int kv_span = kv_len;
     if (causal) kv_span = std::min(kv_len, std::max(0, q_pos_base + q_len - kv_pos_base));
-    const int target = c->prefill_wgs_opt > 0 ? c->prefill_wgs_opt : kTargetPrefillWgs;
+    const int target = c->prefill_wgs_opt > 0 ? c->prefill_wgs_opt : c->n_cu;
     PrefillPlan plan = plan_prefill(q_len, kv_span, c->group, c->cfg.n_kv_heads, target, kMaxPrefillSegs);
     if (prefill_workspace_floats(plan, q_len, c->cfg.n_q_heads, c->cfg.head_dim) > c->pre_ws_floats)
         plan = plan_prefill(q_len, kv_span, c->group, c->cfg.n_kv_heads, 1, 1);  // one segment
@@ -634,6 +634,7 @@ int create_ctx(const gqa_config* cfg, int32_t page_size, int32_t n_pages, gqa_ct
     c->scale = k.scale > 0.f ? k.scale : (float)(1.0 / sqrt((double)k.head_dim));
     c->cfg.scale = c->scale;
     c->clock_mhz = prop.clockRate / 1000.0;
+    if (prop.multiProcessorCount > 0) c->n_cu = prop.multiProcessorCount;
     if (page_size > 0) {
         c->paged = 1;
         c->page_size = page_size;
@@ -657,7 +658,7 @@ int create_ctx(const gqa_config* cfg, int32_t page_size, int32_t n_pages, gqa_ct
     alloc((void**)&c->part_o, units * c->max_splits_cap * group * D * sizeof(float));
     alloc((void**)&c->part_ml, units * c->max_splits_cap * group * 2 * sizeof(float));
     if (prefill_supported(k.head_dim, group)) {
-        c->pre_ws_floats = prefill_workspace_need(c, kTargetPrefillWgs);
+        c->pre_ws_floats = prefill_workspace_need(c, c->n_cu);
         if (c->pre_ws_floats > 0) alloc((void**)&c->pre_ws, c->pre_ws_floats * sizeof(float));
     }
     alloc((void**)&c->q_dev, c->stage_words * 2);
@@ -845,7 +846,7 @@ int gqa_set_option(gqa_ctx* c, int32_t option, int64_t value) {
                 return GQA_OK;
             }
             // Grow the segment workspace for the new target (kept if it already suffices).
-            const size_t need = prefill_workspace_need(c, value > 0 ? (int)value : kTargetPrefillWgs);
+            const size_t need = prefill_workspace_need(c, value > 0 ? (int)value : c->n_cu);
             if (need > c->pre_ws_floats) {
                 int rc = txn_idle(c);
                 if (rc != GQA_OK) return rc;

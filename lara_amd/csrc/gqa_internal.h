@@ -87,8 +87,6 @@ struct PrefillPlan {
     int32_t n_segs;
 };
 PrefillPlan plan_prefill(int q_len, int kv_span, int group, int n_kv_heads, int target_wgs, int max_segs);
-// Work-groups the KV segmentation of a prefill launch should aim for (one per CU).
-constexpr int kPrefillTargetWgs = 256;
 // fp32 words of partial-output workspace a plan needs (O and (m, l) per row, per segment).
 size_t prefill_workspace_floats(const PrefillPlan& p, int q_len, int n_q_heads, int head_dim);
 
