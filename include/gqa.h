@@ -59,10 +59,10 @@ extern "C" {
 #define GQA_TIMER_COUNT   4
 
 /* Tunables for gqa_set_option. */
-#define GQA_OPT_DECODE_CHUNK 1 /* keys per split-KV work-group (multiple of 64; 0 = auto) */
+#define GQA_OPT_DECODE_CHUNK 1 /* keys per split-KV work-group (multiple of 256; 0 = auto: about 8 waves per CU) */
 #define GQA_OPT_PROFILE      2 /* 1 = time every kernel launch with HIP events (restarts the record);
                                   each event pair idles the GPU ~10 us between launches */
-#define GQA_OPT_PREFILL_WGS  3 /* prefill work-groups the KV segmentation aims for (0 = auto, 1 = none) */
+#define GQA_OPT_PREFILL_WGS  3 /* prefill work-groups the KV segmentation aims for (0 = auto: one per CU, 1 = none) */
 #define GQA_OPT_NUMERICS     4 /* GQA_NUMERICS_*: arithmetic of prefill / transactions (decode: EXACT only) */
 
 /* Numerics of the attention kernels (GQA_OPT_NUMERICS).
