@@ -42,6 +42,7 @@ WORKLOAD_NAMES = {
     "decode-b64-ragged": "llama3-8b-gqa-decode-b64-ragged-512..8192",
     "decode-b4-ctx131072": "long-context-gqa-decode-b4-64q8kv-ctx131072",
     "decode-b1-d64-ctx256": "board-shape-gqa-decode-b1-8q2kv-d64-ctx256",
+    "decode-b256-ragged": "llama3-8b-gqa-decode-b256-ragged-512..8192",
 }
 
 

@@ -96,6 +96,8 @@ WORKLOADS = {
                          ragged=(512, 8192), seed=3),
     "decode-b4-ctx131072": DecodeWorkload("decode-b4-ctx131072", "long-context decode: B4, 64q/8kv, D128, L 131072, 1% K rows x8", 4, 64, 8, 128,
                          attended=131072, outlier_fraction=0.01, outlier_scale=8.0, seed=4),
+    "decode-b256-ragged": DecodeWorkload("decode-b256-ragged", "batched decode: B256, 32q/8kv, D128, L ~ U[512, 8192]",
+                                         256, 32, 8, 128, ragged=(512, 8192), seed=10),
     "decode-b64-ctx8192": DecodeWorkload("decode-b64-ctx8192", "Llama-3-8B GQA decode: B64, 32q/8kv, D128, ctx 8192", 64, 32, 8, 128,
                          attended=8192, seed=5),
 }

@@ -117,23 +117,69 @@ __device__ __forceinline__ int clamp_len(int len, int l_max) {
 
 __device__ __forceinline__ u32x4 ld_stream(const u32x4* p) { return __builtin_nontemporal_load(p); }
 
-// The sequence of rank `rank` when the batch (at most 64 sequences, one per lane) is ordered
-// by attended length, longest first, ties in index order.  Every wave computes it for itself:
-// one load of the lengths, a wave min/max (a batch of equal lengths keeps its order and skips
-// the rest) and a batch-long loop of lane reads; no LDS and no barrier.
+// The sequence of rank `rank` when the batch is ordered longest first.  Every wave computes it
+// for itself from the lengths (no LDS, no barrier); a batch of equal lengths keeps index order.
+//  * Up to 64 sequences (one per lane): exact -- by attended length, ties in index order (a wave
+//    min/max, then a batch-long loop of lane reads).
+//  * More: by length bucket (kBuckets equal slices of 0..l_max), longest bucket first, index
+//    order inside a bucket -- a histogram of ballots over 64-sequence chunks, then the rank's
+//    bucket and its position among that bucket's members.
+constexpr int kBuckets = 16;
+
+__device__ __forceinline__ int length_bucket(const DecodeArgs& a, int s) {
+    const int L = clamp_len(a.lens[s], a.l_max);
+    return (int)(((int64_t)L * kBuckets) / ((int64_t)a.l_max + 1));
+}
+
 __device__ int rank_to_sequence(const DecodeArgs& a, int rank) {
     const int lane = threadIdx.x & 63;
-    const int mine = lane < a.batch ? clamp_len(a.lens[lane], a.l_max) : -1;
-    const int lo = __reduce_min_sync(~0ull, lane < a.batch ? mine : INT_MAX);
-    const int hi = __reduce_max_sync(~0ull, mine);
-    if (lo == hi) return rank;
-    int before = 0;  // sequences ordered ahead of this lane's
-    for (int j = 0; j < a.batch; ++j) {
-        const int other = __builtin_amdgcn_readlane(mine, j);
-        before += (other > mine) || (other == mine && j < lane);
+    if (a.batch <= 64) {
+        const int mine = lane < a.batch ? clamp_len(a.lens[lane], a.l_max) : -1;
+        const int lo = __reduce_min_sync(~0ull, lane < a.batch ? mine : INT_MAX);
+        const int hi = __reduce_max_sync(~0ull, mine);
+        if (lo == hi) return rank;
+        int before = 0;  // sequences ordered ahead of this lane's
+        for (int j = 0; j < a.batch; ++j) {
+            const int other = __builtin_amdgcn_readlane(mine, j);
+            before += (other > mine) || (other == mine && j < lane);
+        }
+        const unsigned long long hit = __ballot(lane < a.batch && before == rank);
+        return hit ? (int)__builtin_ctzll(hit) : rank;
     }
-    const unsigned long long hit = __ballot(lane < a.batch && before == rank);
-    return hit ? (int)__builtin_ctzll(hit) : rank;
+    // Bucket histogram (wave-uniform counts).
+    int count[kBuckets];
+#pragma unroll
+    for (int k = 0; k < kBuckets; ++k) count[k] = 0;
+    for (int c0 = 0; c0 < a.batch; c0 += 64) {
+        const int s = c0 + lane;
+        const int kb = s < a.batch ? length_bucket(a, s) : -1;
+#pragma unroll
+        for (int k = 0; k < kBuckets; ++k) count[k] += __popcll(__ballot(kb == k));
+    }
+    // The rank's bucket (longest first) and its position among the bucket's members.
+    int want = -1, pos = rank;
+#pragma unroll
+    for (int k = kBuckets - 1; k >= 0; --k) {
+        if (want < 0) {
+            if (pos < count[k]) want = k;
+            else pos -= count[k];
+        }
+    }
+    if (want < 0) return rank;  // rank outside the batch: not reached for grid rows < batch
+    for (int c0 = 0; c0 < a.batch; c0 += 64) {
+        const int s = c0 + lane;
+        const bool member = s < a.batch && length_bucket(a, s) == want;
+        const unsigned long long m = __ballot(member);
+        const int n = __popcll(m);
+        if (pos < n) {
+            // the member lane with `pos` members below it
+            const int below = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
+            const unsigned long long hit = __ballot(member && below == pos);
+            return c0 + (int)__builtin_ctzll(hit);
+        }
+        pos -= n;
+    }
+    return rank;
 }
 
 template <int D, int G, int NW, bool PAGED>

@@ -228,7 +228,7 @@ int run_decode(gqa_ctx* c, const void* q, const int32_t* lens, const void* k_new
     a.page_shift = c->page_shift;
     a.max_pages = c->max_pages;
     a.zero_row = c->zero_row;
-    a.longest_first = c->cfg.batch > 1 && c->cfg.batch <= 64;
+    a.longest_first = c->cfg.batch > 1;
     timer_begin(c, GQA_TIMER_DECODE, s);
     HIP_TRY(launch_decode(c->cfg.head_dim, c->group, a, s));
     timer_end(c, GQA_TIMER_DECODE, s);

@@ -35,8 +35,9 @@ struct DecodeArgs {
     int32_t page_shift;
     int32_t max_pages;
     const uint16_t* zero_row;
-    // Nonzero: grid row y runs the (y / H_kv)-th longest sequence (ties in index order) instead
-    // of sequence y / H_kv, so the longest sequences are dispatched first.  Needs batch <= 64.
+    // Nonzero: grid row y runs the (y / H_kv)-th longest sequence instead of sequence y / H_kv,
+    // so the longest sequences are dispatched first (exact order up to 64 sequences, by length
+    // bucket beyond).
     int32_t longest_first;
 };
 

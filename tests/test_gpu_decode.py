@@ -123,11 +123,11 @@ def test_decode_ragged_edges(hq, hkv, d):
         assert not out[0].any()
 
 
-@pytest.mark.parametrize("B", [64, 65])
+@pytest.mark.parametrize("B", [64, 65, 200])
 def test_decode_longest_first_order_is_invisible(B):
-    # Batches of up to 64 sequences are dispatched longest first (ranked inside the kernel, ties
-    # in index order); above 64 the grid keeps index order.  Either way every sequence's output
-    # must be the oracle's, and word for word the same when the batch is listed in another order.
+    # Sequences are dispatched longest first, ranked inside the kernel: exactly up to 64 sequences
+    # (ties in index order), by length bucket above.  Either way every sequence's output must be
+    # the oracle's, and word for word the same when the batch is listed in another order.
     rng = np.random.default_rng(600 + B)
     hq, hkv, d = 32, 8, 128
     lens = rng.choice(np.array([0, 1, 16, 17, 100, 256, 257, 300, 511, 600], np.int32), size=B)
