@@ -201,7 +201,9 @@ int gqa_read_perf(gqa_ctx* ctx, uint64_t* total_ticks, uint64_t* kernel_ticks,
  * and return without synchronising.  The context stream is a blocking HIP stream: work
  * on it is ordered both ways with the legacy default stream (handle 0, PyTorch's default
  * stream), so passing NULL from code that uses the default stream needs no extra sync.
- * A non-default caller stream gets no such ordering: pass that stream itself. */
+ * A non-default caller stream gets no such ordering: pass that stream itself.
+ * q, k_rows, v_rows and the prefill output o must be 16-byte aligned (the kernels move them
+ * in 16-byte vectors; any hipMalloc or PyTorch allocation is), else GQA_ERR_RANGE. */
 int gqa_append_kv_device(gqa_ctx* ctx, const void* k_rows, const void* v_rows,
                          const int32_t* positions, void* stream);
 int gqa_decode_device(gqa_ctx* ctx, const void* q, const int32_t* ctx_lens,

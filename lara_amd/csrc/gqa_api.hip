@@ -155,6 +155,10 @@ bool rows_backed(const gqa_ctx* c, int b, int64_t row0, int64_t n) {
 
 hipStream_t pick_stream(gqa_ctx* c, void* s) { return s ? (hipStream_t)s : c->stream; }
 
+// Device operands the kernels move in 16-byte vectors (Q, appended K/V rows, prefill output)
+// must be 16-byte aligned; nullptr passes (optional operands are checked for presence apart).
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
 int choose_chunk(const gqa_ctx* c, int max_len) {
     if (c->chunk_opt > 0) return c->chunk_opt;
     const int units = c->cfg.batch * c->cfg.n_kv_heads;
@@ -1084,6 +1088,7 @@ int gqa_decode(gqa_ctx* c, const uint16_t* q, const int32_t* ctx_lens, uint16_t*
 
 int gqa_decode_device(gqa_ctx* c, const void* q, const int32_t* ctx_lens, void* o, float* lse, void* stream) {
     if (!c || !q || !ctx_lens || !o) return GQA_ERR_NULL;
+    if (!aligned16(q)) return GQA_ERR_RANGE;
     return run_decode(c, q, ctx_lens, nullptr, nullptr, nullptr, o, lse, pick_stream(c, stream), c->cfg.max_seq_len);
 }
 
@@ -1126,6 +1131,7 @@ int gqa_decode_append(gqa_ctx* c, const uint16_t* q, const uint16_t* k_rows, con
 int gqa_decode_append_device(gqa_ctx* c, const void* q, const void* k_rows, const void* v_rows,
                              const int32_t* positions, const int32_t* ctx_lens, void* o, float* lse, void* stream) {
     if (!c || !q || !k_rows || !v_rows || !positions || !ctx_lens || !o) return GQA_ERR_NULL;
+    if (!aligned16(q) || !aligned16(k_rows) || !aligned16(v_rows)) return GQA_ERR_RANGE;
     return run_decode(c, q, ctx_lens, k_rows, v_rows, positions, o, lse, pick_stream(c, stream),
                       c->cfg.max_seq_len);
 }
@@ -1183,6 +1189,7 @@ int gqa_prefill_append_device(gqa_ctx* c, int32_t b, const void* q, const void* 
                               int32_t n_new, int32_t q_len, int32_t q_pos_base, int32_t kv_len, int32_t kv_pos_base,
                               int32_t causal, void* o, float* lse, void* stream) {
     if (!c || !q || !k_rows || !v_rows || !o) return GQA_ERR_NULL;
+    if (!aligned16(q) || !aligned16(k_rows) || !aligned16(v_rows) || !aligned16(o)) return GQA_ERR_RANGE;
     int rc = check_prefill_args(c, b, q_len, q_pos_base, kv_len, kv_pos_base);
     if (rc != GQA_OK) return rc;
     if (!rows_backed(c, b, 0, kv_len)) return GQA_ERR_RANGE;
@@ -1194,6 +1201,7 @@ int gqa_prefill_append_device(gqa_ctx* c, int32_t b, const void* q, const void* 
 int gqa_prefill_device(gqa_ctx* c, int32_t b, const void* q, int32_t q_len, int32_t q_pos_base, int32_t kv_len,
                        int32_t kv_pos_base, int32_t causal, void* o, float* lse, void* stream) {
     if (!c || !q || !o) return GQA_ERR_NULL;
+    if (!aligned16(q) || !aligned16(o)) return GQA_ERR_RANGE;
     int rc = check_prefill_args(c, b, q_len, q_pos_base, kv_len, kv_pos_base);
     if (rc != GQA_OK) return rc;
     if (!rows_backed(c, b, 0, kv_len)) return GQA_ERR_RANGE;
@@ -1310,6 +1318,7 @@ int gqa_graph_capture_decode_append(gqa_ctx* c, const void* q, const void* k_row
     if ((k_rows == nullptr) != (v_rows == nullptr) || (k_rows != nullptr && positions == nullptr))
         return GQA_ERR_NULL;
     *out = nullptr;
+    if (!aligned16(q) || !aligned16(k_rows) || !aligned16(v_rows)) return GQA_ERR_RANGE;
     int rc = txn_idle(c);
     if (rc != GQA_OK) return rc;
     HIP_TRY(hipSetDevice(c->cfg.device));

@@ -529,17 +529,18 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
 // Merge of a row's KV segments.  Segment s holds keys [s*seg_len, (s+1)*seg_len); a row
 // reads the segments below its own key limit, which are exactly the ones prefill_kernel
 // wrote for it.  A work-group merges kMergeRows rows of one query head; each row is handled
-// by D/4 threads owning four dims (8-byte fp16 loads).  The (m, l, scale) rows and O slices of
-// up to kMergeBatch segments are loaded together, so a row pays one memory latency per batch.
-constexpr int kMergeRows = 8;
+// by D/8 threads owning eight dims (16-byte fp16 loads).  The (m, l, scale) rows and O slices
+// of up to kMergeBatch segments are loaded together, so a row pays one memory latency per batch.
+constexpr int kMergeRows = 16;
 constexpr int kMergeBatch = 8;
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 template <int D>
-__global__ __launch_bounds__(kMergeRows * D / 4) void prefill_combine_kernel(PrefillArgs a) {
-    constexpr int TPR = D / 4;  // threads per row
+__global__ __launch_bounds__(kMergeRows * D / 8) void prefill_combine_kernel(PrefillArgs a) {
+    constexpr int TPR = D / 8;  // threads per row
     const int hq = blockIdx.y;
     const int row = blockIdx.x * kMergeRows + threadIdx.x / TPR;
-    const int d4 = threadIdx.x % TPR;
+    const int d8 = threadIdx.x % TPR;
     if (row >= a.q_len) return;
     int hi = a.kv_len;
     if (a.causal) hi = min(hi, a.q_pos_base + row - a.kv_pos_base + 1);
@@ -548,22 +549,21 @@ __global__ __launch_bounds__(kMergeRows * D / 4) void prefill_combine_kernel(Pre
     const size_t seg_stride = (size_t)a.n_q_heads * a.q_len;
     const size_t prow = (size_t)hq * a.q_len + row;
     const float4* ml = reinterpret_cast<const float4*>(a.part_ml) + prow;
-    const uint2* po = reinterpret_cast<const uint2*>(a.part_o) + prow * TPR + d4;
+    const uint4* po = reinterpret_cast<const uint4*>(a.part_o) + prow * TPR + d8;
     float M = -INFINITY;  // running max over the merged segments (log2 units)
-    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+    float O[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     float Ls = 0.f;
     for (int s0 = 0; s0 < n_valid; s0 += kMergeBatch) {
         float4 e[kMergeBatch];  // (m, l, scale, -) of the segment
-        float4 v[kMergeBatch];  // four dims of the segment's O / l / scale
+        f16x8 v[kMergeBatch];   // eight dims of the segment's O / l / scale
 #pragma unroll
         for (int j = 0; j < kMergeBatch; ++j) {
             if (s0 + j < n_valid) {
                 e[j] = ml[(size_t)(s0 + j) * seg_stride];
-                const f16x4 h = __builtin_bit_cast(f16x4, po[(size_t)(s0 + j) * seg_stride * TPR]);
-                v[j] = make_float4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
+                v[j] = __builtin_bit_cast(f16x8, po[(size_t)(s0 + j) * seg_stride * TPR]);
             } else {
                 e[j] = make_float4(-INFINITY, 0.f, 0.f, 0.f);
-                v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+                v[j] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
             }
         }
         float bm = M;
@@ -571,29 +571,27 @@ __global__ __launch_bounds__(kMergeRows * D / 4) void prefill_combine_kernel(Pre
         for (int j = 0; j < kMergeBatch; ++j) bm = fmaxf(bm, e[j].x);
         if (bm == -INFINITY) continue;  // no valid key in the segments so far
         const float corr = __builtin_amdgcn_exp2f(M - bm);  // 0 while M = -inf
-        O.x *= corr;
-        O.y *= corr;
-        O.z *= corr;
-        O.w *= corr;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) O[i] *= corr;
         Ls *= corr;
 #pragma unroll
         for (int j = 0; j < kMergeBatch; ++j) {
             const float wl = __builtin_amdgcn_exp2f(e[j].x - bm) * e[j].y;  // 0 for a segment past n_valid
             const float w = wl * e[j].z;                                    // O_s = l * scale * v
-            O.x = fmaf(w, v[j].x, O.x);
-            O.y = fmaf(w, v[j].y, O.y);
-            O.z = fmaf(w, v[j].z, O.z);
-            O.w = fmaf(w, v[j].w, O.w);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) O[i] = fmaf(w, (float)v[j][i], O[i]);
             Ls += wl;
         }
         M = bm;
     }
     const float inv = Ls > 0.f ? 1.f / Ls : 0.f;
-    uint2 w;
-    w.x = (uint32_t)f32_to_bf16_rne(O.x * inv) | ((uint32_t)f32_to_bf16_rne(O.y * inv) << 16);
-    w.y = (uint32_t)f32_to_bf16_rne(O.z * inv) | ((uint32_t)f32_to_bf16_rne(O.w * inv) << 16);
-    *reinterpret_cast<uint2*>(a.out + prow * D + 4 * d4) = w;
-    if (d4 == 0 && a.lse != nullptr) a.lse[prow] = Ls > 0.f ? (M + log2f(Ls)) * kLn2 : -INFINITY;
+    uint4 w;
+    w.x = (uint32_t)f32_to_bf16_rne(O[0] * inv) | ((uint32_t)f32_to_bf16_rne(O[1] * inv) << 16);
+    w.y = (uint32_t)f32_to_bf16_rne(O[2] * inv) | ((uint32_t)f32_to_bf16_rne(O[3] * inv) << 16);
+    w.z = (uint32_t)f32_to_bf16_rne(O[4] * inv) | ((uint32_t)f32_to_bf16_rne(O[5] * inv) << 16);
+    w.w = (uint32_t)f32_to_bf16_rne(O[6] * inv) | ((uint32_t)f32_to_bf16_rne(O[7] * inv) << 16);
+    *reinterpret_cast<uint4*>(a.out + prow * D + 8 * d8) = w;
+    if (d8 == 0 && a.lse != nullptr) a.lse[prow] = Ls > 0.f ? (M + log2f(Ls)) * kLn2 : -INFINITY;
 }
 
 template <int D, int G>
@@ -631,9 +629,9 @@ size_t prefill_workspace_floats(const PrefillPlan& p, int q_len, int n_q_heads, 
 hipError_t launch_prefill_combine(int head_dim, const PrefillArgs& a, hipStream_t s) {
     const dim3 grid((a.q_len + kMergeRows - 1) / kMergeRows, a.n_q_heads);
     if (head_dim == 128) {
-        hipLaunchKernelGGL(prefill_combine_kernel<128>, grid, dim3(kMergeRows * 32), 0, s, a);
+        hipLaunchKernelGGL(prefill_combine_kernel<128>, grid, dim3(kMergeRows * 16), 0, s, a);
     } else if (head_dim == 64) {
-        hipLaunchKernelGGL(prefill_combine_kernel<64>, grid, dim3(kMergeRows * 16), 0, s, a);
+        hipLaunchKernelGGL(prefill_combine_kernel<64>, grid, dim3(kMergeRows * 8), 0, s, a);
     } else {
         return hipErrorInvalidValue;
     }

@@ -60,3 +60,27 @@ def test_null_stream_calls_are_ordered_with_the_default_stream():
     ref, _ = orc.attention(orc.bf16_u16_to_fp32(q[0][:, None]), orc.bf16_u16_to_fp32(kw), orc.bf16_u16_to_fp32(vw),
                            causal=False)
     assert float(orc.row_ulp_error(o[0][:, None], ref).max()) <= 2.0
+
+
+def test_device_entry_points_refuse_misaligned_vector_operands():
+    # Q, appended K/V rows and the prefill output are moved in 16-byte vectors: a pointer off a
+    # 16-byte boundary is refused on the host (GQA_ERR_RANGE) before anything is launched.
+    c = ctypes.c_void_p
+    lib = _lib.lib()
+    with AttentionAccelerator(batch=2, max_seq_len=256, max_q_len=64) as acc:
+        buf = torch.zeros(1 << 20, dtype=torch.int16, device="cuda")  # 256-byte aligned base
+        ok, off = buf.data_ptr(), buf.data_ptr() + 8
+        lens = torch.tensor([16, 16], dtype=torch.int32, device="cuda")
+        pos = torch.tensor([15, 15], dtype=torch.int32, device="cuda")
+        o = ok + (1 << 19)
+        lp = c(lens.data_ptr())
+        assert lib.gqa_decode_device(acc._ctx, c(off), lp, c(o), None, None) == _lib.GQA_ERR_RANGE
+        assert lib.gqa_decode_append_device(acc._ctx, c(ok), c(off), c(ok), c(pos.data_ptr()), lp, c(o), None,
+                                            None) == _lib.GQA_ERR_RANGE
+        assert lib.gqa_prefill_device(acc._ctx, 0, c(ok), 16, 0, 16, 0, 1, c(o + 8), None, None) == _lib.GQA_ERR_RANGE
+        assert lib.gqa_prefill_append_device(acc._ctx, 0, c(ok), c(ok), c(off), 16, 16, 0, 16, 0, 1, c(o), None,
+                                             None) == _lib.GQA_ERR_RANGE
+        # the aligned forms of the same calls run
+        _lib.check(lib.gqa_decode_device(acc._ctx, c(ok), lp, c(o), None, None), "aligned decode")
+        _lib.check(lib.gqa_prefill_device(acc._ctx, 0, c(ok), 16, 0, 16, 0, 1, c(o), None, None), "aligned prefill")
+        torch.cuda.synchronize()
