@@ -496,14 +496,14 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
 }
 
 // Log-sum-exp merge of the split partials: one work-group per (sequence, kv head, query
-// head of the group), one thread per dim.  The per-split weights exp2(m_s - M) are
-// computed once into LDS (dynamic, max_splits floats), then every thread streams its
-// column of the partial O with independent loads.
+// head of the group), one thread per dim.  Each thread loads the (m, l) pairs (the same address
+// across the work-group) and its dim of the partial O of kCombineBatch splits together and
+// folds them into a running (M, O, l) with one rescale per batch, so a sequence pays one memory
+// round trip per batch of splits; no LDS and no barrier.
+constexpr int kCombineBatch = 8;
+
 template <int D, int G>
 __global__ __launch_bounds__(D) void decode_combine_kernel(DecodeArgs a) {
-    extern __shared__ float lds_w[];  // [max_splits] split weights
-    __shared__ float red[D / 64];
-    __shared__ float bcast;
     const int unit = blockIdx.x;
     const int g = blockIdx.y;
     const int b = unit / a.n_kv_heads;
@@ -512,48 +512,39 @@ __global__ __launch_bounds__(D) void decode_combine_kernel(DecodeArgs a) {
     const int n_splits = L > 0 ? (L + a.chunk - 1) / a.chunk : 1;
     if (n_splits <= 1) return;  // written directly by the split kernel
     const int d = threadIdx.x;
-    const int lane = d & 63;
-    const int wave = d >> 6;
     const size_t base = (size_t)unit * a.max_splits * G + g;  // partial index of split 0
-
-    float m = -INFINITY;
-    for (int sp = d; sp < n_splits; sp += D) m = fmaxf(m, a.part_ml[(base + (size_t)sp * G) * 2]);
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-    if (lane == 0) red[wave] = m;
-    __syncthreads();
-    if (d == 0) {
-        float M = red[0];
-        for (int w = 1; w < D / 64; ++w) M = fmaxf(M, red[w]);
-        bcast = M;
-    }
-    __syncthreads();
-    const float M = bcast;
-    float ls = 0.f;
-    for (int sp = d; sp < n_splits; sp += D) {
-        const size_t pidx = base + (size_t)sp * G;
-        const float w = (M == -INFINITY) ? 0.f : fast_exp2(a.part_ml[pidx * 2] - M);
-        lds_w[sp] = w;
-        ls = fmaf(w, a.part_ml[pidx * 2 + 1], ls);
-    }
-    for (int off = 32; off > 0; off >>= 1) ls += __shfl_xor(ls, off);
-    __syncthreads();  // lds_w complete; red[] free again
-    if (lane == 0) red[wave] = ls;
-    __syncthreads();
-    float Ls = 0.f;
-    for (int w = 0; w < D / 64; ++w) Ls += red[w];
-
+    const float2* ml = reinterpret_cast<const float2*>(a.part_ml) + base;
     const float* po = a.part_o + base * D + d;
-    const size_t stride = (size_t)G * D;
-    float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
-    int sp = 0;
-    for (; sp + 4 <= n_splits; sp += 4) {
-        o0 = fmaf(lds_w[sp + 0], po[(size_t)(sp + 0) * stride], o0);
-        o1 = fmaf(lds_w[sp + 1], po[(size_t)(sp + 1) * stride], o1);
-        o2 = fmaf(lds_w[sp + 2], po[(size_t)(sp + 2) * stride], o2);
-        o3 = fmaf(lds_w[sp + 3], po[(size_t)(sp + 3) * stride], o3);
+    const size_t stride = (size_t)G;  // partial rows between consecutive splits
+    float M = -INFINITY, O = 0.f, Ls = 0.f;
+    for (int s0 = 0; s0 < n_splits; s0 += kCombineBatch) {
+        float2 e[kCombineBatch];
+        float v[kCombineBatch];
+#pragma unroll
+        for (int j = 0; j < kCombineBatch; ++j) {
+            if (s0 + j < n_splits) {
+                e[j] = ml[(size_t)(s0 + j) * stride];
+                v[j] = po[(size_t)(s0 + j) * stride * D];
+            } else {
+                e[j] = make_float2(-INFINITY, 0.f);
+                v[j] = 0.f;
+            }
+        }
+        float bm = M;
+#pragma unroll
+        for (int j = 0; j < kCombineBatch; ++j) bm = fmaxf(bm, e[j].x);
+        if (bm == -INFINITY) continue;  // no valid key in the splits so far
+        const float corr = fast_exp2(M - bm);  // 0 while M = -inf
+        O *= corr;
+        Ls *= corr;
+#pragma unroll
+        for (int j = 0; j < kCombineBatch; ++j) {
+            const float w = fast_exp2(e[j].x - bm);  // 0 for a split past n_splits
+            O = fmaf(w, v[j], O);
+            Ls = fmaf(w, e[j].y, Ls);
+        }
+        M = bm;
     }
-    for (; sp < n_splits; ++sp) o0 = fmaf(lds_w[sp], po[(size_t)sp * stride], o0);
-    const float O = (o0 + o1) + (o2 + o3);
     const size_t row = (size_t)b * a.n_kv_heads * G + h * G + g;
     a.out[row * D + d] = f32_to_bf16_rne(Ls > 0.f ? O / Ls : 0.f);
     if (d == 0 && a.lse != nullptr) a.lse[row] = Ls > 0.f ? (M + log2f(Ls)) * kLn2 : -INFINITY;
@@ -582,8 +573,7 @@ hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t s) {
 
 template <int D, int G>
 hipError_t launch_combine_t(const DecodeArgs& a, hipStream_t s) {
-    const size_t lds = (size_t)a.max_splits * sizeof(float);
-    hipLaunchKernelGGL((decode_combine_kernel<D, G>), dim3(a.batch * a.n_kv_heads, G), dim3(D), lds, s, a);
+    hipLaunchKernelGGL((decode_combine_kernel<D, G>), dim3(a.batch * a.n_kv_heads, G), dim3(D), 0, s, a);
     return hipGetLastError();
 }
 
