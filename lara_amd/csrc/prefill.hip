@@ -608,13 +608,15 @@ hipError_t launch_prefill_t(const PrefillArgs& a, hipStream_t s) {
 
 }  // namespace
 
+constexpr int kMinSegBlocks = 2;  // key blocks per KV segment, at least
+
 PrefillPlan plan_prefill(int q_len, int kv_span, int group, int n_kv_heads, int target_wgs, int max_segs) {
     const int n_rb = (q_len + kRows - 1) / kRows;
     const int base = ((n_rb * group + kWaves - 1) / kWaves) * n_kv_heads;
     const int blocks = (kv_span + kBN - 1) / kBN;
     int segs = (target_wgs + base - 1) / base;
     segs = min(segs, max_segs);
-    segs = min(segs, blocks);
+    segs = min(segs, blocks / kMinSegBlocks);  // a segment of one block pays a whole work-group's fixed cost
     if (segs <= 1) return PrefillPlan{blocks > 0 ? blocks * kBN : kBN, 1};
     const int seg_blocks = (blocks + segs - 1) / segs;
     const int seg_len = seg_blocks * kBN;
