@@ -86,16 +86,19 @@ def timed_passes(lib, _lib, ctx, stream, step, steps: int, warmup: int) -> dict:
     gpu_ms = ev0.elapsed_time(ev1) / steps
     _lib.check(lib.gqa_set_option(ctx, _lib.GQA_OPT_PROFILE, 1), "profile on")
     try:
+        t1 = time.perf_counter()
         for _ in range(steps):
             step()
         torch.cuda.synchronize()
+        profiled_wall_ms = (time.perf_counter() - t1) * 1e3 / steps
         times = (ctypes.c_float * _lib.GQA_TIMER_COUNT)()
         counts = (ctypes.c_int32 * _lib.GQA_TIMER_COUNT)()
         _lib.check(lib.gqa_kernel_times(ctx, times, _lib.GQA_TIMER_COUNT), "kernel times")
         _lib.check(lib.gqa_kernel_launch_counts(ctx, counts, _lib.GQA_TIMER_COUNT), "counts")
     finally:
         _lib.check(lib.gqa_set_option(ctx, _lib.GQA_OPT_PROFILE, 0), "profile off")
-    return {"wall_ms": wall_ms, "gpu_ms": gpu_ms, "times": list(times), "counts": list(counts)}
+    return {"wall_ms": wall_ms, "gpu_ms": gpu_ms, "times": list(times), "counts": list(counts),
+            "profiled_wall_ms": profiled_wall_ms}
 
 
 class DecodeBench:
@@ -177,6 +180,7 @@ class DecodeBench:
             "decode_launches": int(t["counts"][_lib.GQA_TIMER_DECODE]),
             "combine_us": t["times"][_lib.GQA_TIMER_COMBINE],
             "combine_launches": int(t["counts"][_lib.GQA_TIMER_COMBINE]),
+            "profiled_us_per_step": t["profiled_wall_ms"] * 1e3,
         }
 
     def run_graph(self, steps: int, warmup: int) -> float:
@@ -310,7 +314,8 @@ class PrefillBench:
         merges = t["counts"][_lib.GQA_TIMER_COMBINE] / max(1, t["counts"][_lib.GQA_TIMER_PREFILL])
         return {"wall_ms_per_prompt": t["wall_ms"], "gpu_ms_per_prompt": t["gpu_ms"],
                 "prefill_us_per_launch": t["times"][_lib.GQA_TIMER_PREFILL],
-                "merge_us_per_launch": t["times"][_lib.GQA_TIMER_COMBINE] * merges}
+                "merge_us_per_launch": t["times"][_lib.GQA_TIMER_COMBINE] * merges,
+                "profiled_us_per_prompt": t["profiled_wall_ms"] * 1e3}
 
     def close(self) -> None:
         self.lib.gqa_destroy(self.ctx)
@@ -343,6 +348,7 @@ def measure_prefill(name: str, steps: int, warmup: int, target_wgs: int = 0) -> 
         "prompt_tflops": flops / (r["wall_ms_per_prompt"] * 1e-3) / 1e12,
         "kernel_timing": "per-launch events on the kernels' stream (isolated launches)",
         "tokens_per_s": w.prompt / (r["wall_ms_per_prompt"] * 1e-3),
+        "profiled_us_per_prompt": r["profiled_us_per_prompt"],
     }
     out["mfma_frac_of_bf16_peak"] = out["kernel_tflops"] / BF16_DENSE_TFLOPS if out["kernel_tflops"] else None
     log(f"{name}: {out['us_per_prompt']:.1f} us/prompt, prefill kernels {kern_us:.1f} us = "
@@ -824,7 +830,7 @@ def main() -> int:
             others[name] = measure_layer(name, max(10, args.steps // 4), max(2, args.warmup // 2), args.prefill_wgs)
             continue
         r = measure(name, max(10, args.steps // 2), max(2, args.warmup // 2), page_rows=args.page_rows)
-        others[name] = {k: r[k] for k in ("us_per_step", "step_gbps", "step_frac_of_peak", "decode_us",
+        others[name] = {k: r[k] for k in ("us_per_step", "profiled_us_per_step", "combine_us", "step_gbps", "step_frac_of_peak", "decode_us",
                                            "decode_kernel_gbps", "decode_isolated_us", "decode_launches_per_step",
                                            "tokens_per_s", "graph_us_per_step") if k in r}
     cpu = None

@@ -561,20 +561,16 @@ constexpr int decode_waves_t() {
 }
 
 template <int D, int G>
-hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t s) {
+hipError_t launch_decode_t(const DecodeArgs& a, const Launch& l) {
     constexpr int NW = decode_waves_t<G>();
     dim3 grid(a.max_splits, a.batch * a.n_kv_heads);
-    if (a.block_table != nullptr)
-        hipLaunchKernelGGL((decode_split_kernel<D, G, NW, true>), grid, dim3(NW * 64), 0, s, a);
-    else
-        hipLaunchKernelGGL((decode_split_kernel<D, G, NW, false>), grid, dim3(NW * 64), 0, s, a);
-    return hipGetLastError();
+    if (a.block_table != nullptr) return launch_kernel(decode_split_kernel<D, G, NW, true>, grid, dim3(NW * 64), l, a);
+    return launch_kernel(decode_split_kernel<D, G, NW, false>, grid, dim3(NW * 64), l, a);
 }
 
 template <int D, int G>
-hipError_t launch_combine_t(const DecodeArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL((decode_combine_kernel<D, G>), dim3(a.batch * a.n_kv_heads, G), dim3(D), 0, s, a);
-    return hipGetLastError();
+hipError_t launch_combine_t(const DecodeArgs& a, const Launch& l) {
+    return launch_kernel(decode_combine_kernel<D, G>, dim3(a.batch * a.n_kv_heads, G), dim3(D), l, a);
 }
 
 }  // namespace
@@ -603,12 +599,12 @@ bool decode_supported(int head_dim, int group) {
         return hipErrorInvalidValue;                                   \
     } while (0)
 
-hipError_t launch_decode(int head_dim, int group, const DecodeArgs& a, hipStream_t s) {
-    LARA_DISPATCH_DG(launch_decode_t, head_dim, group, a, s);
+hipError_t launch_decode(int head_dim, int group, const DecodeArgs& a, const Launch& l) {
+    LARA_DISPATCH_DG(launch_decode_t, head_dim, group, a, l);
 }
 
-hipError_t launch_combine(int head_dim, int group, const DecodeArgs& a, hipStream_t s) {
-    LARA_DISPATCH_DG(launch_combine_t, head_dim, group, a, s);
+hipError_t launch_combine(int head_dim, int group, const DecodeArgs& a, const Launch& l) {
+    LARA_DISPATCH_DG(launch_combine_t, head_dim, group, a, l);
 }
 
 

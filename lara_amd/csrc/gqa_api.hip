@@ -159,10 +159,11 @@ hipStream_t pick_stream(gqa_ctx* c, void* s) { return s ? (hipStream_t)s : c->st
 // must be 16-byte aligned; nullptr passes (optional operands are checked for presence apart).
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-int choose_chunk(const gqa_ctx* c, int max_len) {
-    if (c->chunk_opt > 0) return c->chunk_opt;
-    const int units = c->cfg.batch * c->cfg.n_kv_heads;
-    const int target_wgs = kDecodeWavesPerCu * c->n_cu / decode_waves(c->group);
+// Keys per split for max_len attended keys: about kDecodeWavesPerCu waves per CU over the batch's
+// units, each split a multiple of kMinChunk.
+int plan_chunk(int batch, int n_kv_heads, int group, int n_cu, int max_len) {
+    const int units = batch * n_kv_heads;
+    const int target_wgs = kDecodeWavesPerCu * n_cu / decode_waves(group);
     int splits = (target_wgs + units - 1) / units;
     if (splits < 1) splits = 1;
     int chunk = (max_len + splits - 1) / splits;
@@ -171,18 +172,24 @@ int choose_chunk(const gqa_ctx* c, int max_len) {
     return chunk;
 }
 
-constexpr int kProfileLaunches = 512;  // event pairs kept per timer slot
-
-void timer_begin(gqa_ctx* c, int slot, hipStream_t s) {
-    if (c->profile && !c->capturing && c->ev_count[slot] < kProfileLaunches)
-        (void)hipEventRecord(c->ev_pool[slot][2 * c->ev_count[slot]], s);
+int choose_chunk(const gqa_ctx* c, int max_len) {
+    if (c->chunk_opt > 0) return c->chunk_opt;
+    return plan_chunk(c->cfg.batch, c->cfg.n_kv_heads, c->group, c->n_cu, max_len);
 }
 
-void timer_end(gqa_ctx* c, int slot, hipStream_t s) {
+constexpr int kProfileLaunches = 512;  // event pairs kept per timer slot
+
+// A launch on stream s; while profiling (outside a graph capture), with the next event pair of
+// the timer slot bound to the launch itself (no marker commands between launches).
+Launch timed(gqa_ctx* c, int slot, hipStream_t s) {
+    Launch l;
+    l.stream = s;
     if (c->profile && !c->capturing && c->ev_count[slot] < kProfileLaunches) {
-        (void)hipEventRecord(c->ev_pool[slot][2 * c->ev_count[slot] + 1], s);
+        l.start = c->ev_pool[slot][2 * c->ev_count[slot]];
+        l.stop = c->ev_pool[slot][2 * c->ev_count[slot] + 1];
         c->ev_count[slot] += 1;
     }
+    return l;
 }
 
 void timers_reset(gqa_ctx* c) {
@@ -233,14 +240,8 @@ int run_decode(gqa_ctx* c, const void* q, const int32_t* lens, const void* k_new
     a.max_pages = c->max_pages;
     a.zero_row = c->zero_row;
     a.longest_first = c->cfg.batch > 1;
-    timer_begin(c, GQA_TIMER_DECODE, s);
-    HIP_TRY(launch_decode(c->cfg.head_dim, c->group, a, s));
-    timer_end(c, GQA_TIMER_DECODE, s);
-    if (max_splits > 1) {
-        timer_begin(c, GQA_TIMER_COMBINE, s);
-        HIP_TRY(launch_combine(c->cfg.head_dim, c->group, a, s));
-        timer_end(c, GQA_TIMER_COMBINE, s);
-    }
+    HIP_TRY(launch_decode(c->cfg.head_dim, c->group, a, timed(c, GQA_TIMER_DECODE, s)));
+    if (max_splits > 1) HIP_TRY(launch_combine(c->cfg.head_dim, c->group, a, timed(c, GQA_TIMER_COMBINE, s)));
     return GQA_OK;
 }
 
@@ -288,9 +289,7 @@ int run_prefill(gqa_ctx* c, int32_t b, const void* q, int32_t q_len, int32_t q_p
         r.scale_bits = sb;
         r.out = (uint16_t*)o;
         r.lse = lse;
-        timer_begin(c, GQA_TIMER_PREFILL, s);
-        HIP_TRY(launch_rtl_transaction(c->cfg.head_dim, r, s));
-        timer_end(c, GQA_TIMER_PREFILL, s);
+        HIP_TRY(launch_rtl_transaction(c->cfg.head_dim, r, timed(c, GQA_TIMER_PREFILL, s)));
         return GQA_OK;
     }
     if (!prefill_supported(c->cfg.head_dim, c->group)) return GQA_ERR_UNSUPPORTED;
@@ -327,14 +326,8 @@ int run_prefill(gqa_ctx* c, int32_t b, const void* q, int32_t q_len, int32_t q_p
     a.zero_row = c->zero_row;
     a.part_o = reinterpret_cast<uint16_t*>(c->pre_ws);
     a.part_ml = c->pre_ws + (size_t)plan.n_segs * c->cfg.n_q_heads * q_len * (c->cfg.head_dim / 2);
-    timer_begin(c, GQA_TIMER_PREFILL, s);
-    HIP_TRY(launch_prefill(c->cfg.head_dim, c->group, a, s));
-    timer_end(c, GQA_TIMER_PREFILL, s);
-    if (plan.n_segs > 1) {
-        timer_begin(c, GQA_TIMER_COMBINE, s);
-        HIP_TRY(launch_prefill_combine(c->cfg.head_dim, a, s));
-        timer_end(c, GQA_TIMER_COMBINE, s);
-    }
+    HIP_TRY(launch_prefill(c->cfg.head_dim, c->group, a, timed(c, GQA_TIMER_PREFILL, s)));
+    if (plan.n_segs > 1) HIP_TRY(launch_prefill_combine(c->cfg.head_dim, a, timed(c, GQA_TIMER_COMBINE, s)));
     return GQA_OK;
 }
 
@@ -522,7 +515,7 @@ int run_layer_qkv(gqa_ctx* c, int32_t b, const void* x, int32_t n_tokens, int32_
         na.n_tokens = n_tokens;
         na.hidden = hidden;
         na.eps = eps;
-        HIP_TRY(launch_rms_norm(na, s));
+        HIP_TRY(launch_rms_norm(na, Launch{s}));
         src = na.y;
     }
     HIP_TRY(mark(1));
@@ -581,7 +574,7 @@ int run_layer_qkv(gqa_ctx* c, int32_t b, const void* x, int32_t n_tokens, int32_
     ra.l_cap = c->l_cap;
     ra.row0 = row0;
     for (int p = 0; p < D / 2; ++p) ra.theta[p] = (float)pow(kRopeBase, -2.0 * p / D);
-    HIP_TRY(launch_rope_scatter(ra, s));
+    HIP_TRY(launch_rope_scatter(ra, Launch{s}));
     HIP_TRY(mark(3));
     c->layer_timed = timed;
     return GQA_OK;
@@ -1050,11 +1043,10 @@ int gqa_append_kv_device(gqa_ctx* c, const void* k_rows, const void* v_rows, con
                          void* stream) {
     if (!c || !k_rows || !v_rows || !positions) return GQA_ERR_NULL;
     hipStream_t s = pick_stream(c, stream);
-    timer_begin(c, GQA_TIMER_APPEND, s);
     HIP_TRY(launch_append((const uint16_t*)k_rows, (const uint16_t*)v_rows, positions, c->k_cache, c->v_cache,
                           c->cfg.batch, c->cfg.n_kv_heads, c->cfg.head_dim, c->l_cap, c->cfg.max_seq_len,
-                          c->paged ? c->table_dev : nullptr, c->page_shift, c->max_pages, s));
-    timer_end(c, GQA_TIMER_APPEND, s);
+                          c->paged ? c->table_dev : nullptr, c->page_shift, c->max_pages,
+                          timed(c, GQA_TIMER_APPEND, s)));
     return GQA_OK;
 }
 

@@ -1,12 +1,31 @@
 // Internal declarations shared by the libgqa translation units (not part of the ABI).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 namespace lara {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Where a kernel goes: its stream and, while profiling, a start/stop event pair that the runtime
+// stamps with the launch's own begin and end (hipExtLaunchKernel binds them to the dispatch
+// itself, so no marker command sits between timed launches and they run back to back).
+struct Launch {
+    hipStream_t stream = nullptr;
+    hipEvent_t start = nullptr;
+    hipEvent_t stop = nullptr;
+};
+
+template <typename... KArgs, typename... Args>
+inline hipError_t launch_kernel(void (*kernel)(KArgs...), dim3 grid, dim3 block, const Launch& l, Args... args) {
+    if (l.start != nullptr || l.stop != nullptr)
+        hipExtLaunchKernelGGL(kernel, grid, block, 0, l.stream, l.start, l.stop, 0, args...);
+    else
+        hipLaunchKernelGGL(kernel, grid, block, 0, l.stream, args...);
+    return hipGetLastError();
+}
 
 // Split-KV decode launch description.  All pointers are device pointers.
 struct DecodeArgs {
@@ -108,27 +127,27 @@ struct RtlArgs {
     uint16_t* out;          // [H_q][q_len][D] bf16
     float* lse;             // [H_q][q_len] or nullptr
 };
-hipError_t launch_rtl_transaction(int head_dim, const RtlArgs& a, hipStream_t s);
+hipError_t launch_rtl_transaction(int head_dim, const RtlArgs& a, const Launch& l);
 
 bool decode_supported(int head_dim, int group);
 // Waves per split work-group of the decode kernel for a group size.
 int decode_waves(int group);
 // Split-KV attention with an optional fused row append; sequences longer than one split
 // leave fp32 partials that launch_combine merges.
-hipError_t launch_decode(int head_dim, int group, const DecodeArgs& a, hipStream_t s);
-hipError_t launch_combine(int head_dim, int group, const DecodeArgs& a, hipStream_t s);
+hipError_t launch_decode(int head_dim, int group, const DecodeArgs& a, const Launch& l);
+hipError_t launch_combine(int head_dim, int group, const DecodeArgs& a, const Launch& l);
 
 bool prefill_supported(int head_dim, int group);
-hipError_t launch_prefill(int head_dim, int group, const PrefillArgs& a, hipStream_t s);
+hipError_t launch_prefill(int head_dim, int group, const PrefillArgs& a, const Launch& l);
 // Merges the KV segments of a prefill launch with n_segs > 1.
-hipError_t launch_prefill_combine(int head_dim, const PrefillArgs& a, hipStream_t s);
+hipError_t launch_prefill_combine(int head_dim, const PrefillArgs& a, const Launch& l);
 
 // K/V row append: rows [B][H_kv][D] -> cache row positions[b] (skipped if < 0 or >= l_max, or,
 // in a paged cache (block_table != nullptr, [B][max_pages]), if the row's page is unmapped).
 hipError_t launch_append(const uint16_t* k_rows, const uint16_t* v_rows, const int32_t* positions,
                          uint16_t* kc, uint16_t* vc, int batch, int n_kv_heads, int head_dim,
                          int l_cap, int l_max, const int32_t* block_table, int page_shift, int max_pages,
-                         hipStream_t s);
+                         const Launch& l);
 
 // Layer input stage of run_layer (sw/attn_driver.py:552-576): RMSNorm of the hidden states
 // and, after the QKV projection GEMM, RoPE plus the head-major scatter of Q and of K/V into
@@ -140,7 +159,7 @@ struct NormArgs {
     int n_tokens, hidden;
     float eps;
 };
-hipError_t launch_rms_norm(const NormArgs& a, hipStream_t s);
+hipError_t launch_rms_norm(const NormArgs& a, const Launch& l);
 
 constexpr int kMaxRopePairs = 64;  // head_dim <= 128
 struct RopeArgs {
@@ -156,7 +175,7 @@ struct RopeArgs {
     int page_shift;
     float theta[kMaxRopePairs];  // rotation frequency of pair (2p, 2p+1)
 };
-hipError_t launch_rope_scatter(const RopeArgs& a, hipStream_t s);
+hipError_t launch_rope_scatter(const RopeArgs& a, const Launch& l);
 
 // fp32 -> bf16 word, round to nearest even on the upper half: the output rounding of
 // fp32_to_bf16 in hw/rtl/pkg/attn_pkg.sv:618-626 (no NaN special case).

@@ -40,16 +40,15 @@ __global__ __launch_bounds__(256) void append_kv_kernel(const u32x4* __restrict_
 hipError_t launch_append(const uint16_t* k_rows, const uint16_t* v_rows, const int32_t* positions,
                          uint16_t* kc, uint16_t* vc, int batch, int n_kv_heads, int head_dim,
                          int l_cap, int l_max, const int32_t* block_table, int page_shift, int max_pages,
-                         hipStream_t s) {
+                         const Launch& l) {
     const int words_per_row = head_dim / 8;
     const int n_words = batch * n_kv_heads * words_per_row;
     const int block = 256;
     const int grid = (n_words + block - 1) / block;
-    hipLaunchKernelGGL(append_kv_kernel, dim3(grid), dim3(block), 0, s,
-                       reinterpret_cast<const u32x4*>(k_rows), reinterpret_cast<const u32x4*>(v_rows),
-                       positions, reinterpret_cast<u32x4*>(kc), reinterpret_cast<u32x4*>(vc), n_words,
-                       words_per_row, n_kv_heads, l_cap, l_max, block_table, page_shift, max_pages);
-    return hipGetLastError();
+    return launch_kernel(append_kv_kernel, dim3(grid), dim3(block), l, reinterpret_cast<const u32x4*>(k_rows),
+                         reinterpret_cast<const u32x4*>(v_rows), positions, reinterpret_cast<u32x4*>(kc),
+                         reinterpret_cast<u32x4*>(vc), n_words, words_per_row, n_kv_heads, l_cap, l_max, block_table,
+                         page_shift, max_pages);
 }
 
 }  // namespace lara

@@ -162,18 +162,16 @@ __global__ __launch_bounds__(kRopeThreads) void rope_scatter_kernel(RopeArgs a) 
 
 }  // namespace
 
-hipError_t launch_rms_norm(const NormArgs& a, hipStream_t s) {
+hipError_t launch_rms_norm(const NormArgs& a, const Launch& l) {
     if (a.n_tokens < 1) return hipSuccess;
-    hipLaunchKernelGGL(rms_norm_kernel, dim3(a.n_tokens), dim3(kNormThreads), 0, s, a);
-    return hipGetLastError();
+    return launch_kernel(rms_norm_kernel, dim3(a.n_tokens), dim3(kNormThreads), l, a);
 }
 
-hipError_t launch_rope_scatter(const RopeArgs& a, hipStream_t s) {
+hipError_t launch_rope_scatter(const RopeArgs& a, const Launch& l) {
     if (a.n_tokens < 1) return hipSuccess;
     if (a.head_dim < 8 || a.head_dim > 2 * kMaxRopePairs || (a.head_dim & 7) || kRopeThreads % (a.head_dim / 8))
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(rope_scatter_kernel, dim3(a.n_tokens), dim3(kRopeThreads), 0, s, a);
-    return hipGetLastError();
+    return launch_kernel(rope_scatter_kernel, dim3(a.n_tokens), dim3(kRopeThreads), l, a);
 }
 
 }  // namespace lara

@@ -595,15 +595,12 @@ __global__ __launch_bounds__(kMergeRows * D / 8) void prefill_combine_kernel(Pre
 }
 
 template <int D, int G>
-hipError_t launch_prefill_t(const PrefillArgs& a, hipStream_t s) {
+hipError_t launch_prefill_t(const PrefillArgs& a, const Launch& l) {
     const int n_rb = (a.q_len + kRows - 1) / kRows;
     const int n_tasks = n_rb * G;
     dim3 grid((n_tasks + kWaves - 1) / kWaves, a.n_kv_heads, a.n_segs);
-    if (a.block_table != nullptr)
-        hipLaunchKernelGGL((prefill_kernel<D, G, true>), grid, dim3(kWaves * 64), 0, s, a);
-    else
-        hipLaunchKernelGGL((prefill_kernel<D, G, false>), grid, dim3(kWaves * 64), 0, s, a);
-    return hipGetLastError();
+    if (a.block_table != nullptr) return launch_kernel(prefill_kernel<D, G, true>, grid, dim3(kWaves * 64), l, a);
+    return launch_kernel(prefill_kernel<D, G, false>, grid, dim3(kWaves * 64), l, a);
 }
 
 }  // namespace
@@ -628,35 +625,30 @@ size_t prefill_workspace_floats(const PrefillPlan& p, int q_len, int n_q_heads, 
     return (size_t)p.n_segs * n_q_heads * q_len * (head_dim / 2 + 4);  // fp16 O row + (m, l, scale, -)
 }
 
-hipError_t launch_prefill_combine(int head_dim, const PrefillArgs& a, hipStream_t s) {
+hipError_t launch_prefill_combine(int head_dim, const PrefillArgs& a, const Launch& l) {
     const dim3 grid((a.q_len + kMergeRows - 1) / kMergeRows, a.n_q_heads);
-    if (head_dim == 128) {
-        hipLaunchKernelGGL(prefill_combine_kernel<128>, grid, dim3(kMergeRows * 16), 0, s, a);
-    } else if (head_dim == 64) {
-        hipLaunchKernelGGL(prefill_combine_kernel<64>, grid, dim3(kMergeRows * 8), 0, s, a);
-    } else {
-        return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
+    if (head_dim == 128) return launch_kernel(prefill_combine_kernel<128>, grid, dim3(kMergeRows * 16), l, a);
+    if (head_dim == 64) return launch_kernel(prefill_combine_kernel<64>, grid, dim3(kMergeRows * 8), l, a);
+    return hipErrorInvalidValue;
 }
 
 bool prefill_supported(int head_dim, int group) {
     return (head_dim == 64 || head_dim == 128) && (group == 1 || group == 2 || group == 4 || group == 8 || group == 16);
 }
 
-hipError_t launch_prefill(int head_dim, int group, const PrefillArgs& a, hipStream_t s) {
+hipError_t launch_prefill(int head_dim, int group, const PrefillArgs& a, const Launch& l) {
     if (head_dim == 128) {
-        if (group == 4) return launch_prefill_t<128, 4>(a, s);
-        if (group == 8) return launch_prefill_t<128, 8>(a, s);
-        if (group == 2) return launch_prefill_t<128, 2>(a, s);
-        if (group == 1) return launch_prefill_t<128, 1>(a, s);
-        if (group == 16) return launch_prefill_t<128, 16>(a, s);
+        if (group == 4) return launch_prefill_t<128, 4>(a, l);
+        if (group == 8) return launch_prefill_t<128, 8>(a, l);
+        if (group == 2) return launch_prefill_t<128, 2>(a, l);
+        if (group == 1) return launch_prefill_t<128, 1>(a, l);
+        if (group == 16) return launch_prefill_t<128, 16>(a, l);
     } else if (head_dim == 64) {
-        if (group == 4) return launch_prefill_t<64, 4>(a, s);
-        if (group == 8) return launch_prefill_t<64, 8>(a, s);
-        if (group == 2) return launch_prefill_t<64, 2>(a, s);
-        if (group == 1) return launch_prefill_t<64, 1>(a, s);
-        if (group == 16) return launch_prefill_t<64, 16>(a, s);
+        if (group == 4) return launch_prefill_t<64, 4>(a, l);
+        if (group == 8) return launch_prefill_t<64, 8>(a, l);
+        if (group == 2) return launch_prefill_t<64, 2>(a, l);
+        if (group == 1) return launch_prefill_t<64, 1>(a, l);
+        if (group == 16) return launch_prefill_t<64, 16>(a, l);
     }
     return hipErrorInvalidValue;
 }

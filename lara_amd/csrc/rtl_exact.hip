@@ -313,16 +313,11 @@ __global__ __launch_bounds__(kLanes) void rtl_transaction_kernel(RtlArgs a) {
 
 }  // namespace
 
-hipError_t launch_rtl_transaction(int head_dim, const RtlArgs& a, hipStream_t s) {
+hipError_t launch_rtl_transaction(int head_dim, const RtlArgs& a, const Launch& l) {
     dim3 grid((a.q_len + kLanes - 1) / kLanes, a.n_q_heads);
-    if (head_dim == 128) {
-        hipLaunchKernelGGL(rtl_transaction_kernel<128>, grid, dim3(kLanes), 0, s, a);
-    } else if (head_dim == 64) {
-        hipLaunchKernelGGL(rtl_transaction_kernel<64>, grid, dim3(kLanes), 0, s, a);
-    } else {
-        return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
+    if (head_dim == 128) return launch_kernel(rtl_transaction_kernel<128>, grid, dim3(kLanes), l, a);
+    if (head_dim == 64) return launch_kernel(rtl_transaction_kernel<64>, grid, dim3(kLanes), l, a);
+    return hipErrorInvalidValue;
 }
 
 }  // namespace lara
