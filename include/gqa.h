@@ -44,6 +44,7 @@ extern "C" {
 #define GQA_ERR_TIMEOUT        0x25 /* gqa_wait deadline expired */
 #define GQA_ERR_NO_TRANSACTION 0x26 /* start/wait/read with nothing submitted */
 #define GQA_ERR_UNSUPPORTED    0x27 /* shape with no compiled kernel (head_dim, group) */
+#define GQA_ERR_SCRATCH        0x28 /* plan exceeds GQA_NOALLOC_SCRATCH_BYTES (gqa_decode_append_noalloc) */
 
 /* STATUS word bits returned by gqa_status (CSR_STATUS, attn_driver.py:51-57). */
 #define GQA_STATUS_START_READY (1u << 0)
@@ -223,6 +224,29 @@ int gqa_load_kv_device(gqa_ctx* ctx, int32_t b, int32_t start_pos, int32_t n,
                        const void* k, const void* v, void* stream);
 /* Device addresses of the K and V caches ([B][H_kv][L_cap][D] bf16) and L_cap. */
 int gqa_cache_pointers(gqa_ctx* ctx, void** k_cache, void** v_cache, int32_t* l_cap);
+
+/* ---- decode without allocation ------------------------------------------------------
+ * No counterpart in the reference (the board has no allocator to avoid).  For callers that
+ * cannot allocate device memory -- code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc: gqa_decode_append_device without a context.  The caller owns every
+ * buffer: k_cache and v_cache are [B][H_kv][l_cap][D] bf16 in device memory (l_cap a multiple of
+ * 64, >= cfg->max_seq_len; the layout of gqa_create's cache), q, k_rows, v_rows, positions,
+ * ctx_lens, o and lse as for gqa_decode_append_device (k_rows = v_rows = positions = NULL:
+ * attend only).  cfg supplies B, H_q, H_kv, D, max_seq_len, scale and device (max_q_len is
+ * ignored).  The call allocates nothing: the split-KV partials of sequences longer than one split
+ * live in a static device array of GQA_NOALLOC_SCRATCH_BYTES per device, held until the process
+ * ends (its last 256 bytes are a zero K/V row); a plan that needs more returns GQA_ERR_SCRATCH
+ * (the automatic plan needs at most about 9 MiB).  Every call on a device shares that array,
+ * which keeps the last call's partials (each call writes every partial it reads): calls that
+ * overlap on one device (other streams, other threads) race and must be serialised by the caller.
+ * The first call on a device sets the array up (address lookup, zero row; it synchronises the
+ * device) and returns GQA_ERR_UNSUPPORTED if `stream` is capturing: make one call before
+ * capturing.  Same kernels and split plan as gqa_decode_append_device for the same cfg, so the
+ * output words are the same. */
+#define GQA_NOALLOC_SCRATCH_BYTES (16u << 20)
+int gqa_decode_append_noalloc(const gqa_config* cfg, void* k_cache, void* v_cache, int32_t l_cap, const void* q,
+                              const void* k_rows, const void* v_rows, const int32_t* positions,
+                              const int32_t* ctx_lens, void* o, float* lse, void* stream);
 
 /* ---- layer input stage (run_layer) -------------------------------------------------
  * Replace the host RMSNorm / QKV projection / RoPE / reshape_to_heads of

@@ -28,6 +28,8 @@ GQA_ERR_RANGE = 0x24
 GQA_ERR_TIMEOUT = 0x25
 GQA_ERR_NO_TRANSACTION = 0x26
 GQA_ERR_UNSUPPORTED = 0x27
+GQA_ERR_SCRATCH = 0x28
+GQA_NOALLOC_SCRATCH_BYTES = 16 << 20
 
 GQA_STATUS_START_READY = 1 << 0
 GQA_STATUS_BUSY = 1 << 1
@@ -101,6 +103,8 @@ _SIGNATURES = {
     "gqa_decode_device": [_CTX, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p],
     "gqa_decode_append_device": [_CTX, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                  c_void_p],
+    "gqa_decode_append_noalloc": [POINTER(GqaConfig), c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_void_p,
+                                  c_void_p, c_void_p, c_void_p, c_void_p, c_void_p],
     "gqa_prefill_device": [_CTX, c_int32, c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_void_p,
                            c_void_p, c_void_p],
     "gqa_prefill_append_device": [_CTX, c_int32, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32,

@@ -8,6 +8,7 @@
 #include <hipblaslt/hipblaslt.h>
 
 #include <algorithm>
+#include <mutex>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -733,6 +734,58 @@ int copy_rows_paged(gqa_ctx* c, int b, int start, int n, const uint16_t* k_src, 
 
 }  // namespace
 
+// ---- decode without allocation (gqa_decode_append_noalloc) ---------------------------------
+// Split-KV partials of gqa_decode_append_noalloc: one copy per device, held until the process
+// ends.  Its last kNoAllocZeroBytes are the zero K/V row (the source of rows past a sequence's
+// length), cleared at set-up and never written afterwards.  Host code uses the per-device address
+// from hipGetSymbolAddress, never this name.
+static __device__ __align__(256) uint8_t scratch[GQA_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kNoAllocDevices = 64;
+constexpr size_t kNoAllocZeroBytes = 256;  // one K/V row of D <= 128 bf16 words
+constexpr size_t kNoAllocPartialBytes = GQA_NOALLOC_SCRATCH_BYTES - kNoAllocZeroBytes;
+
+struct NoAllocDevice {
+    bool ready = false;
+    uint8_t* scratch = nullptr;      // device address of `scratch` on this device
+    const uint16_t* zero = nullptr;  // its zero row
+    int n_cu = 0;
+};
+
+NoAllocDevice g_noalloc[kNoAllocDevices];
+std::mutex g_noalloc_mu;
+
+// Once per device, with that device current and outside any stream capture: the device address of
+// `scratch`, the zero row cleared (and finished before any launch that reads it), and the CU count
+// the split planner targets.
+int noalloc_setup(int device, hipStream_t stream, NoAllocDevice** out) {
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    NoAllocDevice& d = g_noalloc[device];
+    if (!d.ready) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        HIP_TRY(hipStreamIsCapturing(stream, &cs));
+        if (cs != hipStreamCaptureStatusNone) return GQA_ERR_UNSUPPORTED;  // set-up cannot be captured
+        hipDeviceProp_t prop;
+        if (hipGetDeviceProperties(&prop, device) != hipSuccess || strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+            return GQA_ERR_NO_DEVICE;
+        void* p = nullptr;
+        HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        uint8_t* base = static_cast<uint8_t*>(p);
+        HIP_TRY(hipMemset(base + kNoAllocPartialBytes, 0, kNoAllocZeroBytes));
+        HIP_TRY(hipDeviceSynchronize());
+        d.scratch = base;
+        d.zero = reinterpret_cast<const uint16_t*>(base + kNoAllocPartialBytes);
+        d.n_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+        d.ready = true;
+    }
+    *out = &d;
+    return GQA_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 const char* gqa_status_string(int32_t code) {
@@ -751,6 +804,7 @@ const char* gqa_status_string(int32_t code) {
         case GQA_ERR_TIMEOUT: return "timed out waiting for the transaction";
         case GQA_ERR_NO_TRANSACTION: return "no transaction has been submitted";
         case GQA_ERR_UNSUPPORTED: return "no kernel compiled for this head_dim / group size";
+        case GQA_ERR_SCRATCH: return "the split plan needs more than the no-allocation scratch (GQA_NOALLOC_SCRATCH_BYTES)";
         default: return "unknown status";
     }
 }
@@ -1126,6 +1180,65 @@ int gqa_decode_append_device(gqa_ctx* c, const void* q, const void* k_rows, cons
     if (!aligned16(q) || !aligned16(k_rows) || !aligned16(v_rows)) return GQA_ERR_RANGE;
     return run_decode(c, q, ctx_lens, k_rows, v_rows, positions, o, lse, pick_stream(c, stream),
                       c->cfg.max_seq_len);
+}
+
+int gqa_decode_append_noalloc(const gqa_config* cfg, void* k_cache, void* v_cache, int32_t l_cap, const void* q,
+                              const void* k_rows, const void* v_rows, const int32_t* positions,
+                              const int32_t* ctx_lens, void* o, float* lse, void* stream) {
+    if (!cfg || !k_cache || !v_cache || !q || !ctx_lens || !o) return GQA_ERR_NULL;
+    if ((k_rows == nullptr) != (v_rows == nullptr) || (k_rows != nullptr && positions == nullptr)) return GQA_ERR_NULL;
+    const gqa_config& k = *cfg;
+    if (k.batch < 1 || k.n_q_heads < 1 || k.n_kv_heads < 1 || k.n_q_heads % k.n_kv_heads != 0 || k.max_seq_len < 1 ||
+        k.max_seq_len > kMaxRows || !(k.scale >= 0.f) || !isfinite(k.scale))
+        return GQA_ERR_BAD_CFG;
+    const int group = k.n_q_heads / k.n_kv_heads;
+    if (!decode_supported(k.head_dim, group)) return GQA_ERR_UNSUPPORTED;
+    // Rounds of keys never straddle a (sequence, kv head) region: l_cap is a multiple of 64.
+    if (l_cap < k.max_seq_len || l_cap % 64 != 0 || l_cap > kMaxRows + 64) return GQA_ERR_RANGE;
+    if (!aligned16(q) || !aligned16(k_rows) || !aligned16(v_rows) || !aligned16(k_cache) || !aligned16(v_cache))
+        return GQA_ERR_RANGE;
+    int n_dev = 0;
+    if (hipGetDeviceCount(&n_dev) != hipSuccess || k.device < 0 || k.device >= n_dev || k.device >= kNoAllocDevices)
+        return GQA_ERR_NO_DEVICE;
+    HIP_TRY(hipSetDevice(k.device));
+    NoAllocDevice* dev = nullptr;
+    int rc = noalloc_setup(k.device, (hipStream_t)stream, &dev);
+    if (rc != GQA_OK) return rc;
+    // The plan gqa_decode_append_device makes for the same configuration (keys per split from the
+    // CU count and max_seq_len), so both entry points give the same words.
+    const int chunk = plan_chunk(k.batch, k.n_kv_heads, group, dev->n_cu, k.max_seq_len);
+    const int max_splits = (k.max_seq_len + chunk - 1) / chunk;
+    const size_t rows = (size_t)k.batch * k.n_kv_heads * max_splits * group;  // partial rows of the plan
+    const size_t o_bytes = max_splits > 1 ? (rows * k.head_dim * sizeof(float) + 255) / 256 * 256 : 0;
+    const size_t ml_bytes = max_splits > 1 ? rows * 2 * sizeof(float) : 0;
+    if (o_bytes + ml_bytes > kNoAllocPartialBytes) return GQA_ERR_SCRATCH;
+    DecodeArgs a{};
+    a.q = (const uint16_t*)q;
+    a.kc = (uint16_t*)k_cache;
+    a.vc = (uint16_t*)v_cache;
+    a.lens = ctx_lens;
+    a.k_new = (const uint16_t*)k_rows;
+    a.v_new = (const uint16_t*)v_rows;
+    a.positions = positions;
+    a.batch = k.batch;
+    a.n_kv_heads = k.n_kv_heads;
+    a.l_cap = l_cap;
+    a.l_max = k.max_seq_len;
+    a.chunk = chunk;
+    a.max_splits = max_splits;
+    const float scale = k.scale > 0.f ? k.scale : (float)(1.0 / sqrt((double)k.head_dim));
+    a.scale_log2 = scale * 1.4426950408889634f;
+    a.part_o = reinterpret_cast<float*>(dev->scratch);
+    a.part_ml = reinterpret_cast<float*>(dev->scratch + o_bytes);
+    a.out = (uint16_t*)o;
+    a.lse = lse;
+    a.zero_row = dev->zero;
+    a.longest_first = k.batch > 1;
+    Launch l;
+    l.stream = (hipStream_t)stream;
+    HIP_TRY(launch_decode(k.head_dim, group, a, l));
+    if (max_splits > 1) HIP_TRY(launch_combine(k.head_dim, group, a, l));
+    return GQA_OK;
 }
 
 int gqa_prefill(gqa_ctx* c, int32_t b, const uint16_t* q, int32_t q_len, int32_t q_pos_base, int32_t kv_len,

@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_status_strings():
     assert _lib.status_string(_lib.GQA_OK) == "ok"
-    for code in (0x01, 0x02, 0x10, 0x11, 0x12, 0x21, 0x22, 0x23, 0x24, 0x25, 0x26, 0x27):
+    for code in (0x01, 0x02, 0x10, 0x11, 0x12, 0x21, 0x22, 0x23, 0x24, 0x25, 0x26, 0x27, 0x28):
         assert _lib.status_string(code) not in ("", "unknown status")
     assert _lib.status_string(0x7F) == "unknown status"
 
