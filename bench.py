@@ -59,15 +59,47 @@ def bench_stream(dev):
     return torch.cuda.Stream(device=dev)
 
 
-def timed_passes(lib, _lib, ctx, stream, step, steps: int, warmup: int) -> dict:
-    """Warm-up, then two passes of `steps` calls of `step` on `stream`.
+_SLEEP_CYCLES_PER_US = None
+MAX_GATE_US = 200_000.0  # longest hold of the gate kernel (a bounded spin)
 
-    The timed pass runs the steps alone between two synchronisations (wall clock) and one pair
-    of events on the stream (device time per step).  The kernel pass repeats them with the
-    library's per-launch HIP events on the same stream (GQA_OPT_PROFILE) and returns each
-    kernel's average launch duration.  Every recorded event pair leaves the GPU idle for
-    several microseconds between launches on this runtime, which is why it stays out of the
-    timed pass.
+
+def sleep_rate(stream) -> float:
+    """Cycles per microsecond of torch.cuda._sleep (a spin kernel of a given cycle count) on this GPU."""
+    global _SLEEP_CYCLES_PER_US
+    if _SLEEP_CYCLES_PER_US is None:
+        import torch
+
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            torch.cuda._sleep(10_000)
+            e0.record(stream)
+            torch.cuda._sleep(4_000_000)
+            e1.record(stream)
+        torch.cuda.synchronize()
+        _SLEEP_CYCLES_PER_US = 4_000_000 / (e0.elapsed_time(e1) * 1e3)
+    return _SLEEP_CYCLES_PER_US
+
+
+MIN_GATED_STEPS = 50  # steps of the gated pass, at least (per-step median and p95)
+
+
+def timed_passes(lib, _lib, ctx, stream, step, steps: int, warmup: int) -> dict:
+    """Warm-up, then a timed pass of `steps` calls of `step` and a gated pass of at least
+    MIN_GATED_STEPS calls, on `stream`.
+
+    Timed pass: the steps alone, back to back, between two synchronisations (wall clock) and one
+    pair of events on the stream (device time per step).
+
+    Gated pass: a spin kernel of bounded length (torch.cuda._sleep) holds the stream while the host
+    queues every step with, through the library's profiling option, a start/stop event pair bound to
+    each kernel launch (hipExtLaunchKernel stamps them with the dispatch's own begin and end).  The
+    host needs several microseconds per timed launch, which left the GPU idle between launches when
+    the steps were queued as they ran; behind the gate the queue is full before the GPU starts, so
+    the launches run back to back as in the timed pass (one event pair around the whole pass checks
+    that).  It gives each kernel's launch durations; a step's kernel time is the sum of its launches'
+    (the steps of a workload all make the same launches).  `gate_held` says whether the gate was
+    still running when the last step had been queued.
     """
     import torch
 
@@ -84,27 +116,62 @@ def timed_passes(lib, _lib, ctx, stream, step, steps: int, warmup: int) -> dict:
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
     gpu_ms = ev0.elapsed_time(ev1) / steps
+
+    n_gated = max(steps, MIN_GATED_STEPS)
     _lib.check(lib.gqa_set_option(ctx, _lib.GQA_OPT_PROFILE, 1), "profile on")
     try:
         t1 = time.perf_counter()
-        for _ in range(steps):
-            step()
+        step()  # host cost of one profiled step
+        host_us = (time.perf_counter() - t1) * 1e6
         torch.cuda.synchronize()
-        profiled_wall_ms = (time.perf_counter() - t1) * 1e3 / steps
+        _lib.check(lib.gqa_set_option(ctx, _lib.GQA_OPT_PROFILE, 1), "profile restart")
+        gate_us = min(MAX_GATE_US, 2.0 * host_us * n_gated + 1000.0)
+        g0 = torch.cuda.Event(enable_timing=True)
+        g1 = torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            torch.cuda._sleep(int(gate_us * sleep_rate(stream)))
+        g0.record(stream)
+        for _ in range(n_gated):
+            step()
+        g1.record(stream)
+        gate_held = not g0.query()
+        torch.cuda.synchronize()
+        gated_gpu_ms = g0.elapsed_time(g1) / n_gated
         times = (ctypes.c_float * _lib.GQA_TIMER_COUNT)()
         counts = (ctypes.c_int32 * _lib.GQA_TIMER_COUNT)()
         _lib.check(lib.gqa_kernel_times(ctx, times, _lib.GQA_TIMER_COUNT), "kernel times")
         _lib.check(lib.gqa_kernel_launch_counts(ctx, counts, _lib.GQA_TIMER_COUNT), "counts")
+        step_us = np.zeros(n_gated)
+        for slot in range(_lib.GQA_TIMER_COUNT):
+            n = int(counts[slot])
+            if n == 0:
+                continue
+            d = (ctypes.c_float * n)()
+            got = ctypes.c_int32()
+            _lib.check(lib.gqa_kernel_durations(ctx, slot, d, n, ctypes.byref(got)), "durations")
+            per = np.frombuffer(d, dtype=np.float32).astype(np.float64)
+            if n % n_gated == 0:
+                step_us += per.reshape(n_gated, n // n_gated).sum(axis=1)
+            else:  # launches do not split evenly over the steps: spread the mean
+                step_us += per.sum() / n_gated
     finally:
         _lib.check(lib.gqa_set_option(ctx, _lib.GQA_OPT_PROFILE, 0), "profile off")
     return {"wall_ms": wall_ms, "gpu_ms": gpu_ms, "times": list(times), "counts": list(counts),
-            "profiled_wall_ms": profiled_wall_ms}
+            "step_us": step_us, "gate_held": bool(gate_held), "gate_us": gate_us, "gated_steps": n_gated,
+            "gated_gpu_ms": gated_gpu_ms}
+
+
+def step_stats(step_us) -> dict:
+    """Median / p95 / mean / min / max of per-step kernel times (us) from the gated pass."""
+    a = np.asarray(step_us, dtype=np.float64)
+    return {"median": float(np.median(a)), "p95": float(np.percentile(a, 95)), "mean": float(a.mean()),
+            "min": float(a.min()), "max": float(a.max()), "n": int(a.size)}
 
 
 class DecodeBench:
     """Owns one libgqa context and HBM-resident inputs for a decode workload."""
 
-    def __init__(self, w, device: int = 0, chunk: int = 0, page_size: int = 0):
+    def __init__(self, w, device: int = 0, chunk: int = 0, page_size: int = 0, merge: int = 0):
         import torch
         from lara_amd import _lib
 
@@ -131,6 +198,7 @@ class DecodeBench:
             _lib.check(self.lib.gqa_create(ctypes.byref(cfg), ctypes.byref(self.ctx)), "gqa_create")
         if chunk:
             _lib.check(self.lib.gqa_set_option(self.ctx, _lib.GQA_OPT_DECODE_CHUNK, chunk), "chunk")
+        _lib.check(self.lib.gqa_set_option(self.ctx, _lib.GQA_OPT_DECODE_MERGE, merge), "merge")
         dev = torch.device("cuda", device)
         self.stream = bench_stream(dev)
         sptr = ctypes.c_void_p(self.stream.cuda_stream)
@@ -173,14 +241,21 @@ class DecodeBench:
     def run(self, steps: int, warmup: int) -> dict:
         _lib = self._lib
         t = timed_passes(self.lib, _lib, self.ctx, self.stream, self.step, steps, warmup)
+        n_dec = max(1, int(t["counts"][_lib.GQA_TIMER_DECODE]))
+        merges_per_step = int(t["counts"][_lib.GQA_TIMER_COMBINE]) / n_dec
+        decode_us = t["times"][_lib.GQA_TIMER_DECODE]
+        combine_us = t["times"][_lib.GQA_TIMER_COMBINE]
         return {
-            "wall_ms_per_step": t["wall_ms"],
-            "gpu_ms_per_step": t["gpu_ms"],
-            "decode_us": t["times"][_lib.GQA_TIMER_DECODE],
-            "decode_launches": int(t["counts"][_lib.GQA_TIMER_DECODE]),
-            "combine_us": t["times"][_lib.GQA_TIMER_COMBINE],
-            "combine_launches": int(t["counts"][_lib.GQA_TIMER_COMBINE]),
-            "profiled_us_per_step": t["profiled_wall_ms"] * 1e3,
+            "wall_us_per_step": t["wall_ms"] * 1e3,
+            "gpu_us_per_step": t["gpu_ms"] * 1e3,
+            "step_us": step_stats(t["step_us"]),
+            "gate_held": t["gate_held"],
+            "gated_gpu_us_per_step": t["gated_gpu_ms"] * 1e3,
+            "decode_us": decode_us,
+            "decode_launches": n_dec,
+            "combine_us": combine_us,
+            "merges_per_step": merges_per_step,
+            "kernels_us_per_step": decode_us + combine_us * merges_per_step,
         }
 
     def run_graph(self, steps: int, warmup: int) -> float:
@@ -215,13 +290,17 @@ PAGED_SUFFIX = "-paged"  # a decode workload over a paged cache (64-row pages un
 PAGE_ROWS = 64
 
 
-def measure(name: str, steps: int, warmup: int, chunk: int = 0, page_rows: int = PAGE_ROWS) -> dict:
-    from lara_amd.benchmark import WORKLOADS, decode_kernel_bytes, decode_step_bytes, HBM_PEAK_GBPS
+DECODE_MERGE = {"fused": 0, "launch": 1}  # GQA_DECODE_MERGE_FUSED / _LAUNCH
+
+
+def measure(name: str, steps: int, warmup: int, chunk: int = 0, page_rows: int = PAGE_ROWS,
+            merge: str = "fused") -> dict:
+    from lara_amd.benchmark import HBM_PEAK_GBPS, WORKLOADS, decode_kernel_bytes, decode_step_bytes
 
     paged = name.endswith(PAGED_SUFFIX)
     w = WORKLOADS[name[: -len(PAGED_SUFFIX)] if paged else name]
     log(f"{name}: filling HBM cache")
-    bench = DecodeBench(w, chunk=chunk, page_size=page_rows if paged else 0)
+    bench = DecodeBench(w, chunk=chunk, page_size=page_rows if paged else 0, merge=DECODE_MERGE[merge])
     try:
         log(f"{name}: warmup {warmup}, timing {steps} steps")
         r = bench.run(steps, warmup)
@@ -229,37 +308,34 @@ def measure(name: str, steps: int, warmup: int, chunk: int = 0, page_rows: int =
             r["graph_us_per_step"] = bench.run_graph(steps, warmup)
     finally:
         bench.close()
-    # The decode kernel's average duration.  A step of one launch is timed by the events that
-    # bracket the timed (back-to-back) steps on the kernel's stream; launches isolated by the
-    # kernel pass's per-launch events run a few percent faster than back-to-back ones, and that
-    # figure is kept as decode_isolated_us.  A step with a merge launch uses the per-launch events.
-    r["decode_isolated_us"] = r["decode_us"]
-    r["decode_launches_per_step"] = 1 + (r["combine_launches"] > 0)
-    if r["combine_launches"] == 0:
-        r["decode_us"] = r["gpu_ms_per_step"] * 1e3
-        r["decode_timing"] = "timed region: events around the back-to-back steps on the kernel's stream"
-        r["decode_launches"] = steps
-    else:
-        r["decode_timing"] = "per-launch events on the kernel's stream (isolated launches)"
     lens = w.lengths()
+    single = r["merges_per_step"] == 0
     step_bytes = decode_step_bytes(w.n_q_heads, w.n_kv_heads, w.head_dim, lens)
-    kern_bytes = decode_kernel_bytes(w.n_q_heads, w.n_kv_heads, w.head_dim, lens)
-    ms = r["wall_ms_per_step"]
+    # The split kernel moves K/V, Q and the appended rows, and writes O itself when no merge follows.
+    kern_bytes = decode_kernel_bytes(w.n_q_heads, w.n_kv_heads, w.head_dim, lens, writes_output=single)
+    us = r["wall_us_per_step"]
     r.update(
         workload=name,
         step_bytes=step_bytes,
         decode_kernel_bytes=kern_bytes,
-        us_per_step=ms * 1e3,
-        step_gbps=step_bytes / (ms * 1e-3) / 1e9,
+        us_per_step=us,
+        step_gbps=step_bytes / (us * 1e-6) / 1e9,
         decode_kernel_gbps=kern_bytes / (r["decode_us"] * 1e-6) / 1e9 if r["decode_us"] > 0 else None,
-        tokens_per_s=w.batch / (ms * 1e-3),
+        kernels_gbps=step_bytes / (r["kernels_us_per_step"] * 1e-6) / 1e9 if r["kernels_us_per_step"] > 0 else None,
+        tokens_per_s=w.batch / (us * 1e-6),
+        kernel_timing="gated pass: launches queued behind a bounded spin kernel and run back to back; "
+                      "event pairs bound to each launch (mean over the steps)",
     )
     r["step_frac_of_peak"] = r["step_gbps"] / HBM_PEAK_GBPS
     if r["decode_kernel_gbps"]:
         r["decode_kernel_frac_of_peak"] = r["decode_kernel_gbps"] / HBM_PEAK_GBPS
-    log(f"{name}: {r['us_per_step']:.1f} us/step, step {r['step_gbps']:.0f} GB/s, decode kernel "
-        f"{r['decode_us']:.1f} us = {r.get('decode_kernel_gbps') or 0:.0f} GB/s"
-        + (f", replayed graph {r['graph_us_per_step']:.1f} us/step" if "graph_us_per_step" in r else ""))
+    log(f"{name}: {us:.1f} us/step (device {r['gpu_us_per_step']:.1f}, gated {r['gated_gpu_us_per_step']:.1f}; "
+        f"kernels median {r['step_us']['median']:.1f}, p95 {r['step_us']['p95']:.1f}), step {r['step_gbps']:.0f} GB/s; "
+        f"decode kernel {r['decode_us']:.1f} us = "
+        f"{r.get('decode_kernel_gbps') or 0:.0f} GB/s"
+        + (f", merge {r['combine_us']:.1f} us" if not single else "")
+        + (f", replayed graph {r['graph_us_per_step']:.1f} us/step" if "graph_us_per_step" in r else "")
+        + ("" if r["gate_held"] else " [gate released before the queue was full]"))
     return r
 
 
@@ -311,11 +387,13 @@ class PrefillBench:
     def run(self, steps: int, warmup: int) -> dict:
         _lib = self._lib
         t = timed_passes(self.lib, _lib, self.ctx, self.stream, self.step, steps, warmup)
-        merges = t["counts"][_lib.GQA_TIMER_COMBINE] / max(1, t["counts"][_lib.GQA_TIMER_PREFILL])
-        return {"wall_ms_per_prompt": t["wall_ms"], "gpu_ms_per_prompt": t["gpu_ms"],
-                "prefill_us_per_launch": t["times"][_lib.GQA_TIMER_PREFILL],
-                "merge_us_per_launch": t["times"][_lib.GQA_TIMER_COMBINE] * merges,
-                "profiled_us_per_prompt": t["profiled_wall_ms"] * 1e3}
+        prompts = t["gated_steps"]
+        return {"wall_us_per_prompt": t["wall_ms"] * 1e3, "gpu_us_per_prompt": t["gpu_ms"] * 1e3,
+                "prompt_us": step_stats(t["step_us"]), "gate_held": t["gate_held"],
+                "gated_gpu_us_per_prompt": t["gated_gpu_ms"] * 1e3,
+                "prefill_us_per_prompt": t["times"][_lib.GQA_TIMER_PREFILL] * t["counts"][_lib.GQA_TIMER_PREFILL] / prompts,
+                "merge_us_per_prompt": t["times"][_lib.GQA_TIMER_COMBINE] * t["counts"][_lib.GQA_TIMER_COMBINE] / prompts,
+                "launches_per_prompt": (t["counts"][_lib.GQA_TIMER_PREFILL] + t["counts"][_lib.GQA_TIMER_COMBINE]) / prompts}
 
     def close(self) -> None:
         self.lib.gqa_destroy(self.ctx)
@@ -335,24 +413,34 @@ def measure_prefill(name: str, steps: int, warmup: int, target_wgs: int = 0) -> 
     sched = prefill_chunk_schedule(w)
     pairs = sum(valid_pairs(ql, kl, causal=w.causal, q_pos_base=qb) for qb, ql, kl in sched)
     flops = prefill_flops(w.n_q_heads, w.head_dim, pairs)
-    kern_us = r["prefill_us_per_launch"] * len(sched)
-    merge_us = r["merge_us_per_launch"] * len(sched)
+    kern_us = r["prefill_us_per_prompt"]
+    merge_us = r["merge_us_per_prompt"]
+    tflops = lambda us: flops / (us * 1e-6) / 1e12 if us > 0 else None  # noqa: E731
     out = {
-        "us_per_prompt": r["wall_ms_per_prompt"] * 1e3,
+        "us_per_prompt": r["wall_us_per_prompt"],
+        "gpu_us_per_prompt": r["gpu_us_per_prompt"],
+        "prompt_us": r["prompt_us"],
+        "gated_gpu_us_per_prompt": r["gated_gpu_us_per_prompt"],
         "prefill_kernel_us_per_prompt": kern_us,
         "segment_merge_us_per_prompt": merge_us,
-        "kernels_tflops_incl_merge": flops / ((kern_us + merge_us) * 1e-6) / 1e12 if kern_us > 0 else None,
+        "launches_per_prompt": r["launches_per_prompt"],
         "chunks": len(sched),
         "flops_per_prompt": flops,
-        "kernel_tflops": flops / (kern_us * 1e-6) / 1e12 if kern_us > 0 else None,
-        "prompt_tflops": flops / (r["wall_ms_per_prompt"] * 1e-3) / 1e12,
-        "kernel_timing": "per-launch events on the kernels' stream (isolated launches)",
-        "tokens_per_s": w.prompt / (r["wall_ms_per_prompt"] * 1e-3),
-        "profiled_us_per_prompt": r["profiled_us_per_prompt"],
+        "kernel_tflops": tflops(kern_us),
+        "kernels_tflops_incl_merge": tflops(kern_us + merge_us),
+        "prompt_tflops": tflops(r["wall_us_per_prompt"]),
+        "kernel_timing": "gated pass: launches queued behind a bounded spin kernel and run back to back; event "
+                         "pairs bound to each launch (sums per prompt)",
+        "gate_held": r["gate_held"],
+        "tokens_per_s": w.prompt / (r["wall_us_per_prompt"] * 1e-6),
     }
     out["mfma_frac_of_bf16_peak"] = out["kernel_tflops"] / BF16_DENSE_TFLOPS if out["kernel_tflops"] else None
-    log(f"{name}: {out['us_per_prompt']:.1f} us/prompt, prefill kernels {kern_us:.1f} us = "
-        f"{out['kernel_tflops'] or 0:.1f} TFLOP/s, segment merges {merge_us:.1f} us")
+    out["mfma_frac_incl_merge"] = (out["kernels_tflops_incl_merge"] / BF16_DENSE_TFLOPS
+                                   if out["kernels_tflops_incl_merge"] else None)
+    log(f"{name}: {out['us_per_prompt']:.1f} us/prompt (device {out['gpu_us_per_prompt']:.1f}, gated "
+        f"{out['gated_gpu_us_per_prompt']:.1f}), prefill kernels "
+        f"{kern_us:.1f} us = {out['kernel_tflops'] or 0:.1f} TFLOP/s, segment merges {merge_us:.1f} us"
+        + ("" if r["gate_held"] else " [gate released before the queue was full]"))
     return out
 
 
@@ -403,30 +491,20 @@ class LayerBench:
     def run(self, steps: int, warmup: int) -> dict:
         _lib = self._lib
         t = timed_passes(self.lib, _lib, self.ctx, self.stream, self.step, steps, warmup)
-        # Stage times: a few more calls with the library's stage events on (profiling on), each
-        # read back after its own synchronisation.
-        _lib.check(self.lib.gqa_set_option(self.ctx, _lib.GQA_OPT_PROFILE, 1), "profile on")
-        stage = np.zeros(3)
-        try:
-            for _ in range(5):
-                self.step()
-                stage_us = (ctypes.c_float * 3)()
-                _lib.check(self.lib.gqa_layer_times(self.ctx, stage_us, 3), "layer times")
-                stage += np.array(stage_us[:]) / 5
-        finally:
-            _lib.check(self.lib.gqa_set_option(self.ctx, _lib.GQA_OPT_PROFILE, 0), "profile off")
-        merges = t["counts"][_lib.GQA_TIMER_COMBINE] / max(1, t["counts"][_lib.GQA_TIMER_PREFILL])
-        return {"wall_ms": t["wall_ms"], "gpu_ms": t["gpu_ms"], "stage_us": stage,
-                "prefill_us": t["times"][_lib.GQA_TIMER_PREFILL],
-                "merge_us": t["times"][_lib.GQA_TIMER_COMBINE] * merges}
+        n = t["gated_steps"]
+        per = lambda slot: t["times"][slot] * t["counts"][slot] / n  # noqa: E731  (us per layer)
+        return {"wall_us": t["wall_ms"] * 1e3, "gpu_us": t["gpu_ms"] * 1e3, "layer_us": step_stats(t["step_us"]),
+                "gate_held": t["gate_held"], "norm_us": per(_lib.GQA_TIMER_NORM),
+                "proj_us": per(_lib.GQA_TIMER_PROJECTION), "rope_us": per(_lib.GQA_TIMER_ROPE),
+                "prefill_us": per(_lib.GQA_TIMER_PREFILL), "merge_us": per(_lib.GQA_TIMER_COMBINE)}
 
     def close(self) -> None:
         self.lib.gqa_destroy(self.ctx)
 
 
 def measure_layer(name: str, steps: int, warmup: int, target_wgs: int = 0) -> dict:
-    from lara_amd.benchmark import BF16_DENSE_TFLOPS, LAYER_WORKLOADS, layer_projection_flops, prefill_flops, \
-        valid_pairs
+    from lara_amd.benchmark import BF16_DENSE_TFLOPS, HBM_PEAK_GBPS, LAYER_WORKLOADS, layer_projection_flops, \
+        prefill_flops, valid_pairs
 
     w = LAYER_WORKLOADS[name]
     log(f"{name}: layer set-up")
@@ -435,26 +513,39 @@ def measure_layer(name: str, steps: int, warmup: int, target_wgs: int = 0) -> di
         r = bench.run(steps, warmup)
     finally:
         bench.close()
-    norm_us, proj_us, rope_us = (float(v) for v in r["stage_us"])
+    norm_us, proj_us, rope_us = r["norm_us"], r["proj_us"], r["rope_us"]
     proj_flops = layer_projection_flops(w)
     attn_flops = prefill_flops(w.n_q_heads, w.head_dim, valid_pairs(w.tokens, w.tokens, causal=w.causal))
     attn_us = r["prefill_us"] + r["merge_us"]
+    # HBM bytes of the two streaming kernels: RMSNorm reads x and writes y (plus gamma); RoPE/scatter
+    # reads the [tokens][Q|K|V] projection and writes Q and the K/V cache rows.
+    norm_bytes = 2 * w.tokens * w.hidden * 2 + w.hidden * 2
+    rope_bytes = 2 * w.tokens * (w.n_q_heads + 2 * w.n_kv_heads) * w.head_dim * 2
+    gbps = lambda b, us: b / (us * 1e-6) / 1e9 if us > 0 else None  # noqa: E731
     out = {
-        "us_per_layer": r["wall_ms"] * 1e3,
+        "us_per_layer": r["wall_us"],
+        "gpu_us_per_layer": r["gpu_us"],
+        "layer_us": r["layer_us"],
         "tokens": w.tokens,
         "rms_norm_us": norm_us,
+        "rms_norm_gbps": gbps(norm_bytes, norm_us),
         "qkv_projection_us": proj_us,
         "qkv_projection_tflops": proj_flops / (proj_us * 1e-6) / 1e12 if proj_us > 0 else None,
         "rope_scatter_us": rope_us,
+        "rope_scatter_gbps": gbps(rope_bytes, rope_us),
         "attention_us": attn_us,
         "attention_tflops": attn_flops / (attn_us * 1e-6) / 1e12 if attn_us > 0 else None,
-        "tokens_per_s": w.tokens / (r["wall_ms"] * 1e-3),
+        "tokens_per_s": w.tokens / (r["wall_us"] * 1e-6),
+        "gate_held": r["gate_held"],
     }
+    for k in ("rms_norm", "rope_scatter"):
+        out[f"{k}_frac_of_hbm_peak"] = out[f"{k}_gbps"] / HBM_PEAK_GBPS if out[f"{k}_gbps"] else None
     out["qkv_projection_frac_of_bf16_peak"] = (out["qkv_projection_tflops"] / BF16_DENSE_TFLOPS
                                                if out["qkv_projection_tflops"] else None)
-    log(f"{name}: {out['us_per_layer']:.1f} us/layer: norm {norm_us:.1f} us, QKV GEMM {proj_us:.1f} us = "
-        f"{out['qkv_projection_tflops'] or 0:.0f} TFLOP/s, RoPE {rope_us:.1f} us, attention {attn_us:.1f} us = "
-        f"{out['attention_tflops'] or 0:.0f} TFLOP/s")
+    log(f"{name}: {out['us_per_layer']:.1f} us/layer: norm {norm_us:.1f} us = {out['rms_norm_gbps'] or 0:.0f} GB/s, "
+        f"QKV GEMM {proj_us:.1f} us = {out['qkv_projection_tflops'] or 0:.0f} TFLOP/s, RoPE {rope_us:.1f} us = "
+        f"{out['rope_scatter_gbps'] or 0:.0f} GB/s, attention {attn_us:.1f} us = {out['attention_tflops'] or 0:.0f} "
+        "TFLOP/s")
     return out
 
 
@@ -493,19 +584,18 @@ def measure_prefill_oneshot(name: str, steps: int, warmup: int) -> dict:
                        "prefill")
 
         r = timed_passes(lib, _lib, ctx, stream, step, steps, warmup)
-        wall_us = r["wall_ms"] * 1e3
-        t = r["times"]
-        merges = r["counts"][_lib.GQA_TIMER_COMBINE]
     finally:
         lib.gqa_destroy(ctx)
-    isolated_us = t[_lib.GQA_TIMER_PREFILL] + t[_lib.GQA_TIMER_COMBINE]
-    # One launch per prompt: its duration is the timed region's event time per step.
-    kern_us = r["gpu_ms"] * 1e3 if merges == 0 else isolated_us
+    t, n = r["times"], r["counts"]
+    kern_us = (t[_lib.GQA_TIMER_PREFILL] * n[_lib.GQA_TIMER_PREFILL] + t[_lib.GQA_TIMER_COMBINE] *
+               n[_lib.GQA_TIMER_COMBINE]) / r["gated_steps"]
     flops = prefill_flops(32, 128, valid_pairs(L, L, causal=True))
-    out = {"tokens": L, "us_per_prompt": wall_us, "kernel_us": kern_us, "isolated_launch_us": isolated_us,
+    out = {"tokens": L, "us_per_prompt": r["wall_ms"] * 1e3, "gpu_us_per_prompt": r["gpu_ms"] * 1e3,
+           "prompt_us": step_stats(r["step_us"]), "kernel_us": kern_us, "gate_held": r["gate_held"],
            "kernel_tflops": flops / (kern_us * 1e-6) / 1e12 if kern_us > 0 else None}
     out["mfma_frac_of_bf16_peak"] = out["kernel_tflops"] / BF16_DENSE_TFLOPS if out["kernel_tflops"] else None
-    log(f"{name}: {wall_us:.1f} us/prompt, kernel {kern_us:.1f} us = {out['kernel_tflops'] or 0:.0f} TFLOP/s")
+    log(f"{name}: {out['us_per_prompt']:.1f} us/prompt, kernels {kern_us:.1f} us = "
+        f"{out['kernel_tflops'] or 0:.0f} TFLOP/s")
     return out
 
 
@@ -520,62 +610,219 @@ def read_traffic():
         return None
 
 
-def cpu_baseline(name: str, budget_s: float, pool_units: int = 16) -> dict:
-    """Time the fp32 NumPy oracle on host cores over whole steps of the workload.
+def read_ceiling(gib: int = 4, launches: int = 10) -> dict:
+    """Measured HBM streaming-read ceiling (gqa_stream_read_device) beside the 8 TB/s specification.
 
-    One step is every (sequence, kv head) unit of the batch, one unit at a time (the
-    reference's CPU model works per KV group, sw/board_performance.py:158-192).  Inputs are
-    seeded bf16 words of each unit's shape, drawn once for a pool of ``pool_units`` units and
-    cycled over the step (the arithmetic does not depend on the values; the pool is larger
-    than the last-level cache, so K/V stream from DRAM as they would).  One warm-up step,
-    then whole steps until ``budget_s`` seconds of timed work (at least one), median per step
-    (the reference's warm-up / repeat / median method, sw/board_performance.py:295-331).
+    A ``gib`` GiB buffer (16x the 256 MB Infinity Cache) is read by the probe kernel with the decode
+    kernel's access pattern (16-byte nontemporal loads, 512-thread work-groups over contiguous
+    shares), for loads in flight per thread x work-groups over a small grid; each configuration runs
+    ``launches`` launches back to back between two events.  The best configuration is the ceiling.
     """
+    import torch
+    from lara_amd import _lib
+    from lara_amd.benchmark import HBM_PEAK_GBPS
+
+    lib = _lib.lib()
+    n = gib << 30
+    buf = torch.empty(n, dtype=torch.uint8, device="cuda")
+    buf.random_(0, 255)
+    sink = torch.zeros(8192, dtype=torch.int32, device="cuda")
+    stream = bench_stream(torch.device("cuda", 0))
+    sptr = ctypes.c_void_p(stream.cuda_stream)
+    torch.cuda.synchronize()
+    results = []
+    for unroll in (1, 2, 4, 8):
+        for wgs in (512, 1024, 2048, 4096):
+            call = lambda: _lib.check(lib.gqa_stream_read_device(  # noqa: E731
+                ctypes.c_void_p(buf.data_ptr()), n, wgs, unroll, ctypes.c_void_p(sink.data_ptr()), sptr), "read probe")
+            call()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(launches):
+                call()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / launches
+            results.append({"unroll": unroll, "work_groups": wgs, "us": us, "gbps": n / (us * 1e-6) / 1e9})
+    del buf
+    best = max(results, key=lambda x: x["gbps"])
+    log(f"read ceiling: {best['gbps']:.0f} GB/s ({best['unroll']} loads in flight per thread, "
+        f"{best['work_groups']} work-groups)")
+    return {"gbps": best["gbps"], "frac_of_spec": best["gbps"] / HBM_PEAK_GBPS, "spec_gbps": HBM_PEAK_GBPS,
+            "bytes": n, "best": best, "sweep": results,
+            "method": f"gqa_stream_read_device over {gib} GiB: 16-byte nontemporal loads, 512-thread work-groups, "
+                      f"{launches} launches back to back between two events per configuration"}
+
+
+def cpu_threads_all() -> int:
+    """Host threads of the all-cores pass: the affinity set, capped by OMP_NUM_THREADS when set."""
+    aff = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    return max(1, min(int(env), aff)) if env.isdigit() and int(env) > 0 else aff
+
+
+def _timed_repeats(fn, budget_s: float, max_repeats: int = 1000):
+    """One warm-up call, then calls until budget_s seconds of timed work (at least one): the
+    reference's warm-up / repeat / median method (sw/board_performance.py:295-331)."""
+    fn()
+    times = []
+    while not times or (sum(times) < budget_s and len(times) < max_repeats):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return times
+
+
+def decode_input_pool(name: str, max_bytes: int = 512 << 20, max_units: int = 16) -> list:
+    """Seeded bf16 words for the CPU decode baseline: (q, k, v) of up to ``max_units`` units of the
+    workload's longest length, at most ``max_bytes`` of K/V in all (at least two units)."""
+    from lara_amd.benchmark import WORKLOADS
+    from oracle.gqa_oracle import fp32_to_bf16_u16
+
+    w = WORKLOADS[name]
+    max_len = int(w.lengths().max())
+    unit_bytes = 2 * max_len * w.head_dim * 2
+    n_units = w.batch * w.n_kv_heads
+    n_pool = max(2, min(max_units, n_units, max_bytes // unit_bytes))
+    rng = np.random.default_rng(w.seed + 1000)
+    draw = lambda shape: fp32_to_bf16_u16(rng.standard_normal(shape, dtype=np.float32) * np.float32(w.amplitude))  # noqa: E731
+    return [(draw((w.group, w.head_dim)), draw((max_len, w.head_dim)), draw((max_len, w.head_dim)))
+            for _ in range(min(n_pool, n_units))]
+
+
+def cpu_decode_baseline(name: str, budget_s: float, threads: int = 1, pool=None) -> dict:
+    """The fp32 NumPy oracle timed on host cores over the workload's decode step.
+
+    A step is every (sequence, kv head) unit of the batch (the reference's CPU model works per KV
+    group, sw/board_performance.py:158-192).  Inputs are seeded bf16 words (decode_input_pool)
+    cycled over the step's units (the arithmetic does not depend on the values; the pool is larger
+    than the last-level cache, so K/V stream from DRAM).  With ``threads`` > 1 the units run on a
+    thread pool (NumPy releases the GIL in its kernels), each with one BLAS thread.  When a whole
+    step would take more than a third of the budget, a sample of units is timed instead and scaled
+    to the step by attended keys (the work of a unit is proportional to its keys).
+    """
+    from concurrent.futures import ThreadPoolExecutor
+
     from threadpoolctl import threadpool_limits
 
     from lara_amd.benchmark import WORKLOADS, decode_step_bytes
-    from oracle.gqa_oracle import decode_fp32_baseline, fp32_to_bf16_u16
+    from oracle.gqa_oracle import decode_fp32_baseline
 
     w = WORKLOADS[name]
     lens = w.lengths()
-    rng = np.random.default_rng(w.seed + 1000)
+    pool = pool if pool is not None else decode_input_pool(name)
+    n_pool = len(pool)
     units = [(b, h) for b in range(w.batch) for h in range(w.n_kv_heads)]
-    n_pool = min(pool_units, len(units))
-    max_len = int(lens.max())
-    pool = []
-    for _ in range(n_pool):
-        q = fp32_to_bf16_u16(rng.standard_normal((w.group, w.head_dim), dtype=np.float32) * w.amplitude)
-        k = fp32_to_bf16_u16(rng.standard_normal((max_len, w.head_dim), dtype=np.float32) * w.amplitude)
-        v = fp32_to_bf16_u16(rng.standard_normal((max_len, w.head_dim), dtype=np.float32) * w.amplitude)
-        pool.append((q, k, v))
+    keys = np.array([int(lens[b]) for b, _ in units], dtype=np.int64)
 
-    def one_step() -> float:
-        t0 = time.perf_counter()
-        for i, (b, _h) in enumerate(units):
-            q, k, v = pool[i % n_pool]
-            L = int(lens[b])
-            decode_fp32_baseline(q, k[:L], v[:L], scale=w.scale)
-        return time.perf_counter() - t0
+    def unit(i: int) -> None:
+        q, k, v = pool[i % n_pool]
+        L = int(keys[i])
+        decode_fp32_baseline(q, k[:L], v[:L], scale=w.scale)
 
-    with threadpool_limits(limits=1):
-        one_step()  # warm-up
-        times = []
-        while not times or (sum(times) < budget_s and len(times) < 1000):
-            times.append(one_step())
-    step_s = float(np.median(times))
+    ex = ThreadPoolExecutor(max_workers=threads) if threads > 1 else None
+
+    def run(sel) -> None:
+        if ex is None:
+            for i in sel:
+                unit(i)
+        else:
+            list(ex.map(unit, sel))
+
+    try:
+        with threadpool_limits(limits=1):
+            probe = list(range(min(len(units), threads)))
+            run(probe)
+            t0 = time.perf_counter()
+            run(probe)
+            est_step = (time.perf_counter() - t0) * keys.sum() / max(1, keys[probe].sum())
+            if est_step <= budget_s / 3:
+                sel = list(range(len(units)))
+            else:
+                n_sel = max(threads, int(len(units) * (budget_s / 3) / est_step))
+                if n_sel > threads:
+                    n_sel -= n_sel % threads
+                sel = list(range(min(len(units), n_sel)))
+            times = _timed_repeats(lambda: run(sel), budget_s)
+    finally:
+        if ex is not None:
+            ex.shutdown()
+    scale = float(keys.sum()) / float(keys[sel].sum())
+    step_s = float(np.median(times)) * scale
     step_bytes = decode_step_bytes(w.n_q_heads, w.n_kv_heads, w.head_dim, lens)
+    whole = len(sel) == len(units)
     return {
         "value": step_bytes / step_s / 1e9,
         "unit": "GB/s",
-        "cores": 1,
+        "cores": threads,
         "kind": "port",
-        "sample": (f"{len(times)} whole steps ({len(units)} (sequence, kv head) units each) after 1 warm-up step, "
-                   f"median; fp32 NumPy oracle (bf16 words in, stable softmax), 1 BLAS thread, seeded inputs "
-                   f"cycled from {n_pool} units' data; {sum(times):.1f} s timed"),
+        "sample": (f"{len(times)} timed repeats of {'whole steps' if whole else f'{len(sel)} of {len(units)} units'} "
+                   f"({len(units)} (sequence, kv head) units per step) after 1 warm-up, median"
+                   + ("" if whole else f", scaled to the step by attended keys (x{scale:.2f})")
+                   + f"; fp32 NumPy oracle (bf16 words in, stable softmax), {threads} thread(s) x 1 BLAS thread, "
+                   f"seeded inputs cycled from {n_pool} units' data; {sum(times):.1f} s timed"),
         "us_per_step": step_s * 1e6,
-        "us_per_step_p95": float(np.percentile(times, 95)) * 1e6,
-        "host_cpu_count": os.cpu_count(),
+        "us_per_step_p95": float(np.percentile(times, 95)) * scale * 1e6,
     }
+
+
+def cpu_prefill_baseline(name: str, budget_s: float, threads: int = 1) -> dict:
+    """The fp32 NumPy oracle timed on host cores over whole chunked prompts of the workload.
+
+    A prompt runs every chunk's transaction (cpu_attention_numpy_fp32: per KV group, causal mask
+    at the chunk's absolute positions, sw/board_performance.py:158-192 generalised) on seeded bf16
+    words; BLAS uses ``threads`` threads.  Rate: causal-valid FLOPs (4 * H_q * pairs * D,
+    sw/board_performance.py:386-388) per second of the median prompt.
+    """
+    from threadpoolctl import threadpool_limits
+
+    from lara_amd.benchmark import PREFILL_WORKLOADS, prefill_chunk_schedule, prefill_flops, valid_pairs
+    from oracle.gqa_oracle import cpu_attention_numpy_fp32, fp32_to_bf16_u16
+
+    w = PREFILL_WORKLOADS[name]
+    rng = np.random.default_rng(w.seed + 1000)
+    q = fp32_to_bf16_u16(rng.standard_normal((w.n_q_heads, w.prompt, w.head_dim), dtype=np.float32))
+    k = fp32_to_bf16_u16(rng.standard_normal((w.n_kv_heads, w.prompt, w.head_dim), dtype=np.float32))
+    v = fp32_to_bf16_u16(rng.standard_normal((w.n_kv_heads, w.prompt, w.head_dim), dtype=np.float32))
+    sched = prefill_chunk_schedule(w)
+
+    def prompt() -> None:
+        for start, q_len, kv_len in sched:
+            cpu_attention_numpy_fp32(q[:, start:start + q_len], k[:, :kv_len], v[:, :kv_len], causal=w.causal,
+                                     q_pos_base=start, kv_pos_base=0)
+
+    with threadpool_limits(limits=threads):
+        times = _timed_repeats(prompt, budget_s)
+    pairs = sum(valid_pairs(ql, kl, causal=w.causal, q_pos_base=qb) for qb, ql, kl in sched)
+    flops = prefill_flops(w.n_q_heads, w.head_dim, pairs)
+    med = float(np.median(times))
+    return {
+        "value": flops / med / 1e12,
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"{len(times)} whole prompts ({len(sched)} chunks each) after 1 warm-up, median; fp32 NumPy "
+                   f"oracle per KV group, {threads} BLAS thread(s); {sum(times):.1f} s timed"),
+        "us_per_prompt": med * 1e6,
+        "us_per_prompt_p95": float(np.percentile(times, 95)) * 1e6,
+    }
+
+
+def cpu_baselines(name: str, budget_s: float, all_budget_s: float) -> dict:
+    """One-thread pass and all-cores pass of the CPU baseline for a decode or prefill workload."""
+    from lara_amd.benchmark import PREFILL_WORKLOADS
+
+    n_all = cpu_threads_all()
+    log(f"{name}: cpu baseline, 1 thread ({budget_s:.0f} s) and {n_all} threads ({all_budget_s:.0f} s)")
+    if name in PREFILL_WORKLOADS:
+        one = cpu_prefill_baseline(name, budget_s, 1)
+        one["all_cores"] = cpu_prefill_baseline(name, all_budget_s, n_all) if n_all > 1 else None
+    else:
+        pool = decode_input_pool(name)
+        one = cpu_decode_baseline(name, budget_s, 1, pool)
+        one["all_cores"] = cpu_decode_baseline(name, all_budget_s, n_all, pool) if n_all > 1 else None
+    return one
 
 
 def copy_calibration(mib: int) -> int:
@@ -765,6 +1012,8 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--workload", default="decode-b64-ctx8192", choices=sorted(WORKLOAD_NAMES))
     parser.add_argument("--chunk", type=int, default=0, help="keys per split-KV work-group (0 = auto)")
+    parser.add_argument("--decode-merge", default="fused", choices=sorted(DECODE_MERGE),
+                        help="split merge of the decode: in the decode launch (fused) or a second launch")
     parser.add_argument("--page-rows", type=int, default=PAGE_ROWS,
                         help="rows per page of the paged-cache workloads (power of two, >= 64)")
     parser.add_argument("--prefill-wgs", type=int, default=0,
@@ -772,7 +1021,11 @@ def main() -> int:
     parser.add_argument("--others", default=",".join(DEFAULT_OTHERS),
                         help="extra workloads to report, comma-separated ('' = none); decode workloads also run "
                              "on a paged cache with the suffix " + PAGED_SUFFIX)
-    parser.add_argument("--cpu-seconds", type=float, default=12.0)
+    parser.add_argument("--cpu-seconds", type=float, default=12.0,
+                        help="CPU baseline budget of the headline workload's one-thread pass")
+    parser.add_argument("--cpu-seconds-other", type=float, default=3.0,
+                        help="CPU baseline budget of every other pass (all-cores, other workloads)")
+    parser.add_argument("--no-read-ceiling", action="store_true", help="skip the streaming-read ceiling probe")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--calibrate-copy-mib", type=int, default=0,
                         help="only run a plain device-to-device copy of this many MiB (5 times) and exit; "
@@ -817,26 +1070,32 @@ def main() -> int:
         return copy_calibration(args.calibrate_copy_mib)
     if args.board_matrix:
         return board_matrix(args)
-    main_r = measure(args.workload, args.steps, args.warmup, args.chunk, args.page_rows)
+    main_r = measure(args.workload, args.steps, args.warmup, args.chunk, args.page_rows, args.decode_merge)
     others = {}
+    decode_keys = ("us_per_step", "gpu_us_per_step", "gated_gpu_us_per_step", "step_us", "step_gbps", "step_frac_of_peak", "decode_us",
+                   "combine_us", "merges_per_step", "kernels_us_per_step", "decode_kernel_bytes",
+                   "decode_kernel_gbps", "decode_kernel_frac_of_peak", "kernels_gbps", "tokens_per_s",
+                   "graph_us_per_step", "gate_held")
     for name in [x for x in args.others.split(",") if x and x != args.workload]:
         if name in PREFILL_WORKLOADS:
             others[name] = measure_prefill(name, max(10, args.steps // 2), max(2, args.warmup // 2), args.prefill_wgs)
-            continue
-        if name in ONESHOT_PREFILL:
+        elif name in ONESHOT_PREFILL:
             others[name] = measure_prefill_oneshot(name, max(5, args.steps // 10), 2)
-            continue
-        if name in LAYER_WORKLOADS:
+        elif name in LAYER_WORKLOADS:
             others[name] = measure_layer(name, max(10, args.steps // 4), max(2, args.warmup // 2), args.prefill_wgs)
-            continue
-        r = measure(name, max(10, args.steps // 2), max(2, args.warmup // 2), page_rows=args.page_rows)
-        others[name] = {k: r[k] for k in ("us_per_step", "profiled_us_per_step", "combine_us", "step_gbps", "step_frac_of_peak", "decode_us",
-                                           "decode_kernel_gbps", "decode_isolated_us", "decode_launches_per_step",
-                                           "tokens_per_s", "graph_us_per_step") if k in r}
+        else:
+            r = measure(name, max(10, args.steps // 2), max(2, args.warmup // 2), page_rows=args.page_rows,
+                        merge=args.decode_merge)
+            others[name] = {k: r[k] for k in decode_keys if k in r}
+    ceiling = None if args.no_read_ceiling else read_ceiling()
     cpu = None
     if not args.no_cpu_baseline:
-        log(f"cpu baseline ({args.cpu_seconds:.0f} s budget)")
-        cpu = cpu_baseline(args.workload, args.cpu_seconds)
+        cpu = cpu_baselines(args.workload, args.cpu_seconds, args.cpu_seconds_other)
+        for name in others:
+            if name in WORKLOADS or name in PREFILL_WORKLOADS:
+                others[name]["cpu_baseline"] = cpu_baselines(name, args.cpu_seconds_other, args.cpu_seconds_other)
+
+    from lara_amd.benchmark import collect_environment
 
     w = WORKLOADS[args.workload]
     achieved = main_r["decode_kernel_gbps"]
@@ -848,11 +1107,16 @@ def main() -> int:
         "unit": "GB/s",
         "frac": achieved / HBM_PEAK_GBPS if achieved else None,
         "traffic": read_traffic() if args.workload == "decode-b64-ctx8192" else None,
+        "traffic_source": (f"{PROFILE_TRAFFIC.relative_to(ROOT)} (rocprofv3 FETCH_SIZE and WRITE_SIZE runs of this "
+                           "kernel, scaled by a plain copy's counters); not measured in this run"
+                           if args.workload == "decode-b64-ctx8192" else None),
         "algorithmic_bytes_per_launch": main_r["decode_kernel_bytes"],
+        "algorithmic_bytes": "K and V rows read + Q read + appended K/V rows written + O written",
         "avg_launch_us": main_r["decode_us"],
         "launches_averaged": main_r["decode_launches"],
-        "timing": main_r["decode_timing"],
-        "isolated_launch_us": main_r["decode_isolated_us"],
+        "timing": main_r["kernel_timing"],
+        "timed_pass_device_us_per_step": main_r["gpu_us_per_step"],
+        "frac_of_measured_read_ceiling": achieved / ceiling["gbps"] if (achieved and ceiling) else None,
     }
     line = {
         "metric": METRIC,
@@ -861,8 +1125,10 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": main_r["wall_ms_per_step"],
+        "ms_per_step": main_r["us_per_step"] * 1e-3,
         "us_per_step": main_r["us_per_step"],
+        "step_us_median": main_r["step_us"]["median"],
+        "step_us_p95": main_r["step_us"]["p95"],
         "frac_of_hbm_peak": main_r["step_frac_of_peak"],
         "tokens_per_s": main_r["tokens_per_s"],
         "higher_is_better": True,
@@ -883,7 +1149,9 @@ def main() -> int:
         },
         "kernels_us": {"decode_step": main_r["decode_us"]},
         "roofline": roofline,
+        "read_ceiling": ceiling,
         "cpu_baseline": cpu,
+        "environment": collect_environment(),
         "other_workloads": others,
     }
     print(json.dumps(line), flush=True)

@@ -57,14 +57,28 @@ extern "C" {
 #define GQA_TIMER_DECODE  1
 #define GQA_TIMER_COMBINE 2 /* log-sum-exp merge launch of split-KV decode or segmented prefill */
 #define GQA_TIMER_PREFILL 3
-#define GQA_TIMER_COUNT   4
+#define GQA_TIMER_NORM    4 /* layer stage: RMSNorm (gqa_layer_qkv_device) */
+#define GQA_TIMER_PROJECTION 5 /* layer stage: the QKV projection's hipBLASLt kernels, between two recorded events */
+#define GQA_TIMER_ROPE    6 /* layer stage: RoPE + scatter */
+#define GQA_TIMER_COUNT   7
 
 /* Tunables for gqa_set_option. */
-#define GQA_OPT_DECODE_CHUNK 1 /* keys per split-KV work-group (multiple of 256; 0 = auto: about 8 waves per CU) */
-#define GQA_OPT_PROFILE      2 /* 1 = time every kernel launch with HIP events (restarts the record);
-                                  each event pair idles the GPU ~10 us between launches */
+#define GQA_OPT_DECODE_CHUNK 1 /* keys per split-KV work-group (a multiple of 64 giving at most max(l_cap / 256,
+                                  the automatic plan's) splits; a last split of <= chunk/4 keys joins the one
+                                  before it; 0 = auto: about 8 waves per CU, whole 16-key rounds per wave) */
+#define GQA_OPT_PROFILE      2 /* 1 = time every kernel launch with a HIP event pair bound to the launch
+                                  (hipExtLaunchKernel; restarts the record).  Binding adds no GPU work
+                                  between launches, but each timed launch costs the host several us,
+                                  so launches run back to back only if queued ahead of the GPU */
 #define GQA_OPT_PREFILL_WGS  3 /* prefill work-groups the KV segmentation aims for (0 = auto: one per CU, 1 = none) */
 #define GQA_OPT_NUMERICS     4 /* GQA_NUMERICS_*: arithmetic of prefill / transactions (decode: EXACT only) */
+#define GQA_OPT_DECODE_MERGE 5 /* GQA_DECODE_MERGE_*: how split-KV decode merges a sequence's splits */
+
+/* Split merge of the decode (GQA_OPT_DECODE_MERGE).  FUSED (default): the last split of a (sequence,
+ * kv head) to finish merges the others' partials inside the decode launch (agent-scope atomics and a
+ * per-unit arrival counter; one launch per step).  LAUNCH: a second, log-sum-exp merge launch. */
+#define GQA_DECODE_MERGE_FUSED  0
+#define GQA_DECODE_MERGE_LAUNCH 1
 
 /* Numerics of the attention kernels (GQA_OPT_NUMERICS).
  * EXACT: fp32 accumulation, exact exp, exact divide -- within 2 bf16 ulp of exact attention.
@@ -267,9 +281,9 @@ int gqa_decode_append_noalloc(const gqa_config* cfg, void* k_cache, void* v_cach
  * [kv_row0, kv_row0 + n_tokens) of sequence b; it
  * allocates its workspace on first use.  gqa_layer_times returns the device time in us of
  * the RMSNorm, projection and RoPE stages (n <= 3; synchronises) of the last gqa_submit_layer
- * call, or of the last gqa_layer_qkv_device call made while GQA_OPT_PROFILE is on (stage events
- * idle the GPU between launches, so device calls record none otherwise);
- * GQA_ERR_NO_TRANSACTION when the last call recorded none. */
+ * call (GQA_ERR_NO_TRANSACTION when there is none); gqa_layer_qkv_device calls made while
+ * GQA_OPT_PROFILE is on record their stages in the GQA_TIMER_NORM / _PROJECTION / _ROPE slots of
+ * gqa_kernel_times instead. */
 int gqa_submit_layer(gqa_ctx* ctx, int32_t b, const uint16_t* x, int32_t n_tokens, int32_t hidden,
                      const uint16_t* wq, const uint16_t* wk, const uint16_t* wv,
                      const uint16_t* rms_weight, float rms_eps, int32_t q_pos_base,
@@ -296,6 +310,17 @@ int gqa_graph_capture_decode_append(gqa_ctx* ctx, const void* q, const void* k_r
 int gqa_graph_launch(gqa_graph* graph, void* stream);
 int gqa_graph_destroy(gqa_graph* graph);
 
+/* ---- measurement -----------------------------------------------------------------
+ * gqa_stream_read_device: no reference counterpart (the board harness reports against its own
+ * measured PL clock, sw/board_performance.py:237-273).  Reads n_bytes (a multiple of 16) of device
+ * memory at src the way the decode kernel streams its cache -- 16-byte nontemporal loads, 1 KiB
+ * per wave instruction, `unroll` (1, 2, 4 or 8) loads in flight per thread, n_wgs work-groups of
+ * 512 threads over contiguous shares -- and writes (almost) nothing (sink: n_wgs words): the
+ * measured HBM read ceiling beside the 8 TB/s specification.  Enqueues on `stream` (NULL = the
+ * legacy default stream) and returns. */
+int gqa_stream_read_device(const void* src, int64_t n_bytes, int32_t n_wgs, int32_t unroll, uint32_t* sink,
+                           void* stream);
+
 /* ---- timing ---------------------------------------------------------------------
  * gqa_last_elapsed_us: elapsed time of the last synchronous call (HIP events on the ctx
  * stream).  With GQA_OPT_PROFILE on, every kernel launch is bracketed by HIP events on
@@ -307,6 +332,10 @@ int gqa_graph_destroy(gqa_graph* graph);
 int gqa_last_elapsed_us(gqa_ctx* ctx, float* out_us);
 int gqa_kernel_times(gqa_ctx* ctx, float* out_us, int32_t n);
 int gqa_kernel_launch_counts(gqa_ctx* ctx, int32_t* out_counts, int32_t n);
+/* gqa_kernel_durations: the duration (us) of each launch recorded in timer slot `slot` since
+ * profiling was (re)started, in launch order, up to n of them (synchronises on them);
+ * *n_out = the number recorded. */
+int gqa_kernel_durations(gqa_ctx* ctx, int32_t slot, float* out_us, int32_t n, int32_t* n_out);
 int gqa_synchronize(gqa_ctx* ctx);
 
 #ifdef __cplusplus

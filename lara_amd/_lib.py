@@ -40,12 +40,18 @@ GQA_TIMER_APPEND = 0
 GQA_TIMER_DECODE = 1
 GQA_TIMER_COMBINE = 2
 GQA_TIMER_PREFILL = 3
-GQA_TIMER_COUNT = 4
+GQA_TIMER_NORM = 4
+GQA_TIMER_PROJECTION = 5
+GQA_TIMER_ROPE = 6
+GQA_TIMER_COUNT = 7
 
 GQA_OPT_DECODE_CHUNK = 1
 GQA_OPT_PROFILE = 2
 GQA_OPT_PREFILL_WGS = 3
 GQA_OPT_NUMERICS = 4
+GQA_OPT_DECODE_MERGE = 5
+GQA_DECODE_MERGE_FUSED = 0
+GQA_DECODE_MERGE_LAUNCH = 1
 GQA_NUMERICS_EXACT = 0
 GQA_NUMERICS_KV260 = 1
 
@@ -124,9 +130,11 @@ _SIGNATURES = {
                                         POINTER(c_void_p)],
     "gqa_graph_launch": [c_void_p, c_void_p],
     "gqa_graph_destroy": [c_void_p],
+    "gqa_stream_read_device": [c_void_p, c_int64, c_int32, c_int32, c_void_p, c_void_p],
     "gqa_last_elapsed_us": [_CTX, _PF],
     "gqa_kernel_times": [_CTX, _PF, c_int32],
     "gqa_kernel_launch_counts": [_CTX, _P32, c_int32],
+    "gqa_kernel_durations": [_CTX, c_int32, _PF, c_int32, _P32],
     "gqa_synchronize": [_CTX],
 }
 

@@ -931,7 +931,7 @@ class AttentionAccelerator:
 
     def layer_stage_us(self) -> tuple[float, float, float]:
         """Device time (us) of the RMSNorm, projection and RoPE stages of the last ``run_layer``
-        call, or of the last ``layer_qkv_device`` call made while profiling is on."""
+        call (``layer_qkv_device`` calls made while profiling is on record in the kernel timers)."""
         self._ensure_open()
         out = (ctypes.c_float * 3)()
         self._call("gqa_layer_times", out, 3)

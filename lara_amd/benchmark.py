@@ -11,8 +11,9 @@ Algorithmic work (nothing that only exists because of the implementation is coun
 * decode step bytes = sum_b 2*H_kv*L_b*D*2 (K and V rows read)
                       + B*H_q*D*2 (Q read) + B*H_q*D*2 (O written)
                       + B*2*H_kv*D*2 (appended K and V rows written)
-* decode kernel bytes (the split-KV kernel alone) = K/V rows read + Q read
-  = 512 B per (kv head, attended key) at D = 128, plus Q.
+* decode kernel bytes (the split-KV kernel with the append fused into it) = K/V rows read + Q read
+  + appended rows written (+ O written when no merge launch follows, i.e. the step bytes)
+  = 512 B per (kv head, attended key) at D = 128, plus the per-sequence rows.
 * FLOPs = 4*sum_b H_q*L_b*D (QK^T and PV multiply-adds);
   prefill counts causal-valid (query, key) pairs only, ops = 2*(2*H_q*pairs*D)
   (sw/board_performance.py:386-388).
@@ -137,20 +138,21 @@ PREFILL_WORKLOADS = {
 # work model
 # ---------------------------------------------------------------------------------------
 
-def decode_kernel_bytes(n_q_heads: int, n_kv_heads: int, head_dim: int, lengths) -> int:
-    """Bytes the split-KV decode kernel must move: K/V rows + Q."""
+def decode_kernel_bytes(n_q_heads: int, n_kv_heads: int, head_dim: int, lengths, *, writes_output: bool = True) -> int:
+    """Bytes the split-KV decode kernel moves with the append fused into it: K/V rows read, Q read,
+    the appended K/V rows written, and O written when no merge launch follows (writes_output)."""
     lengths = np.asarray(lengths, dtype=np.int64)
+    B = len(lengths)
     kv = int(lengths.sum()) * 2 * n_kv_heads * head_dim * 2
-    q = len(lengths) * n_q_heads * head_dim * 2
-    return kv + q
+    q = B * n_q_heads * head_dim * 2
+    append = B * 2 * n_kv_heads * head_dim * 2
+    o = B * n_q_heads * head_dim * 2 if writes_output else 0
+    return kv + q + append + o
 
 
 def decode_step_bytes(n_q_heads: int, n_kv_heads: int, head_dim: int, lengths) -> int:
     """Bytes of one decode step: K/V read, Q read, O written, appended rows written."""
-    B = len(lengths)
-    return (decode_kernel_bytes(n_q_heads, n_kv_heads, head_dim, lengths)
-            + B * n_q_heads * head_dim * 2
-            + B * 2 * n_kv_heads * head_dim * 2)
+    return decode_kernel_bytes(n_q_heads, n_kv_heads, head_dim, lengths, writes_output=True)
 
 
 def decode_flops(n_q_heads: int, head_dim: int, lengths) -> int:

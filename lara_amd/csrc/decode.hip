@@ -182,6 +182,66 @@ __device__ int rank_to_sequence(const DecodeArgs& a, int rank) {
     return rank;
 }
 
+// Log-sum-exp merge of the split partials of one (sequence, kv head) for query head g of the group
+// and dim d: the (m, l) pairs and dim d of the partial O of kCombineBatch splits are loaded together
+// and folded into a running (M, O, l) with one rescale per batch, so a sequence pays one memory
+// round trip per batch of splits.  COHERENT: agent-scope atomic loads (the partials were written by
+// other work-groups of the same launch); the merge inside the split kernel runs on its critical
+// path, so it takes twice the batch.
+template <bool COHERENT>
+constexpr int combine_batch() {
+    return COHERENT ? 32 : 16;
+}
+
+template <bool COHERENT>
+__device__ __forceinline__ float load_partial(const float* p) {
+    if constexpr (COHERENT) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return *p;
+}
+
+template <int D, int G, bool COHERENT>
+__device__ __forceinline__ void merge_splits(const DecodeArgs& a, int unit, int b, int h, int g, int d, int n_splits) {
+    const size_t base = (size_t)unit * a.max_splits * G + g;  // partial index of split 0
+    const float* ml = a.part_ml + base * 2;
+    const float* po = a.part_o + base * D + d;
+    const size_t stride = (size_t)G;  // partial rows between consecutive splits
+    float M = -INFINITY, O = 0.f, Ls = 0.f;
+    constexpr int kCombineBatch = combine_batch<COHERENT>();
+    for (int s0 = 0; s0 < n_splits; s0 += kCombineBatch) {
+        float em[kCombineBatch], el[kCombineBatch], v[kCombineBatch];
+#pragma unroll
+        for (int j = 0; j < kCombineBatch; ++j) {
+            if (s0 + j < n_splits) {
+                const size_t r = (size_t)(s0 + j) * stride;
+                em[j] = load_partial<COHERENT>(ml + r * 2);
+                el[j] = load_partial<COHERENT>(ml + r * 2 + 1);
+                v[j] = load_partial<COHERENT>(po + r * D);
+            } else {
+                em[j] = -INFINITY;
+                el[j] = 0.f;
+                v[j] = 0.f;
+            }
+        }
+        float bm = M;
+#pragma unroll
+        for (int j = 0; j < kCombineBatch; ++j) bm = fmaxf(bm, em[j]);
+        if (bm == -INFINITY) continue;  // no valid key in the splits so far
+        const float corr = fast_exp2(M - bm);  // 0 while M = -inf
+        O *= corr;
+        Ls *= corr;
+#pragma unroll
+        for (int j = 0; j < kCombineBatch; ++j) {
+            const float w = fast_exp2(em[j] - bm);  // 0 for a split past n_splits
+            O = fmaf(w, v[j], O);
+            Ls = fmaf(w, el[j], Ls);
+        }
+        M = bm;
+    }
+    const size_t row = (size_t)b * a.n_kv_heads * G + h * G + g;
+    a.out[row * D + d] = f32_to_bf16_rne(Ls > 0.f ? O / Ls : 0.f);
+    if (d == 0 && a.lse != nullptr) a.lse[row] = Ls > 0.f ? (M + log2f(Ls)) * kLn2 : -INFINITY;
+}
+
 template <int D, int G, int NW, bool PAGED>
 __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
     constexpr int NCH = D / 8;               // 16-byte words per K/V row
@@ -204,10 +264,10 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
     const int unit = b * a.n_kv_heads + h;
     const int H_q = a.n_kv_heads * G;
     const int L = clamp_len(a.lens[b], a.l_max);
-    const int n_splits = L > 0 ? (L + a.chunk - 1) / a.chunk : 1;
+    const int n_splits = decode_split_count(L, a.chunk);
     if (split >= n_splits) return;  // uniform across the work-group
     const int k_begin = split * a.chunk;
-    const int k_end = min(L, k_begin + a.chunk);
+    const int k_end = split == n_splits - 1 ? L : k_begin + a.chunk;
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -465,6 +525,7 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
     __syncthreads();
 
     const bool single = (n_splits == 1);
+    const bool fused_merge = !single && a.arrivals != nullptr;
     for (int idx = threadIdx.x; idx < G * D; idx += NW * 64) {
         const int g = idx / D;
         const int d = idx - g * D;
@@ -486,68 +547,53 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
             if (d == 0 && a.lse != nullptr) a.lse[row] = Ls > 0.f ? (M + log2f(Ls)) * kLn2 : -INFINITY;
         } else {
             const size_t pidx = ((size_t)unit * a.max_splits + split) * G + g;
-            a.part_o[pidx * D + d] = O;
-            if (d == 0) {
-                a.part_ml[pidx * 2] = M;
-                a.part_ml[pidx * 2 + 1] = Ls;
+            if (fused_merge) {
+                // Agent-scope atomic stores: coherent across the XCDs without an L2 write-back.
+                __hip_atomic_store(&a.part_o[pidx * D + d], O, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (d == 0) {
+                    __hip_atomic_store(&a.part_ml[pidx * 2], M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(&a.part_ml[pidx * 2 + 1], Ls, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            } else {
+                a.part_o[pidx * D + d] = O;
+                if (d == 0) {
+                    a.part_ml[pidx * 2] = M;
+                    a.part_ml[pidx * 2 + 1] = Ls;
+                }
             }
         }
     }
+    if (!fused_merge) return;
+    // The last split of this (sequence, kv head) to arrive merges every split's partial.  Every
+    // thread's partial stores happen before thread 0's release increment (work-group barrier); the
+    // increment that reads n_splits - 1 acquires all of them (release sequence of the counter).
+    // That split resets the counter for the next launch.
+    __shared__ int is_last;
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partial stores are complete
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int prev = __hip_atomic_fetch_add(&a.arrivals[unit], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        is_last = prev == n_splits - 1;
+        if (is_last) {
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // the other splits' partials
+            __hip_atomic_store(&a.arrivals[unit], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    __syncthreads();
+    if (!is_last) return;
+    for (int idx = threadIdx.x; idx < G * D; idx += NW * 64)
+        merge_splits<D, G, true>(a, unit, b, h, idx / D, idx % D, n_splits);
 }
-
-// Log-sum-exp merge of the split partials: one work-group per (sequence, kv head, query
-// head of the group), one thread per dim.  Each thread loads the (m, l) pairs (the same address
-// across the work-group) and its dim of the partial O of kCombineBatch splits together and
-// folds them into a running (M, O, l) with one rescale per batch, so a sequence pays one memory
-// round trip per batch of splits; no LDS and no barrier.
-constexpr int kCombineBatch = 8;
 
 template <int D, int G>
 __global__ __launch_bounds__(D) void decode_combine_kernel(DecodeArgs a) {
     const int unit = blockIdx.x;
-    const int g = blockIdx.y;
     const int b = unit / a.n_kv_heads;
     const int h = unit - b * a.n_kv_heads;
     const int L = clamp_len(a.lens[b], a.l_max);
-    const int n_splits = L > 0 ? (L + a.chunk - 1) / a.chunk : 1;
+    const int n_splits = decode_split_count(L, a.chunk);
     if (n_splits <= 1) return;  // written directly by the split kernel
-    const int d = threadIdx.x;
-    const size_t base = (size_t)unit * a.max_splits * G + g;  // partial index of split 0
-    const float2* ml = reinterpret_cast<const float2*>(a.part_ml) + base;
-    const float* po = a.part_o + base * D + d;
-    const size_t stride = (size_t)G;  // partial rows between consecutive splits
-    float M = -INFINITY, O = 0.f, Ls = 0.f;
-    for (int s0 = 0; s0 < n_splits; s0 += kCombineBatch) {
-        float2 e[kCombineBatch];
-        float v[kCombineBatch];
-#pragma unroll
-        for (int j = 0; j < kCombineBatch; ++j) {
-            if (s0 + j < n_splits) {
-                e[j] = ml[(size_t)(s0 + j) * stride];
-                v[j] = po[(size_t)(s0 + j) * stride * D];
-            } else {
-                e[j] = make_float2(-INFINITY, 0.f);
-                v[j] = 0.f;
-            }
-        }
-        float bm = M;
-#pragma unroll
-        for (int j = 0; j < kCombineBatch; ++j) bm = fmaxf(bm, e[j].x);
-        if (bm == -INFINITY) continue;  // no valid key in the splits so far
-        const float corr = fast_exp2(M - bm);  // 0 while M = -inf
-        O *= corr;
-        Ls *= corr;
-#pragma unroll
-        for (int j = 0; j < kCombineBatch; ++j) {
-            const float w = fast_exp2(e[j].x - bm);  // 0 for a split past n_splits
-            O = fmaf(w, v[j], O);
-            Ls = fmaf(w, e[j].y, Ls);
-        }
-        M = bm;
-    }
-    const size_t row = (size_t)b * a.n_kv_heads * G + h * G + g;
-    a.out[row * D + d] = f32_to_bf16_rne(Ls > 0.f ? O / Ls : 0.f);
-    if (d == 0 && a.lse != nullptr) a.lse[row] = Ls > 0.f ? (M + log2f(Ls)) * kLn2 : -INFINITY;
+    merge_splits<D, G, false>(a, unit, b, h, blockIdx.y, threadIdx.x, n_splits);
 }
 
 // Waves per split work-group.  Up to G = 8 a wave fits in 256 registers, so 8-wave
@@ -574,6 +620,11 @@ hipError_t launch_combine_t(const DecodeArgs& a, const Launch& l) {
 }
 
 }  // namespace
+
+int decode_round_keys(int group) {
+    const int qkg = 64 / group;  // keys per head in the QK layout (RK of decode_split_kernel)
+    return qkg > 16 ? qkg : 16;
+}
 
 int decode_waves(int group) {
     return group <= 4 ? decode_waves_t<4>() : group <= 8 ? decode_waves_t<8>() : decode_waves_t<16>();

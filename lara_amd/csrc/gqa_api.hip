@@ -18,7 +18,8 @@ using namespace lara;
 
 namespace {
 
-constexpr int kMinChunk = 256;     // smallest split (keys); multiple of every decode round size
+constexpr int kChunkOptionQuantum = 64;  // GQA_OPT_DECODE_CHUNK: a multiple of every decode round size
+constexpr int kMinSplitCap = 256;        // the split workspace holds at least l_cap / this splits
 constexpr int kMaxPrefillSegs = 16;
 constexpr int32_t kMaxRows = 1 << 30;  // max_seq_len / max_q_len limit: row counts rounded up stay in int32
 constexpr int kDecodeWavesPerCu = 8;  // split planner target; one split per (sequence, kv head) once that fills the GPU
@@ -61,6 +62,8 @@ struct gqa_ctx {
     uint16_t* v_cache = nullptr;
     float* part_o = nullptr;
     float* part_ml = nullptr;
+    int32_t* arrivals = nullptr;  // [B*H_kv] split arrival counters of the fused merge (zero between launches)
+    int decode_merge = GQA_DECODE_MERGE_FUSED;
     float* pre_ws = nullptr;     // prefill KV-segment partials (O, then (m, l))
     uint16_t* zero_row = nullptr;  // one zero K/V row: the prefill source of rows past kv_len
     size_t pre_ws_floats = 0;
@@ -160,17 +163,26 @@ hipStream_t pick_stream(gqa_ctx* c, void* s) { return s ? (hipStream_t)s : c->st
 // must be 16-byte aligned; nullptr passes (optional operands are checked for presence apart).
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-// Keys per split for max_len attended keys: about kDecodeWavesPerCu waves per CU over the batch's
-// units, each split a multiple of kMinChunk.
-int plan_chunk(int batch, int n_kv_heads, int group, int n_cu, int max_len) {
+// Splits per (sequence, kv head) the automatic plan aims for: about kDecodeWavesPerCu waves per CU
+// over the batch's units.
+int plan_splits(int batch, int n_kv_heads, int group, int n_cu) {
     const int units = batch * n_kv_heads;
     const int target_wgs = kDecodeWavesPerCu * n_cu / decode_waves(group);
-    int splits = (target_wgs + units - 1) / units;
-    if (splits < 1) splits = 1;
-    int chunk = (max_len + splits - 1) / splits;
-    chunk = ((chunk + kMinChunk - 1) / kMinChunk) * kMinChunk;
-    if (chunk < kMinChunk) chunk = kMinChunk;
-    return chunk;
+    const int splits = (target_wgs + units - 1) / units;
+    return splits < 1 ? 1 : splits;
+}
+
+// Keys per split for max_len attended keys: max_len over plan_splits, in whole rounds of every wave
+// of a work-group (128 keys at D 128, group 4) so the waves of a split share its keys evenly --
+// rounded down when that still gives at most plan_splits splits (a short tail joins the last split),
+// else up.  decode_split_count(max_len, chunk) <= plan_splits either way.
+int plan_chunk(int batch, int n_kv_heads, int group, int n_cu, int max_len) {
+    const int quantum = decode_waves(group) * decode_round_keys(group);
+    const int splits = plan_splits(batch, n_kv_heads, group, n_cu);
+    const int even = (max_len + splits - 1) / splits;
+    const int down = std::max(quantum, even / quantum * quantum);
+    if (decode_split_count(max_len, down) <= splits) return down;
+    return (even + quantum - 1) / quantum * quantum;
 }
 
 int choose_chunk(const gqa_ctx* c, int max_len) {
@@ -215,7 +227,7 @@ int run_decode(gqa_ctx* c, const void* q, const int32_t* lens, const void* k_new
                const int32_t* positions, void* o, float* lse, hipStream_t s, int max_len) {
     if (!decode_supported(c->cfg.head_dim, c->group) || c->numerics != GQA_NUMERICS_EXACT) return GQA_ERR_UNSUPPORTED;
     const int chunk = choose_chunk(c, max_len);
-    int max_splits = max_len > 0 ? (max_len + chunk - 1) / chunk : 1;
+    const int max_splits = decode_split_count(max_len, chunk);
     if (max_splits > c->max_splits_cap) return GQA_ERR_RANGE;
     DecodeArgs a{};
     a.q = (const uint16_t*)q;
@@ -241,8 +253,10 @@ int run_decode(gqa_ctx* c, const void* q, const int32_t* lens, const void* k_new
     a.max_pages = c->max_pages;
     a.zero_row = c->zero_row;
     a.longest_first = c->cfg.batch > 1;
+    a.arrivals = c->decode_merge == GQA_DECODE_MERGE_FUSED ? c->arrivals : nullptr;
     HIP_TRY(launch_decode(c->cfg.head_dim, c->group, a, timed(c, GQA_TIMER_DECODE, s)));
-    if (max_splits > 1) HIP_TRY(launch_combine(c->cfg.head_dim, c->group, a, timed(c, GQA_TIMER_COMBINE, s)));
+    if (max_splits > 1 && a.arrivals == nullptr)
+        HIP_TRY(launch_combine(c->cfg.head_dim, c->group, a, timed(c, GQA_TIMER_COMBINE, s)));
     return GQA_OK;
 }
 
@@ -488,7 +502,7 @@ int tune_projection(gqa_ctx* c, ProjectionPlan* p, Gemm&& gemm, hipStream_t s) {
 // row0.. of sequence b.
 int run_layer_qkv(gqa_ctx* c, int32_t b, const void* x, int32_t n_tokens, int32_t hidden, const void* wq,
                   const void* wk, const void* wv, const void* gamma, float eps, int32_t q_pos_base,
-                  int32_t kv_pos_base, int32_t row0, int32_t rope, void* q_out, hipStream_t s, bool timed) {
+                  int32_t kv_pos_base, int32_t row0, int32_t rope, void* q_out, hipStream_t s, bool stage_events) {
     const int D = c->cfg.head_dim, nq = c->cfg.n_q_heads * D, nkv = c->cfg.n_kv_heads * D;
     const int ld = nq + 2 * nkv;
     const size_t y_bytes = gamma ? ((size_t)n_tokens * hidden * 2 + 255) / 256 * 256 : 0;
@@ -502,10 +516,14 @@ int run_layer_qkv(gqa_ctx* c, int32_t b, const void* x, int32_t n_tokens, int32_
             return GQA_ERR_HIP;
         }
     }
-    if (timed && !c->ev_layer[0])
+    if (stage_events && !c->ev_layer[0])
         for (int i = 0; i < 4; ++i) HIP_TRY(hipEventCreate(&c->ev_layer[i]));
     c->layer_timed = false;
-    auto mark = [&](int i) { return timed ? hipEventRecord(c->ev_layer[i], s) : hipSuccess; };
+    auto mark = [&](int i) { return stage_events ? hipEventRecord(c->ev_layer[i], s) : hipSuccess; };
+    // While profiling (device calls), the projection's hipBLASLt kernels are bracketed by the next
+    // event pair of its timer slot; RMSNorm and RoPE have event pairs bound to their launches.
+    const Launch proj_events = stage_events ? Launch{s} : timed(c, GQA_TIMER_PROJECTION, s);
+    if (proj_events.start) HIP_TRY(hipEventRecord(proj_events.start, s));
     HIP_TRY(mark(0));
     const uint16_t* src = (const uint16_t*)x;
     if (gamma) {
@@ -516,7 +534,7 @@ int run_layer_qkv(gqa_ctx* c, int32_t b, const void* x, int32_t n_tokens, int32_
         na.n_tokens = n_tokens;
         na.hidden = hidden;
         na.eps = eps;
-        HIP_TRY(launch_rms_norm(na, Launch{s}));
+        HIP_TRY(launch_rms_norm(na, stage_events ? Launch{s} : timed(c, GQA_TIMER_NORM, s)));
         src = na.y;
     }
     HIP_TRY(mark(1));
@@ -555,6 +573,7 @@ int run_layer_qkv(gqa_ctx* c, int32_t b, const void* x, int32_t n_tokens, int32_
             return GQA_ERR_HIP;
         }
     }
+    if (proj_events.stop) HIP_TRY(hipEventRecord(proj_events.stop, s));
     HIP_TRY(mark(2));
     RopeArgs ra{};
     ra.qkv = qkv;
@@ -575,9 +594,9 @@ int run_layer_qkv(gqa_ctx* c, int32_t b, const void* x, int32_t n_tokens, int32_
     ra.l_cap = c->l_cap;
     ra.row0 = row0;
     for (int p = 0; p < D / 2; ++p) ra.theta[p] = (float)pow(kRopeBase, -2.0 * p / D);
-    HIP_TRY(launch_rope_scatter(ra, Launch{s}));
+    HIP_TRY(launch_rope_scatter(ra, stage_events ? Launch{s} : timed(c, GQA_TIMER_ROPE, s)));
     HIP_TRY(mark(3));
-    c->layer_timed = timed;
+    c->layer_timed = stage_events;
     return GQA_OK;
 }
 
@@ -628,7 +647,9 @@ int create_ctx(const gqa_config* cfg, int32_t page_size, int32_t n_pages, gqa_ct
     c->cfg = k;
     c->group = group;
     c->l_cap = ((k.max_seq_len + 63) / 64) * 64;
-    c->max_splits_cap = (c->l_cap + kMinChunk - 1) / kMinChunk;
+    c->max_splits_cap = std::max((c->l_cap + kMinSplitCap - 1) / kMinSplitCap,
+                                 plan_splits(k.batch, k.n_kv_heads, group, prop.multiProcessorCount > 0
+                                                                             ? prop.multiProcessorCount : 256));
     c->scale = k.scale > 0.f ? k.scale : (float)(1.0 / sqrt((double)k.head_dim));
     c->cfg.scale = c->scale;
     c->clock_mhz = prop.clockRate / 1000.0;
@@ -655,6 +676,7 @@ int create_ctx(const gqa_config* cfg, int32_t page_size, int32_t n_pages, gqa_ct
     alloc((void**)&c->v_cache, kv_words(c) * 2);
     alloc((void**)&c->part_o, units * c->max_splits_cap * group * D * sizeof(float));
     alloc((void**)&c->part_ml, units * c->max_splits_cap * group * 2 * sizeof(float));
+    alloc((void**)&c->arrivals, units * sizeof(int32_t));
     if (prefill_supported(k.head_dim, group)) {
         c->pre_ws_floats = prefill_workspace_need(c, c->n_cu);
         if (c->pre_ws_floats > 0) alloc((void**)&c->pre_ws, c->pre_ws_floats * sizeof(float));
@@ -680,6 +702,7 @@ int create_ctx(const gqa_config* cfg, int32_t page_size, int32_t n_pages, gqa_ct
     }
     // Zero the caches once so rows beyond every sequence's length hold finite words.
     if (rc == GQA_OK && (hipMemsetAsync(c->zero_row, 0, D * 2, c->stream) != hipSuccess ||
+                         hipMemsetAsync(c->arrivals, 0, units * sizeof(int32_t), c->stream) != hipSuccess ||
                          hipMemsetAsync(c->k_cache, 0, kv_words(c) * 2, c->stream) != hipSuccess ||
                          hipMemsetAsync(c->v_cache, 0, kv_words(c) * 2, c->stream) != hipSuccess ||
                          (c->paged && hipMemsetAsync(c->table_dev, 0xFF, (size_t)k.batch * c->max_pages * 4,
@@ -736,20 +759,24 @@ int copy_rows_paged(gqa_ctx* c, int b, int start, int n, const uint16_t* k_src, 
 
 // ---- decode without allocation (gqa_decode_append_noalloc) ---------------------------------
 // Split-KV partials of gqa_decode_append_noalloc: one copy per device, held until the process
-// ends.  Its last kNoAllocZeroBytes are the zero K/V row (the source of rows past a sequence's
-// length), cleared at set-up and never written afterwards.  Host code uses the per-device address
-// from hipGetSymbolAddress, never this name.
+// ends.  Its tail holds the split arrival counters of the fused merge (kNoAllocCounters, zero
+// between launches: the last split to arrive resets its counter) and, last, the zero K/V row (the
+// source of rows past a sequence's length, never written); both are cleared at set-up.  Host code
+// uses the per-device address from hipGetSymbolAddress, never this name.
 static __device__ __align__(256) uint8_t scratch[GQA_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
 constexpr int kNoAllocDevices = 64;
 constexpr size_t kNoAllocZeroBytes = 256;  // one K/V row of D <= 128 bf16 words
-constexpr size_t kNoAllocPartialBytes = GQA_NOALLOC_SCRATCH_BYTES - kNoAllocZeroBytes;
+constexpr int kNoAllocCounters = 1024;     // (sequence, kv head) units the fused merge can count
+constexpr size_t kNoAllocTailBytes = kNoAllocCounters * sizeof(int32_t) + kNoAllocZeroBytes;
+constexpr size_t kNoAllocPartialBytes = GQA_NOALLOC_SCRATCH_BYTES - kNoAllocTailBytes;
 
 struct NoAllocDevice {
     bool ready = false;
     uint8_t* scratch = nullptr;      // device address of `scratch` on this device
+    int32_t* arrivals = nullptr;     // its split arrival counters
     const uint16_t* zero = nullptr;  // its zero row
     int n_cu = 0;
 };
@@ -773,10 +800,11 @@ int noalloc_setup(int device, hipStream_t stream, NoAllocDevice** out) {
         void* p = nullptr;
         HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
         uint8_t* base = static_cast<uint8_t*>(p);
-        HIP_TRY(hipMemset(base + kNoAllocPartialBytes, 0, kNoAllocZeroBytes));
+        HIP_TRY(hipMemset(base + kNoAllocPartialBytes, 0, kNoAllocTailBytes));
         HIP_TRY(hipDeviceSynchronize());
         d.scratch = base;
-        d.zero = reinterpret_cast<const uint16_t*>(base + kNoAllocPartialBytes);
+        d.arrivals = reinterpret_cast<int32_t*>(base + kNoAllocPartialBytes);
+        d.zero = reinterpret_cast<const uint16_t*>(base + kNoAllocPartialBytes + kNoAllocCounters * sizeof(int32_t));
         d.n_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
         d.ready = true;
     }
@@ -835,6 +863,7 @@ int gqa_destroy(gqa_ctx* c) {
     (void)hipFree(c->v_cache);
     (void)hipFree(c->part_o);
     (void)hipFree(c->part_ml);
+    (void)hipFree(c->arrivals);
     (void)hipFree(c->pre_ws);
     (void)hipFree(c->zero_row);
     (void)hipFree(c->q_dev);
@@ -878,12 +907,17 @@ int gqa_set_option(gqa_ctx* c, int32_t option, int64_t value) {
     if (!c) return GQA_ERR_NULL;
     switch (option) {
         case GQA_OPT_DECODE_CHUNK:
-            if (value < 0 || (value > 0 && (value % kMinChunk != 0 || value > c->l_cap + kMinChunk)))
+            if (value < 0 || (value > 0 && (value % kChunkOptionQuantum != 0 || value > c->l_cap + kChunkOptionQuantum ||
+                                            decode_split_count(c->cfg.max_seq_len, (int)value) > c->max_splits_cap)))
                 return GQA_ERR_RANGE;
             c->chunk_opt = (int)value;
             return GQA_OK;
         case GQA_OPT_PROFILE:
             return profile_enable(c, value ? 1 : 0);
+        case GQA_OPT_DECODE_MERGE:
+            if (value != GQA_DECODE_MERGE_FUSED && value != GQA_DECODE_MERGE_LAUNCH) return GQA_ERR_RANGE;
+            c->decode_merge = (int)value;
+            return GQA_OK;
         case GQA_OPT_NUMERICS:
             if (value != GQA_NUMERICS_EXACT && value != GQA_NUMERICS_KV260) return GQA_ERR_RANGE;
             if (value == GQA_NUMERICS_KV260 && ((c->cfg.head_dim != 64 && c->cfg.head_dim != 128) || c->paged))
@@ -1207,7 +1241,7 @@ int gqa_decode_append_noalloc(const gqa_config* cfg, void* k_cache, void* v_cach
     // The plan gqa_decode_append_device makes for the same configuration (keys per split from the
     // CU count and max_seq_len), so both entry points give the same words.
     const int chunk = plan_chunk(k.batch, k.n_kv_heads, group, dev->n_cu, k.max_seq_len);
-    const int max_splits = (k.max_seq_len + chunk - 1) / chunk;
+    const int max_splits = decode_split_count(k.max_seq_len, chunk);
     const size_t rows = (size_t)k.batch * k.n_kv_heads * max_splits * group;  // partial rows of the plan
     const size_t o_bytes = max_splits > 1 ? (rows * k.head_dim * sizeof(float) + 255) / 256 * 256 : 0;
     const size_t ml_bytes = max_splits > 1 ? rows * 2 * sizeof(float) : 0;
@@ -1234,10 +1268,12 @@ int gqa_decode_append_noalloc(const gqa_config* cfg, void* k_cache, void* v_cach
     a.lse = lse;
     a.zero_row = dev->zero;
     a.longest_first = k.batch > 1;
+    // The same merge as the context entry point's default: fused when the counters cover the units.
+    a.arrivals = (size_t)k.batch * k.n_kv_heads <= (size_t)kNoAllocCounters ? dev->arrivals : nullptr;
     Launch l;
     l.stream = (hipStream_t)stream;
     HIP_TRY(launch_decode(k.head_dim, group, a, l));
-    if (max_splits > 1) HIP_TRY(launch_combine(k.head_dim, group, a, l));
+    if (max_splits > 1 && a.arrivals == nullptr) HIP_TRY(launch_combine(k.head_dim, group, a, l));
     return GQA_OK;
 }
 
@@ -1353,7 +1389,7 @@ int gqa_layer_qkv_device(gqa_ctx* c, int32_t b, const void* x, int32_t n_tokens,
     if (!(rms_eps >= 0.f) || !isfinite(rms_eps)) return GQA_ERR_RANGE;
     HIP_TRY(hipSetDevice(c->cfg.device));
     return run_layer_qkv(c, b, x, n_tokens, hidden, wq, wk, wv, rms_weight, rms_eps, q_pos_base, kv_pos_base, kv_row0,
-                         rope, q_out, pick_stream(c, stream), c->profile && !c->capturing);
+                         rope, q_out, pick_stream(c, stream), false);
 }
 
 int gqa_submit_layer(gqa_ctx* c, int32_t b, const uint16_t* x, int32_t n_tokens, int32_t hidden, const uint16_t* wq,
@@ -1568,6 +1604,19 @@ int gqa_read_perf(gqa_ctx* c, uint64_t* total_ticks, uint64_t* kernel_ticks, uin
     return GQA_OK;
 }
 
+// ---- measurement ----------------------------------------------------------------------
+
+int gqa_stream_read_device(const void* src, int64_t n_bytes, int32_t n_wgs, int32_t unroll, uint32_t* sink,
+                           void* stream) {
+    if (!src || !sink) return GQA_ERR_NULL;
+    if (n_bytes < 16 || n_bytes % 16 != 0 || n_wgs < 1 || !aligned16(src)) return GQA_ERR_RANGE;
+    if (unroll != 1 && unroll != 2 && unroll != 4 && unroll != 8) return GQA_ERR_RANGE;
+    Launch l;
+    l.stream = (hipStream_t)stream;
+    HIP_TRY(launch_stream_read(src, n_bytes, n_wgs, unroll, sink, l));
+    return GQA_OK;
+}
+
 // ---- timing -------------------------------------------------------------------------
 
 int gqa_last_elapsed_us(gqa_ctx* c, float* out_us) {
@@ -1590,6 +1639,20 @@ int gqa_kernel_times(gqa_ctx* c, float* out_us, int32_t n) {
             total += ms;
         }
         out_us[i] = (float)(total * 1000.0 / c->ev_count[i]);
+    }
+    return GQA_OK;
+}
+
+int gqa_kernel_durations(gqa_ctx* c, int32_t slot, float* out_us, int32_t n, int32_t* n_out) {
+    if (!c || (n > 0 && !out_us)) return GQA_ERR_NULL;
+    if (slot < 0 || slot >= GQA_TIMER_COUNT || n < 0) return GQA_ERR_RANGE;
+    const int recorded = c->profile ? c->ev_count[slot] : 0;
+    if (n_out) *n_out = recorded;
+    for (int k = 0; k < recorded && k < n; ++k) {
+        HIP_TRY(hipEventSynchronize(c->ev_pool[slot][2 * k + 1]));
+        float ms = 0.f;
+        HIP_TRY(hipEventElapsedTime(&ms, c->ev_pool[slot][2 * k], c->ev_pool[slot][2 * k + 1]));
+        out_us[k] = ms * 1000.f;
     }
     return GQA_OK;
 }

@@ -58,6 +58,9 @@ struct DecodeArgs {
     // so the longest sequences are dispatched first (exact order up to 64 sequences, by length
     // bucket beyond).
     int32_t longest_first;
+    // [B*H_kv] split arrival counters, zero between launches: the last split of a (sequence, kv
+    // head) to finish merges the partials itself (no merge launch); nullptr = decode_combine_kernel.
+    int32_t* arrivals;
 };
 
 // Chunked prefill / full-transaction launch description (one sequence b).
@@ -129,7 +132,19 @@ struct RtlArgs {
 };
 hipError_t launch_rtl_transaction(int head_dim, const RtlArgs& a, const Launch& l);
 
+// Splits of a sequence of L attended keys cut into `chunk`-key splits: a last split of at most
+// chunk/4 keys is folded into the one before it (no work-group is left with a handful of keys, such
+// as the row a decode step appends); at least one split.  Split s covers keys
+// [s*chunk, s == n-1 ? L : (s+1)*chunk).
+__host__ __device__ inline int decode_split_count(int L, int chunk) {
+    if (L <= chunk) return 1;
+    const int n = (L + chunk - 1) / chunk;
+    return (L - (n - 1) * chunk <= chunk / 4) ? n - 1 : n;
+}
+
 bool decode_supported(int head_dim, int group);
+// Keys a wave of the decode kernel takes per round (a divisor of 64) for a group size.
+int decode_round_keys(int group);
 // Waves per split work-group of the decode kernel for a group size.
 int decode_waves(int group);
 // Split-KV attention with an optional fused row append; sequences longer than one split
@@ -176,6 +191,11 @@ struct RopeArgs {
     float theta[kMaxRopePairs];  // rotation frequency of pair (2p, 2p+1)
 };
 hipError_t launch_rope_scatter(const RopeArgs& a, const Launch& l);
+
+// Streaming-read ceiling probe (probe.hip): reads n_bytes (a multiple of 16) at src with n_wgs
+// 512-thread work-groups, `unroll` (1, 2, 4 or 8) 16-byte nontemporal loads in flight per thread.
+hipError_t launch_stream_read(const void* src, int64_t n_bytes, int n_wgs, int unroll, uint32_t* sink,
+                              const Launch& l);
 
 // fp32 -> bf16 word, round to nearest even on the upper half: the output rounding of
 // fp32_to_bf16 in hw/rtl/pkg/attn_pkg.sv:618-626 (no NaN special case).

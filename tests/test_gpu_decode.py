@@ -260,3 +260,31 @@ def test_fused_append_decode_matches_two_launches(hq, hkv, d):
                     assert np.array_equal(kr[:, 0], nk[b]) and np.array_equal(vr[:, 0], nv[b])
             check_decode(out_f, lse_f, q, kc, vc, attend, None)
             cur = attend
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (64, 8, 128)])
+def test_decode_fused_merge_matches_merge_launch(hq, hkv, d):
+    """The in-launch merge (last split to arrive) and the separate merge launch fold the same
+    partials in the same order: equal words and LSE, over repeated steps (the arrival counters
+    reset themselves) with sequences of one split, several splits and no key."""
+    rng = np.random.default_rng(300 + hq)
+    B = 4
+    lens = np.array([3000, 129, 0, 2049], np.int32)
+    cap = 3072
+    with make_engine(B, hq, hkv, d, cap) as fused, make_engine(B, hq, hkv, d, cap) as launch:
+        kc, vc = fill_cache(fused, rng, B, hkv, d, lens, lcap=cap)
+        for b in range(B):
+            if lens[b]:
+                launch.load_kv(kc[b, :, :lens[b]], vc[b, :, :lens[b]], b=b)
+        _lib.check(fused._lib.gqa_set_option(fused._ctx, _lib.GQA_OPT_DECODE_MERGE, _lib.GQA_DECODE_MERGE_FUSED), "m")
+        _lib.check(launch._lib.gqa_set_option(launch._ctx, _lib.GQA_OPT_DECODE_MERGE, _lib.GQA_DECODE_MERGE_LAUNCH),
+                   "m")
+        for eng in (fused, launch):
+            _lib.check(eng._lib.gqa_set_option(eng._ctx, _lib.GQA_OPT_DECODE_CHUNK, 256), "chunk")
+        for step in range(3):
+            q = bf16_normal(rng, (B, hq, d))
+            out_f, lse_f = fused.decode_step(q, lens, return_lse=True)
+            out_l, lse_l = launch.decode_step(q, lens, return_lse=True)
+            assert np.array_equal(out_f, out_l), f"step {step}"
+            assert np.array_equal(lse_f.view(np.uint32), lse_l.view(np.uint32))
+            check_decode(out_f, lse_f, q, kc, vc, lens, None)

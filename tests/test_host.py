@@ -91,8 +91,11 @@ def test_tile_pairs_per_head_brute_force():
 
 def test_roofline_bytes_match_measurement_plan():
     ns = bm.compute_model("decode-b64-ctx8192")
-    assert ns["decode_kernel_bytes"] == 2 ** 31 + 64 * 32 * 128 * 2
-    assert ns["step_bytes"] == 2 ** 31 + int(1.25 * 2 ** 20)
+    # the fused decode launch moves every byte of the step: K/V read, Q read, O and appended rows written
+    assert ns["decode_kernel_bytes"] == ns["step_bytes"] == 2 ** 31 + int(1.25 * 2 ** 20)
+    # with a merge launch after it, the split kernel does not write O
+    lens = np.full(64, 8192)
+    assert bm.decode_kernel_bytes(32, 8, 128, lens, writes_output=False) == 2 ** 31 + int(0.75 * 2 ** 20)
     c2 = bm.compute_model("decode-b1-ctx4097")
     assert c2["step_bytes"] - 2 * 8 * 128 * 2 - 2 * 32 * 128 * 2 == 16781312
     c5 = bm.compute_model("prefill-chunked-2048")
