@@ -120,12 +120,14 @@ def timed_passes(lib, _lib, ctx, stream, step, steps: int, warmup: int) -> dict:
     n_gated = max(steps, MIN_GATED_STEPS)
     _lib.check(lib.gqa_set_option(ctx, _lib.GQA_OPT_PROFILE, 1), "profile on")
     try:
-        t1 = time.perf_counter()
-        step()  # host cost of one profiled step
-        host_us = (time.perf_counter() - t1) * 1e6
-        torch.cuda.synchronize()
+        host_us = 0.0
+        for _ in range(3):  # host cost of a profiled step: the largest of three
+            t1 = time.perf_counter()
+            step()
+            host_us = max(host_us, (time.perf_counter() - t1) * 1e6)
+            torch.cuda.synchronize()
         _lib.check(lib.gqa_set_option(ctx, _lib.GQA_OPT_PROFILE, 1), "profile restart")
-        gate_us = min(MAX_GATE_US, 2.0 * host_us * n_gated + 1000.0)
+        gate_us = min(MAX_GATE_US, 3.0 * host_us * n_gated + 2000.0)
         g0 = torch.cuda.Event(enable_timing=True)
         g1 = torch.cuda.Event(enable_timing=True)
         with torch.cuda.stream(stream):
@@ -142,6 +144,7 @@ def timed_passes(lib, _lib, ctx, stream, step, steps: int, warmup: int) -> dict:
         _lib.check(lib.gqa_kernel_times(ctx, times, _lib.GQA_TIMER_COUNT), "kernel times")
         _lib.check(lib.gqa_kernel_launch_counts(ctx, counts, _lib.GQA_TIMER_COUNT), "counts")
         step_us = np.zeros(n_gated)
+        launch_us = {}
         for slot in range(_lib.GQA_TIMER_COUNT):
             n = int(counts[slot])
             if n == 0:
@@ -150,6 +153,7 @@ def timed_passes(lib, _lib, ctx, stream, step, steps: int, warmup: int) -> dict:
             got = ctypes.c_int32()
             _lib.check(lib.gqa_kernel_durations(ctx, slot, d, n, ctypes.byref(got)), "durations")
             per = np.frombuffer(d, dtype=np.float32).astype(np.float64)
+            launch_us[slot] = per
             if n % n_gated == 0:
                 step_us += per.reshape(n_gated, n // n_gated).sum(axis=1)
             else:  # launches do not split evenly over the steps: spread the mean
@@ -158,7 +162,7 @@ def timed_passes(lib, _lib, ctx, stream, step, steps: int, warmup: int) -> dict:
         _lib.check(lib.gqa_set_option(ctx, _lib.GQA_OPT_PROFILE, 0), "profile off")
     return {"wall_ms": wall_ms, "gpu_ms": gpu_ms, "times": list(times), "counts": list(counts),
             "step_us": step_us, "gate_held": bool(gate_held), "gate_us": gate_us, "gated_steps": n_gated,
-            "gated_gpu_ms": gated_gpu_ms}
+            "gated_gpu_ms": gated_gpu_ms, "launch_us": launch_us}
 
 
 def step_stats(step_us) -> dict:
@@ -388,7 +392,12 @@ class PrefillBench:
         _lib = self._lib
         t = timed_passes(self.lib, _lib, self.ctx, self.stream, self.step, steps, warmup)
         prompts = t["gated_steps"]
+        # mean duration of each chunk's prefill launch (launches repeat chunk by chunk, prompt by prompt)
+        pre = t["launch_us"].get(_lib.GQA_TIMER_PREFILL)
+        per_chunk = (pre.reshape(prompts, -1).mean(axis=0).tolist()
+                     if pre is not None and pre.size % prompts == 0 else None)
         return {"wall_us_per_prompt": t["wall_ms"] * 1e3, "gpu_us_per_prompt": t["gpu_ms"] * 1e3,
+                "prefill_us_per_chunk": per_chunk,
                 "prompt_us": step_stats(t["step_us"]), "gate_held": t["gate_held"],
                 "gated_gpu_us_per_prompt": t["gated_gpu_ms"] * 1e3,
                 "prefill_us_per_prompt": t["times"][_lib.GQA_TIMER_PREFILL] * t["counts"][_lib.GQA_TIMER_PREFILL] / prompts,
@@ -422,6 +431,7 @@ def measure_prefill(name: str, steps: int, warmup: int, target_wgs: int = 0) -> 
         "prompt_us": r["prompt_us"],
         "gated_gpu_us_per_prompt": r["gated_gpu_us_per_prompt"],
         "prefill_kernel_us_per_prompt": kern_us,
+        "prefill_kernel_us_per_chunk": r["prefill_us_per_chunk"],
         "segment_merge_us_per_prompt": merge_us,
         "launches_per_prompt": r["launches_per_prompt"],
         "chunks": len(sched),
@@ -441,6 +451,8 @@ def measure_prefill(name: str, steps: int, warmup: int, target_wgs: int = 0) -> 
         f"{out['gated_gpu_us_per_prompt']:.1f}), prefill kernels "
         f"{kern_us:.1f} us = {out['kernel_tflops'] or 0:.1f} TFLOP/s, segment merges {merge_us:.1f} us"
         + ("" if r["gate_held"] else " [gate released before the queue was full]"))
+    if r["prefill_us_per_chunk"]:
+        log(f"{name}: prefill kernel per chunk (us): " + ", ".join(f"{x:.1f}" for x in r["prefill_us_per_chunk"]))
     return out
 
 

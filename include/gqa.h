@@ -73,6 +73,17 @@ extern "C" {
 #define GQA_OPT_PREFILL_WGS  3 /* prefill work-groups the KV segmentation aims for (0 = auto: one per CU, 1 = none) */
 #define GQA_OPT_NUMERICS     4 /* GQA_NUMERICS_*: arithmetic of prefill / transactions (decode: EXACT only) */
 #define GQA_OPT_DECODE_MERGE 5 /* GQA_DECODE_MERGE_*: how split-KV decode merges a sequence's splits */
+#define GQA_OPT_PREFILL_KERNEL 6 /* GQA_PREFILL_KERNEL_*: decomposition of prefill / transaction launches */
+
+/* Prefill decomposition (GQA_OPT_PREFILL_KERNEL).  SHARED: a work-group per kv head and 8 (32-row
+ * block, query head) tasks shares each K/V tile over its GQA group; launches smaller than the GPU are
+ * cut into KV segments merged by a second launch (GQA_OPT_PREFILL_WGS).  ROWS: a work-group per
+ * (query head, 32-row block) whose waves split the keys and merge in LDS (one launch, no segments).
+ * AUTO (default): ROWS when the SHARED grid without segments has fewer work-groups than the GPU has
+ * CUs and no segment target is set, else SHARED. */
+#define GQA_PREFILL_KERNEL_AUTO   0
+#define GQA_PREFILL_KERNEL_SHARED 1
+#define GQA_PREFILL_KERNEL_ROWS   2
 
 /* Split merge of the decode (GQA_OPT_DECODE_MERGE).  FUSED (default): the last split of a (sequence,
  * kv head) to finish merges the others' partials inside the decode launch (agent-scope atomics and a

@@ -52,6 +52,10 @@ GQA_OPT_NUMERICS = 4
 GQA_OPT_DECODE_MERGE = 5
 GQA_DECODE_MERGE_FUSED = 0
 GQA_DECODE_MERGE_LAUNCH = 1
+GQA_OPT_PREFILL_KERNEL = 6
+GQA_PREFILL_KERNEL_AUTO = 0
+GQA_PREFILL_KERNEL_SHARED = 1
+GQA_PREFILL_KERNEL_ROWS = 2
 GQA_NUMERICS_EXACT = 0
 GQA_NUMERICS_KV260 = 1
 

@@ -64,6 +64,7 @@ struct gqa_ctx {
     float* part_ml = nullptr;
     int32_t* arrivals = nullptr;  // [B*H_kv] split arrival counters of the fused merge (zero between launches)
     int decode_merge = GQA_DECODE_MERGE_FUSED;
+    int prefill_kernel = GQA_PREFILL_KERNEL_AUTO;
     float* pre_ws = nullptr;     // prefill KV-segment partials (O, then (m, l))
     uint16_t* zero_row = nullptr;  // one zero K/V row: the prefill source of rows past kv_len
     size_t pre_ws_floats = 0;
@@ -308,6 +309,11 @@ int run_prefill(gqa_ctx* c, int32_t b, const void* q, int32_t q_len, int32_t q_p
         return GQA_OK;
     }
     if (!prefill_supported(c->cfg.head_dim, c->group)) return GQA_ERR_UNSUPPORTED;
+    // Launches whose shared-tile grid would not fill the GPU without KV segments take the row-block
+    // kernel (no segments, no merge launch), unless a segment target is set.
+    const bool rows = c->prefill_kernel == GQA_PREFILL_KERNEL_ROWS ||
+                      (c->prefill_kernel == GQA_PREFILL_KERNEL_AUTO && c->prefill_wgs_opt == 0 &&
+                       prefill_shared_wgs(q_len, c->group, c->cfg.n_kv_heads) < c->n_cu);
     int kv_span = kv_len;
     if (causal) kv_span = std::min(kv_len, std::max(0, q_pos_base + q_len - kv_pos_base));
     const int target = c->prefill_wgs_opt > 0 ? c->prefill_wgs_opt : c->n_cu;
@@ -341,6 +347,10 @@ int run_prefill(gqa_ctx* c, int32_t b, const void* q, int32_t q_len, int32_t q_p
     a.zero_row = c->zero_row;
     a.part_o = reinterpret_cast<uint16_t*>(c->pre_ws);
     a.part_ml = c->pre_ws + (size_t)plan.n_segs * c->cfg.n_q_heads * q_len * (c->cfg.head_dim / 2);
+    if (rows) {
+        HIP_TRY(launch_prefill_rows(c->cfg.head_dim, a, timed(c, GQA_TIMER_PREFILL, s)));
+        return GQA_OK;
+    }
     HIP_TRY(launch_prefill(c->cfg.head_dim, c->group, a, timed(c, GQA_TIMER_PREFILL, s)));
     if (plan.n_segs > 1) HIP_TRY(launch_prefill_combine(c->cfg.head_dim, a, timed(c, GQA_TIMER_COMBINE, s)));
     return GQA_OK;
@@ -914,6 +924,12 @@ int gqa_set_option(gqa_ctx* c, int32_t option, int64_t value) {
             return GQA_OK;
         case GQA_OPT_PROFILE:
             return profile_enable(c, value ? 1 : 0);
+        case GQA_OPT_PREFILL_KERNEL:
+            if (value != GQA_PREFILL_KERNEL_AUTO && value != GQA_PREFILL_KERNEL_SHARED &&
+                value != GQA_PREFILL_KERNEL_ROWS)
+                return GQA_ERR_RANGE;
+            c->prefill_kernel = (int)value;
+            return GQA_OK;
         case GQA_OPT_DECODE_MERGE:
             if (value != GQA_DECODE_MERGE_FUSED && value != GQA_DECODE_MERGE_LAUNCH) return GQA_ERR_RANGE;
             c->decode_merge = (int)value;

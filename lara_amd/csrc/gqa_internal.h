@@ -85,8 +85,9 @@ struct PrefillArgs {
     float* lse;             // [H_q][q_len] or nullptr
     int32_t seg_len;        // keys per KV segment (multiple of 64)
     int32_t n_segs;         // KV segments (grid z); 1 = write the output directly
-    uint16_t* part_o;       // [n_segs][H_q][q_len][D] fp16 words: the segment's O / l divided by `scale`
-    float* part_ml;         // [n_segs][H_q][q_len][4] (running max in log2 units, sum l, scale, unused)
+    uint16_t* part_o;       // [n_segs][H_q][q_len][D] fp16 words: the segment's O divided by 2^e, e the
+                            //   exponent of the row's largest |O| (frexp)
+    float* part_ml;         // [n_segs][H_q][q_len][4] (running max in log2 units, sum l, e, unused)
     const uint16_t* zero_row;  // >= D zero words: the source of K/V rows past kv_len
     // Paged cache: block_table is sequence b's row of page indices (-1 = unmapped, read as
     // zero_row, never written), kc/vc the pools [n_pages][H_kv][2^page_shift][D]; nullptr =
@@ -154,6 +155,12 @@ hipError_t launch_combine(int head_dim, int group, const DecodeArgs& a, const La
 
 bool prefill_supported(int head_dim, int group);
 hipError_t launch_prefill(int head_dim, int group, const PrefillArgs& a, const Launch& l);
+// One work-group per (query head, 32-row block), the waves splitting the keys and merging in LDS:
+// for launches whose shared-tile grid (prefill_shared_wgs, no KV segments) is smaller than the GPU.
+// Ignores seg_len / n_segs / part_*.
+hipError_t launch_prefill_rows(int head_dim, const PrefillArgs& a, const Launch& l);
+// Work-groups of launch_prefill for q_len rows without KV segments.
+int prefill_shared_wgs(int q_len, int group, int n_kv_heads);
 // Merges the KV segments of a prefill launch with n_segs > 1.
 hipError_t launch_prefill_combine(int head_dim, const PrefillArgs& a, const Launch& l);
 

@@ -101,7 +101,20 @@ __device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_addr) {
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(gptr), "s"(lds_addr)
                  : "memory", "m0");
 }
+// The same load with a wave-uniform 64-bit base in SGPRs and a 32-bit per-lane byte offset.
+__device__ __forceinline__ void dma16_sbase(uint64_t sbase, uint32_t voff, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 offset:0" : : "v"(voff), "s"(sbase),
+                 "s"(lds_addr) : "memory", "m0");
+}
 #pragma clang diagnostic pop
+
+// A wave-uniform pointer as an SGPR pair.
+__device__ __forceinline__ uint64_t uniform_address(const void* p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return ((uint64_t)hi << 32) | lo;
+}
 
 // 16-byte LDS read issued from inline assembly, so it stays where it is written: the
 // compiler's scheduler, short of registers, would otherwise move every read next to its use
@@ -485,9 +498,10 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
     if (a.n_segs > 1) {
         // Rows this wave never reached in the segment are not read by the merge.
         if (seg_begin >= wave_hi) return;
-        // The segment's O / l in fp16, divided by the row's largest |O / l| so every dim keeps
-        // 11 significant bits relative to the row (a bf16 ulp is 8), and (m, l, scale) in fp32:
-        // half the bytes of an fp32 partial, written here and read once by the merge.
+        // The segment's unnormalised O in fp16, divided by the power of two 2^e just above the row's
+        // largest |O| (exact, any magnitude) so every dim keeps 11 significant bits relative to the
+        // row (a bf16 ulp is 8), and (m, l, e) in fp32: half the bytes of an fp32 partial, written
+        // here and read once by the merge.
         const size_t prow = ((size_t)blockIdx.z * a.n_q_heads + hq) * a.q_len + row;
         float amax = 0.f;
 #pragma unroll
@@ -495,20 +509,19 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(o[mt][i]));
         amax = fmaxf(amax, half_swap(amax, half));  // the row's other half-wave
-        // The merge rebuilds O_s as l * scale * (o * k) = o * amax * k: k only has to be close
-        // to 1 / amax (so o * k stays within fp16 range), not exact.
-        const float k = amax > 0.f ? __builtin_amdgcn_rcpf(amax) : 0.f;
-        const float scale = l_row > 0.f && amax > 0.f ? amax / l_row : 1.f;
+        int e = 0;
+        if (amax > 0.f) (void)frexpf(amax, &e);  // amax in [2^(e-1), 2^e)
         uint16_t* po = a.part_o + prow * D;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
             for (int r4 = 0; r4 < 4; ++r4) {
-                const f16x4 w = {(_Float16)(o[mt][4 * r4 + 0] * k), (_Float16)(o[mt][4 * r4 + 1] * k),
-                                 (_Float16)(o[mt][4 * r4 + 2] * k), (_Float16)(o[mt][4 * r4 + 3] * k)};
+                const f16x4 w = {(_Float16)ldexpf(o[mt][4 * r4 + 0], -e), (_Float16)ldexpf(o[mt][4 * r4 + 1], -e),
+                                 (_Float16)ldexpf(o[mt][4 * r4 + 2], -e), (_Float16)ldexpf(o[mt][4 * r4 + 3], -e)};
                 *reinterpret_cast<uint2*>(po + mt * 32 + 8 * r4 + 4 * half) = __builtin_bit_cast(uint2, w);
             }
-        if (half == 0) *reinterpret_cast<float4*>(a.part_ml + prow * 4) = make_float4(m_run, l_row, scale, 0.f);
+        if (half == 0)
+            *reinterpret_cast<float4*>(a.part_ml + prow * 4) = make_float4(m_run, l_row, (float)e, 0.f);
         return;
     }
     const float inv = l_row > 0.f ? 1.f / l_row : 0.f;
@@ -526,6 +539,391 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
         a.lse[(size_t)hq * a.q_len + row] = l_row > 0.f ? (m_run + log2f(l_row)) * kLn2 : -INFINITY;
 }
 
+// ---- Row-block prefill for launches too small to fill the GPU ------------------------------
+//
+// One work-group per (query head, 32-row block): a 256-row chunk over 32 query heads is 256
+// work-groups, one per CU, with no KV segments across work-groups and so no partials and no merge
+// launch.  The four waves (one per SIMD) take the row block's 32-key blocks in turn (wave w: blocks
+// w, w+4, ...), each streaming its own K and V tiles through a private two-stage LDS ring with
+// direct-to-LDS loads, so no wave waits for another inside the loop.  At the end the waves merge
+// their (m, l, O) through LDS and write the bf16 rows.  Grid x is the kv head: work-groups are dealt
+// to the XCDs round robin by linear index, so with 8 kv heads every work-group reading one head's
+// K/V runs on the same XCD and finds them in its L2.  Fragment layouts are prefill_kernel's with one
+// 32-key tile per block (S^T = K . Q^T one 32x32 tile, eight k-steps; O^T += V^T . P^T in two
+// 16-key k-steps per 32-dim tile).
+constexpr int kRowBN = 32;  // keys per block
+
+// s_waitcnt lgkmcnt(N) that the compiler sees as producing a (see lgkm_wait).
+template <int N, typename T>
+__device__ __forceinline__ void lgkm_wait1(T& a) {
+    static_assert(N >= 0 && N < 16, "lgkmcnt range");
+    asm volatile("s_waitcnt %1" : "+v"(a) : "i"(0xF | (0x3 << 14) | (0x7 << 4) | (N << 8)));
+}
+
+// NW waves per work-group take the row block's key blocks in turn; NS: stages of each wave's ring.
+template <int D, bool PAGED, int NW, int NS>
+__global__ __launch_bounds__(NW * 64) void prefill_rows_kernel(PrefillArgs a) {
+    constexpr int kRowWaves = NW;
+    constexpr int kRowStages = NS;
+    static_assert(NS == 1 || NS == 2, "ring depth");
+    constexpr int NCH = D / 8;         // 16-byte chunks per K/V row
+    constexpr int KSTEPS = D / 16;     // QK k-steps
+    constexpr int MT = D / 32;         // PV result tiles (32 dims each)
+    constexpr int TILE = kRowBN * NCH; // 16-byte chunks per K (or V) tile
+    constexpr int DMA = TILE / 64;     // direct-to-LDS loads per lane per tile
+    constexpr int LPB = 2 * DMA;       // per block (K and V)
+    static_assert(DMA >= 1 && DMA * 64 == TILE, "tile shape");
+    static_assert(D * kRows * 4 <= kRowStages * 2 * TILE * 16, "a wave's O^T fits its ring");
+
+    // Per wave: its ring of [stage][K, V] tiles, reused for the wave's O^T after the loop, and its
+    // rows' (m, l).
+    __shared__ __attribute__((aligned(16))) u32x4 lds[kRowWaves][kRowStages][2][TILE];
+    __shared__ float lds_ml[kRowWaves][2][kRows];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = blockIdx.x;  // kv head
+    const int G = a.n_q_heads / a.n_kv_heads;
+    const int n_rb = (a.q_len + kRows - 1) / kRows;
+    const int g = blockIdx.y % G;
+    // Causal row blocks grow in work with their index: the largest are dispatched first.
+    const int rb = a.causal ? n_rb - 1 - (int)(blockIdx.y / G) : (int)(blockIdx.y / G);
+    const int hq = h * G + g;
+
+    int kv_hi = a.kv_len;  // keys the row block needs: [0, kv_hi)
+    if (a.causal) kv_hi = min(kv_hi, a.q_pos_base + min(a.q_len, (rb + 1) * kRows) - 1 - a.kv_pos_base + 1);
+    kv_hi = max(kv_hi, 0);
+    const int n_blocks = (kv_hi + kRowBN - 1) / kRowBN;
+    const int my_blocks = n_blocks > wave ? (n_blocks - wave + kRowWaves - 1) / kRowWaves : 0;
+
+    const int col = lane & 31;   // query row within the block (MFMA column)
+    const int half = lane >> 5;  // which 8 k-values of a step this lane carries
+    const int row = rb * kRows + col;
+    const bool row_ok = row < a.q_len;
+    const int q_pos = a.q_pos_base + row;
+
+    const u32x4* kg = reinterpret_cast<const u32x4*>(a.kc + (PAGED ? 0 : (size_t)h * a.l_cap * D));
+    const u32x4* vg = reinterpret_cast<const u32x4*>(a.vc + (PAGED ? 0 : (size_t)h * a.l_cap * D));
+    const bool has_new = a.k_new != nullptr && a.n_new > 0;
+    const u32x4* kn = has_new ? reinterpret_cast<const u32x4*>(a.k_new) + (size_t)h * a.n_new * NCH : nullptr;
+    const u32x4* vn = has_new ? reinterpret_cast<const u32x4*>(a.v_new) + (size_t)h * a.n_new * NCH : nullptr;
+    const u32x4* zero = reinterpret_cast<const u32x4*>(a.zero_row);
+
+    // Direct-to-LDS staging of the block at key j0 into this wave's stage st: load instruction i
+    // fills slots i*64 + lane, and each lane loads the 16-byte chunk the swizzled layout wants in its
+    // slot: byte offset koff[i] (K) / voff[i] (V) from the block's first row.  A block whose rows all
+    // come from one contiguous run -- the cache, or the rows this launch appends -- takes a
+    // wave-uniform base and these fixed offsets; a block that straddles the appended rows or ends
+    // past kv_len (zero row there: stale words may be NaN) picks each lane's source.
+    uint32_t koff[DMA], voff[DMA];
+#pragma unroll
+    for (int i = 0; i < DMA; ++i) {
+        const int slot = i * 64 + lane;
+        const int key = slot / NCH;
+        koff[i] = 16u * (uint32_t)(key * NCH + ((slot % NCH) ^ k_swz<NCH>(key)));
+        voff[i] = 16u * (uint32_t)(key * NCH + ((slot % NCH) ^ v_swz<D>(key)));
+    }
+    const int new_end = has_new ? a.new_begin + a.n_new : 0;
+    auto issue = [&](int j0, int st) {
+        // Row j0's K and V, or nullptr where the block's rows do not share one source.
+        const u32x4* krow = nullptr;
+        const u32x4* vrow = nullptr;
+        if (j0 + kRowBN <= a.kv_len) {
+            if (has_new && j0 >= a.new_begin && j0 + kRowBN <= new_end) {
+                krow = kn + (size_t)(j0 - a.new_begin) * NCH;
+                vrow = vn + (size_t)(j0 - a.new_begin) * NCH;
+            } else if (!has_new || j0 + kRowBN <= a.new_begin || j0 >= new_end) {
+                if constexpr (PAGED) {  // j0 and the page size are multiples of 32: one page per block
+                    const int64_t pr = paged_row(a.block_table, a.page_shift, a.n_kv_heads, h, j0);
+                    krow = pr < 0 ? nullptr : kg + (size_t)pr * NCH;
+                    vrow = pr < 0 ? nullptr : vg + (size_t)pr * NCH;
+                } else {
+                    krow = kg + (size_t)j0 * NCH;
+                    vrow = vg + (size_t)j0 * NCH;
+                }
+            }
+        }
+        if (krow != nullptr) {
+            const uint64_t kb = uniform_address(krow), vb = uniform_address(vrow);
+#pragma unroll
+            for (int i = 0; i < DMA; ++i) {
+                dma16_sbase(kb, koff[i], lds_addr(&lds[wave][st][0][i * 64]));
+                dma16_sbase(vb, voff[i], lds_addr(&lds[wave][st][1][i * 64]));
+            }
+            return;
+        }
+        int64_t pr0 = 0;  // paged: the block's page row (-1: unmapped, zero rows)
+        if constexpr (PAGED) pr0 = paged_row(a.block_table, a.page_shift, a.n_kv_heads, h, j0);
+#pragma unroll
+        for (int i = 0; i < DMA; ++i) {
+            const int rel = (int)(koff[i] >> 4) / NCH;  // key of this lane's slot within the block
+            const int row_idx = j0 + rel;
+            const uint32_t kc_off = koff[i] - 16u * (uint32_t)(rel * NCH);  // chunk offset within the row
+            const uint32_t vc_off = voff[i] - 16u * (uint32_t)(rel * NCH);
+            const u32x4* sk;
+            const u32x4* sv;
+            const unsigned r_new = (unsigned)(row_idx - a.new_begin);
+            if (row_idx >= a.kv_len || (PAGED && pr0 < 0)) {
+                sk = zero;
+                sv = zero;
+            } else if (has_new && r_new < (unsigned)a.n_new) {
+                sk = kn + (size_t)r_new * NCH;
+                sv = vn + (size_t)r_new * NCH;
+            } else if constexpr (PAGED) {
+                sk = kg + (size_t)(pr0 + rel) * NCH;
+                sv = vg + (size_t)(pr0 + rel) * NCH;
+            } else {
+                sk = kg + (size_t)row_idx * NCH;
+                sv = vg + (size_t)row_idx * NCH;
+            }
+            dma16(reinterpret_cast<const uint8_t*>(sk) + kc_off, lds_addr(&lds[wave][st][0][i * 64]));
+            dma16(reinterpret_cast<const uint8_t*>(sv) + vc_off, lds_addr(&lds[wave][st][1][i * 64]));
+        }
+    };
+
+    // Operand addresses in stage 0 of this wave's ring (a stage adds stage_bytes).
+    constexpr uint32_t stage_bytes = 2 * TILE * 16;
+    uint32_t kaddr[KSTEPS];
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks)
+        kaddr[ks] = lds_addr(&lds[wave][0][0][0]) + 16u * (uint32_t)(col * NCH + ((2 * ks + half) ^ k_swz<NCH>(col)));
+    uint32_t vaddr[MT];
+    {
+        const int key_off = (lane & 15) >> 2;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const int dim = mt * 32 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+            vaddr[mt] = lds_addr(&lds[wave][0][1][0]) + (uint32_t)((key_off + 4 * half) * (D * 2) +
+                                                                   (((dim >> 3) ^ v_swz<D>(key_off)) << 4) +
+                                                                   (((dim >> 2) & 1) << 3));
+        }
+    }
+
+    f32x16 o[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[mt][i] = 0.f;
+    float m_run = -INFINITY;  // running max (log2 units) of this lane's row
+    float l_lane = 0.f;       // this lane's half of the running sum
+    constexpr float kLazyLog2 = 8.0f;  // the reference max moves only when passed by more than this
+    const float c = a.scale_log2;
+
+    // Q^T operand (row `row`, dims 16*ks + 8*half .. +7), the wave's first two blocks and this
+    // work-group's share of the appended rows are all in flight before the first wait.
+    u32x4 qb[KSTEPS];
+    {
+        const u32x4* qp = reinterpret_cast<const u32x4*>(a.q + ((size_t)hq * a.q_len + row) * D);
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks) qb[ks] = row_ok ? qp[2 * ks + half] : u32x4{0u, 0u, 0u, 0u};
+    }
+    if (my_blocks > 0) issue(wave * kRowBN, 0);
+    if (kRowStages > 1 && my_blocks > 1) issue((wave + kRowWaves) * kRowBN, kRowStages - 1);
+    // Appended rows of kv head h go to the cache in equal shares over the kv head's work-groups;
+    // blocks that hold them read k_new/v_new, so no work-group waits for the copy.  A thread's first
+    // word is loaded with Q and the first blocks and stored after the wait below (the loop's own
+    // waits then cover the store); any further words (more appended rows than threads) follow.
+    const int app_words = has_new ? a.n_new * NCH : 0;
+    const int app_stride = gridDim.y * (kRowWaves * 64);
+    const int app_first = blockIdx.y * (kRowWaves * 64) + tid;
+    auto app_dst = [&](int i) -> int64_t {  // 16-byte word index of appended word i, or -1 (unmapped)
+        if constexpr (PAGED) {
+            const int64_t r = paged_row(a.block_table, a.page_shift, a.n_kv_heads, h, a.new_begin + i / NCH);
+            return r < 0 ? -1 : r * NCH + (i % NCH);
+        } else {
+            return ((int64_t)h * a.l_cap + a.new_begin) * NCH + i;
+        }
+    };
+    u32x4 app_k{}, app_v{};
+    if (app_first < app_words) {
+        app_k = kn[app_first];
+        app_v = vn[app_first];
+    }
+    wait_vmcnt<0>();  // Q, the first blocks and the first appended word
+    if (app_first < app_words) {
+        const int64_t dst = app_dst(app_first);
+        if (dst >= 0) {
+            reinterpret_cast<u32x4*>(a.kc)[dst] = app_k;
+            reinterpret_cast<u32x4*>(a.vc)[dst] = app_v;
+        }
+        for (int i = app_first + app_stride; i < app_words; i += app_stride) {
+            const u32x4 wk = kn[i], wv = vn[i];
+            const int64_t d2 = app_dst(i);
+            if (d2 >= 0) {
+                reinterpret_cast<u32x4*>(a.kc)[d2] = wk;
+                reinterpret_cast<u32x4*>(a.vc)[d2] = wv;
+            }
+        }
+        // The stores stay in flight: the loop's vmcnt waits also count them, which only makes the
+        // first of those waits (block 1) wait for them as well.
+    }
+
+    for (int t = 0; t < my_blocks; ++t) {
+        const int st = t % kRowStages;
+        const int j0 = (wave + t * kRowWaves) * kRowBN;
+        if (t >= 1) {  // block t landed once at most the later blocks' loads (a two-stage ring: t+1) remain
+            if (kRowStages > 1 && t + 1 < my_blocks) wait_vmcnt<LPB>(); else wait_vmcnt<0>();
+        }
+        const uint32_t stage_off = (uint32_t)st * stage_bytes;
+
+        // ---- S^T = K . Q^T (raw scores): one 32x32 tile, K fragments read one step ahead ----
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        f32x16 sacc;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sacc[i] = 0.f;
+        u32x4 kf[KSTEPS];
+        kf[0] = lds_read128(kaddr[0] + stage_off);
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks) {
+            if (ks + 1 < KSTEPS) {
+                kf[ks + 1] = lds_read128(kaddr[ks + 1] + stage_off);
+                lgkm_wait1<1>(kf[ks]);
+            } else {
+                lgkm_wait1<0>(kf[ks]);
+            }
+            sacc = mfma32(kf[ks], qb[ks], sacc);
+        }
+
+        // ---- online softmax (log2 domain, scale folded into the exponent) ----
+        const bool need_mask =
+            (j0 + kRowBN > a.kv_len) || (a.causal && a.kv_pos_base + j0 + kRowBN - 1 > a.q_pos_base + rb * kRows);
+        float mx = -INFINITY;
+        if (need_mask) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int j = j0 + 8 * (i >> 2) + 4 * half + (i & 3);
+                const bool ok = row_ok && j < a.kv_len && (!a.causal || a.kv_pos_base + j <= q_pos);
+                sacc[i] = ok ? sacc[i] : -INFINITY;
+                mx = fmaxf(mx, sacc[i]);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[i]);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float bm = mx * c;
+        const bool grow = bm > m_run + kLazyLog2;
+        if (__ballot(grow) != 0) {
+            const float m_new = grow ? bm : m_run;
+            const float corr = (m_run == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
+            m_run = m_new;
+            l_lane *= corr;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) o[mt][i] *= corr;
+        }
+        const float nm = (m_run == -INFINITY) ? 0.f : -m_run;
+        float psum = 0.f;
+        u32x4 pb[2];  // P^T operand of the two PV k-steps (keys 0-15, 16-31 of the block)
+#pragma unroll
+        for (int a2 = 0; a2 < 2; ++a2) {
+            float p[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                p[j] = __builtin_amdgcn_exp2f(fmaf(sacc[8 * a2 + j], c, nm));
+                psum += p[j];
+            }
+            pb[a2] = u32x4{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
+                           pack_bf16x2(p[6], p[7])};
+        }
+        l_lane += psum;
+
+        // ---- O^T += V^T . P^T, transposing V reads one step ahead ----
+        constexpr int PV = MT * 2;
+        u32x2 vf[PV][2];
+        auto read_v = [&](auto step_c) {
+            constexpr int i = decltype(step_c)::value;
+            constexpr int kb = 16 * (i & 1);  // step's key base within the block (half adds 4)
+            const uint32_t va = vaddr[i >> 1] + stage_off;
+            vf[i][0] = lds_read_tr64<kb * (D * 2)>(va);
+            vf[i][1] = lds_read_tr64<(kb + 8) * (D * 2)>(va);
+        };
+        read_v(std::integral_constant<int, 0>{});
+        static_for<PV>([&](auto step_c) {
+            constexpr int i = decltype(step_c)::value;
+            if constexpr (i + 1 < PV) {
+                read_v(std::integral_constant<int, i + 1>{});
+                lgkm_wait<2>(vf[i][0], vf[i][1]);
+            } else {
+                lgkm_wait<0>(vf[i][0], vf[i][1]);
+            }
+            const u32x4 vw = {vf[i][0].x, vf[i][0].y, vf[i][1].x, vf[i][1].y};
+            o[i >> 1] = mfma32(vw, pb[i & 1], o[i >> 1]);
+        });
+        // Every read of stage st is complete (lgkmcnt(0) above): it takes block t + NS.
+        if (t + kRowStages < my_blocks) issue((wave + (t + kRowStages) * kRowWaves) * kRowBN, st);
+    }
+
+    // ---- merge the waves: each writes (O^T [D][32 rows], m, l) to its own ring (no DMA pending) ----
+    const float l_row = l_lane + half_swap(l_lane, half);
+    float* mo = reinterpret_cast<float*>(&lds[wave][0][0][0]);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mo[(mt * 32 + 8 * (i >> 2) + 4 * half + (i & 3)) * kRows + col] = o[mt][i];
+    if (half == 0) {
+        lds_ml[wave][0][col] = m_run;
+        lds_ml[wave][1][col] = l_row;
+    }
+    __syncthreads();
+    // The work-group's threads over 32 rows: each takes DPT dims (at least 8, one 16-byte store).
+    constexpr int NDG = kRowWaves * 64 / kRows;
+    constexpr int DPT = D / NDG >= 8 ? D / NDG : 8;
+    const int r = tid & 31;
+    const int dg = tid >> 5;
+    const int out_row = rb * kRows + r;
+    if (out_row >= a.q_len || dg * DPT >= D) return;
+    float wt[kRowWaves];
+    float M = -INFINITY, L = 0.f;
+#pragma unroll
+    for (int w = 0; w < kRowWaves; ++w) M = fmaxf(M, lds_ml[w][0][r]);
+#pragma unroll
+    for (int w = 0; w < kRowWaves; ++w) {
+        const float mw = lds_ml[w][0][r];
+        wt[w] = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M);
+        L = fmaf(wt[w], lds_ml[w][1][r], L);
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    uint16_t* orow = a.out + ((size_t)hq * a.q_len + out_row) * D + dg * DPT;
+#pragma unroll
+    for (int d8 = 0; d8 < DPT; d8 += 8) {
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            float acc = 0.f;
+#pragma unroll
+            for (int w = 0; w < kRowWaves; ++w)
+                acc = fmaf(wt[w], reinterpret_cast<const float*>(&lds[w][0][0][0])[(dg * DPT + d8 + k) * kRows + r], acc);
+            v[k] = acc * inv;
+        }
+        uint4 wv;
+        wv.x = (uint32_t)f32_to_bf16_rne(v[0]) | ((uint32_t)f32_to_bf16_rne(v[1]) << 16);
+        wv.y = (uint32_t)f32_to_bf16_rne(v[2]) | ((uint32_t)f32_to_bf16_rne(v[3]) << 16);
+        wv.z = (uint32_t)f32_to_bf16_rne(v[4]) | ((uint32_t)f32_to_bf16_rne(v[5]) << 16);
+        wv.w = (uint32_t)f32_to_bf16_rne(v[6]) | ((uint32_t)f32_to_bf16_rne(v[7]) << 16);
+        *reinterpret_cast<uint4*>(orow + d8) = wv;
+    }
+    if (dg == 0 && a.lse != nullptr)
+        a.lse[(size_t)hq * a.q_len + out_row] = L > 0.f ? (M + log2f(L)) * kLn2 : -INFINITY;
+}
+
+// Row-block kernel shape: 8 waves (two per SIMD: one wave's MFMAs run while the other waits on
+// LDS or loads) with single-stage rings, 128 KiB of LDS at D = 128.
+constexpr int kRowWaves = 8;
+constexpr int kRowStages = 1;
+
+template <int D>
+hipError_t launch_prefill_rows_t(const PrefillArgs& a, const Launch& l) {
+    const int n_rb = (a.q_len + kRows - 1) / kRows;
+    const int G = a.n_q_heads / a.n_kv_heads;
+    dim3 grid(a.n_kv_heads, G * n_rb);
+    if (a.block_table != nullptr)
+        return launch_kernel(prefill_rows_kernel<D, true, kRowWaves, kRowStages>, grid, dim3(kRowWaves * 64), l, a);
+    return launch_kernel(prefill_rows_kernel<D, false, kRowWaves, kRowStages>, grid, dim3(kRowWaves * 64), l, a);
+}
+
 // Merge of a row's KV segments.  Segment s holds keys [s*seg_len, (s+1)*seg_len); a row
 // reads the segments below its own key limit, which are exactly the ones prefill_kernel
 // wrote for it.  A work-group merges kMergeRows rows of one query head; each row is handled
@@ -533,6 +931,7 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
 // of up to kMergeBatch segments are loaded together, so a row pays one memory latency per batch.
 constexpr int kMergeRows = 16;
 constexpr int kMergeBatch = 8;
+constexpr int kMaxMergeSegs = 16;  // segments a launch may have (the host planner's cap)
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 template <int D>
@@ -550,46 +949,58 @@ __global__ __launch_bounds__(kMergeRows * D / 8) void prefill_combine_kernel(Pre
     const size_t prow = (size_t)hq * a.q_len + row;
     const float4* ml = reinterpret_cast<const float4*>(a.part_ml) + prow;
     const uint4* po = reinterpret_cast<const uint4*>(a.part_o) + prow * TPR + d8;
-    float M = -INFINITY;  // running max over the merged segments (log2 units)
-    float O[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    float Ls = 0.f;
-    for (int s0 = 0; s0 < n_valid; s0 += kMergeBatch) {
-        float4 e[kMergeBatch];  // (m, l, scale, -) of the segment
-        f16x8 v[kMergeBatch];   // eight dims of the segment's O / l / scale
+    // Segment s contributes 2^(m_s - M) * v_s * 2^(e_s) (M the largest m).  Split its log2 weight
+    // into an integer n_s and a fraction: the contribution's exponent is x_s = e_s + n_s, and O
+    // accumulates relative to X = max_s x_s, so the dominant contributions are scaled by about one
+    // and every term is scaled down by an exact power of two: nothing overflows, and nothing that
+    // matters to the sum is flushed, whatever the partials' magnitudes.
+    float4 e[kMaxMergeSegs];  // (m, l, exponent, -) of each segment
 #pragma unroll
-        for (int j = 0; j < kMergeBatch; ++j) {
-            if (s0 + j < n_valid) {
-                e[j] = ml[(size_t)(s0 + j) * seg_stride];
-                v[j] = __builtin_bit_cast(f16x8, po[(size_t)(s0 + j) * seg_stride * TPR]);
-            } else {
-                e[j] = make_float4(-INFINITY, 0.f, 0.f, 0.f);
-                v[j] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    for (int j = 0; j < kMaxMergeSegs; ++j)
+        e[j] = j < n_valid ? ml[(size_t)j * seg_stride] : make_float4(-INFINITY, 0.f, 0.f, 0.f);
+    float M = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kMaxMergeSegs; ++j) M = fmaxf(M, e[j].x);
+    uint4 w = {0u, 0u, 0u, 0u};
+    float Ls = 0.f;
+    if (M != -INFINITY) {
+        int n[kMaxMergeSegs];
+        int X = INT_MIN;
+#pragma unroll
+        for (int j = 0; j < kMaxMergeSegs; ++j) {
+            n[j] = (int)fmaxf(floorf(e[j].x - M), -1024.f);  // -1024 for an empty segment (m = -inf)
+            if (e[j].x != -INFINITY) X = max(X, (int)e[j].z + n[j]);
+            Ls = fmaf(__builtin_amdgcn_exp2f(e[j].x - M), e[j].y, Ls);
+        }
+        float O[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j0 = 0; j0 < kMaxMergeSegs; j0 += kMergeBatch) {
+            if (j0 >= n_valid) break;
+            f16x8 v[kMergeBatch];
+#pragma unroll
+            for (int j = 0; j < kMergeBatch; ++j)
+                v[j] = j0 + j < n_valid ? __builtin_bit_cast(f16x8, po[(size_t)(j0 + j) * seg_stride * TPR])
+                                        : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+            for (int j = 0; j < kMergeBatch; ++j) {
+                const float4& ej = e[j0 + j];
+                const float wo = ej.x == -INFINITY ? 0.f
+                                                   : ldexpf(__builtin_amdgcn_exp2f(ej.x - M - (float)n[j0 + j]),
+                                                            (int)ej.z + n[j0 + j] - X);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) O[i] = fmaf(wo, (float)v[j][i], O[i]);
             }
         }
-        float bm = M;
+        // out = O * 2^X / Ls, scaled back in one exact step after the division.
+        const float inv = Ls > 0.f ? 1.f / Ls : 0.f;
+        float r8[8];
 #pragma unroll
-        for (int j = 0; j < kMergeBatch; ++j) bm = fmaxf(bm, e[j].x);
-        if (bm == -INFINITY) continue;  // no valid key in the segments so far
-        const float corr = __builtin_amdgcn_exp2f(M - bm);  // 0 while M = -inf
-#pragma unroll
-        for (int i = 0; i < 8; ++i) O[i] *= corr;
-        Ls *= corr;
-#pragma unroll
-        for (int j = 0; j < kMergeBatch; ++j) {
-            const float wl = __builtin_amdgcn_exp2f(e[j].x - bm) * e[j].y;  // 0 for a segment past n_valid
-            const float w = wl * e[j].z;                                    // O_s = l * scale * v
-#pragma unroll
-            for (int i = 0; i < 8; ++i) O[i] = fmaf(w, (float)v[j][i], O[i]);
-            Ls += wl;
-        }
-        M = bm;
+        for (int i = 0; i < 8; ++i) r8[i] = ldexpf(O[i] * inv, X);
+        w.x = (uint32_t)f32_to_bf16_rne(r8[0]) | ((uint32_t)f32_to_bf16_rne(r8[1]) << 16);
+        w.y = (uint32_t)f32_to_bf16_rne(r8[2]) | ((uint32_t)f32_to_bf16_rne(r8[3]) << 16);
+        w.z = (uint32_t)f32_to_bf16_rne(r8[4]) | ((uint32_t)f32_to_bf16_rne(r8[5]) << 16);
+        w.w = (uint32_t)f32_to_bf16_rne(r8[6]) | ((uint32_t)f32_to_bf16_rne(r8[7]) << 16);
     }
-    const float inv = Ls > 0.f ? 1.f / Ls : 0.f;
-    uint4 w;
-    w.x = (uint32_t)f32_to_bf16_rne(O[0] * inv) | ((uint32_t)f32_to_bf16_rne(O[1] * inv) << 16);
-    w.y = (uint32_t)f32_to_bf16_rne(O[2] * inv) | ((uint32_t)f32_to_bf16_rne(O[3] * inv) << 16);
-    w.z = (uint32_t)f32_to_bf16_rne(O[4] * inv) | ((uint32_t)f32_to_bf16_rne(O[5] * inv) << 16);
-    w.w = (uint32_t)f32_to_bf16_rne(O[6] * inv) | ((uint32_t)f32_to_bf16_rne(O[7] * inv) << 16);
     *reinterpret_cast<uint4*>(a.out + prow * D + 8 * d8) = w;
     if (d8 == 0 && a.lse != nullptr) a.lse[prow] = Ls > 0.f ? (M + log2f(Ls)) * kLn2 : -INFINITY;
 }
@@ -626,10 +1037,22 @@ size_t prefill_workspace_floats(const PrefillPlan& p, int q_len, int n_q_heads, 
 }
 
 hipError_t launch_prefill_combine(int head_dim, const PrefillArgs& a, const Launch& l) {
+    if (a.n_segs > kMaxMergeSegs) return hipErrorInvalidValue;
     const dim3 grid((a.q_len + kMergeRows - 1) / kMergeRows, a.n_q_heads);
     if (head_dim == 128) return launch_kernel(prefill_combine_kernel<128>, grid, dim3(kMergeRows * 16), l, a);
     if (head_dim == 64) return launch_kernel(prefill_combine_kernel<64>, grid, dim3(kMergeRows * 8), l, a);
     return hipErrorInvalidValue;
+}
+
+hipError_t launch_prefill_rows(int head_dim, const PrefillArgs& a, const Launch& l) {
+    if ((a.q_len + kRows - 1) / kRows * (a.n_q_heads / a.n_kv_heads) > 65535) return hipErrorInvalidValue;
+    if (head_dim == 128) return launch_prefill_rows_t<128>(a, l);
+    if (head_dim == 64) return launch_prefill_rows_t<64>(a, l);
+    return hipErrorInvalidValue;
+}
+
+int prefill_shared_wgs(int q_len, int group, int n_kv_heads) {
+    return ((q_len + kRows - 1) / kRows * group + kWaves - 1) / kWaves * n_kv_heads;
 }
 
 bool prefill_supported(int head_dim, int group) {

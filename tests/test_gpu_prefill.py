@@ -98,7 +98,16 @@ def test_transaction_protocol_and_busy_start():
     check_rows(out, None, ref, None)
 
 
-def test_chunked_prefill_c5():
+def set_prefill_kernel(acc, kernel):
+    """Force the prefill decomposition: 'auto', 'shared' (GQA-shared tiles + KV segments) or 'rows'."""
+    from lara_amd import _lib
+    code = {"auto": _lib.GQA_PREFILL_KERNEL_AUTO, "shared": _lib.GQA_PREFILL_KERNEL_SHARED,
+            "rows": _lib.GQA_PREFILL_KERNEL_ROWS}[kernel]
+    _lib.check(acc._lib.gqa_set_option(acc._ctx, _lib.GQA_OPT_PREFILL_KERNEL, code), "prefill kernel")
+
+
+@pytest.mark.parametrize("kernel", ["auto", "shared"])
+def test_chunked_prefill_c5(kernel):
     """2048-token prompt in 256-token chunks against a growing cache, causal (32q/8kv, D 128)."""
     rng = np.random.default_rng(5)
     P, C = 2048, 256
@@ -106,6 +115,7 @@ def test_chunked_prefill_c5():
     k = bf16_normal(rng, (8, P, 128))
     v = bf16_normal(rng, (8, P, 128))
     with AttentionAccelerator(max_seq_len=P, max_q_len=C) as acc:
+        set_prefill_kernel(acc, kernel)
         for c in range(P // C):
             s = c * C
             print(f"[c5] chunk {c}", flush=True)
@@ -118,15 +128,18 @@ def test_chunked_prefill_c5():
 @pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (8, 8, 128), (16, 8, 128), (64, 8, 128), (64, 4, 128),
                                       (8, 2, 64), (16, 16, 64), (32, 4, 64), (32, 2, 64)])
 @pytest.mark.parametrize("causal", [True, False])
-def test_prefill_shapes_ragged(hq, hkv, d, causal):
-    """Every compiled (head_dim, group), ragged q_len / kv_len, absolute position bases."""
+@pytest.mark.parametrize("kernel", ["rows", "shared"])
+def test_prefill_shapes_ragged(hq, hkv, d, causal, kernel):
+    """Every compiled (head_dim, group), ragged q_len / kv_len, absolute position bases, both
+    decompositions."""
     rng = np.random.default_rng(hq * 7 + hkv * 3 + d + causal)
     q_len, kv_len, qb, kb = 77, 333, 300, 40
-    print(f"[prefill] hq={hq} hkv={hkv} d={d} causal={causal}", flush=True)
+    print(f"[prefill] hq={hq} hkv={hkv} d={d} causal={causal} kernel={kernel}", flush=True)
     q = bf16_normal(rng, (hq, q_len, d))
     k = bf16_normal(rng, (hkv, kv_len, d))
     v = bf16_normal(rng, (hkv, kv_len, d))
     with AttentionAccelerator(n_q_heads=hq, n_kv_heads=hkv, head_dim=d, max_seq_len=kv_len, max_q_len=q_len) as acc:
+        set_prefill_kernel(acc, kernel)
         acc.load_kv(k, v)
         out, lse = acc.prefill_chunk(q, q_pos_base=qb, kv_len=kv_len, kv_pos_base=kb, causal=causal,
                                      return_lse=True)
@@ -181,7 +194,8 @@ def test_single_row_prefill_matches_decode():
 
 
 @pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (16, 2, 64)])
-def test_fused_chunk_append_matches_load_then_prefill(hq, hkv, d):
+@pytest.mark.parametrize("kernel", ["rows", "shared"])
+def test_fused_chunk_append_matches_load_then_prefill(hq, hkv, d, kernel):
     """prefill_chunk with k_rows/v_rows = load_kv + prefill_chunk, bit for bit, chunk by chunk."""
     rng = np.random.default_rng(300 + hq + d)
     P, C = 700, 192  # the last chunk is partial
@@ -190,6 +204,8 @@ def test_fused_chunk_append_matches_load_then_prefill(hq, hkv, d):
     v = bf16_normal(rng, (hkv, P, d))
     kw = dict(n_q_heads=hq, n_kv_heads=hkv, head_dim=d, max_seq_len=P, max_q_len=C)
     with AttentionAccelerator(**kw) as fused, AttentionAccelerator(**kw) as split:
+        set_prefill_kernel(fused, kernel)
+        set_prefill_kernel(split, kernel)
         for s in range(0, P, C):
             e = min(P, s + C)
             print(f"[fused chunk] {s}..{e}", flush=True)
@@ -222,12 +238,13 @@ def test_prefill_segmentation_invariance(wgs):
     check_rows(out, lse, ref, ref_lse)
 
 
-@pytest.mark.parametrize("v_scale", [1e30, 1e-30, "mixed"])
+@pytest.mark.parametrize("v_scale", [1e30, 1e-30, 1e-39, "mixed", "weighted"])
 def test_segment_partials_at_extreme_magnitudes(v_scale):
     """KV segments hand their rows to the merge as fp16 O / l divided by the row's largest
     |O / l|: outputs of very large or very small magnitude, and rows mixing both, keep the
     2-ulp bound with many segments."""
-    rng = np.random.default_rng(500 if v_scale == "mixed" else int(np.log10(v_scale)) + 600)
+    seeds = {"mixed": 500, "weighted": 501}
+    rng = np.random.default_rng(seeds.get(v_scale) or int(np.log10(v_scale)) + 600)
     q_len, kv_len = 128, 1024
     q = bf16_normal(rng, (32, q_len, 128))
     k = bf16_normal(rng, (8, kv_len, 128))
@@ -235,13 +252,32 @@ def test_segment_partials_at_extreme_magnitudes(v_scale):
         v32 = rng.standard_normal((8, kv_len, 128), dtype=np.float32)
         v32[:, ::7] *= np.float32(1e20)  # every 7th key's row dominates the rows that see it
         v = orc.fp32_to_bf16_u16(v32)
+    elif v_scale == "weighted":
+        # The first 256 keys carry V ~ 1e30 but scores far below the rest (scores 0 against about
+        # 130: weight ~ e^-130 after the softmax), the later keys V ~ 1e-10: the segments with the
+        # largest |O| contribute almost nothing, and must not flush the segments that do.
+        k32 = orc.bf16_u16_to_fp32(k).copy()
+        k32[:, :256] = 0.0
+        k = orc.fp32_to_bf16_u16(k32)
+        q32 = np.abs(orc.bf16_u16_to_fp32(q)) + np.float32(1.0)
+        q = orc.fp32_to_bf16_u16(q32)
+        k32 = orc.bf16_u16_to_fp32(k).copy()
+        k32[:, 256:] = np.abs(k32[:, 256:]) * np.float32(8.0)  # scores of the later keys >> 0
+        k = orc.fp32_to_bf16_u16(k32)
+        v32 = rng.standard_normal((8, kv_len, 128), dtype=np.float32) * np.float32(1e-10)
+        v32[:, :256] = rng.standard_normal((8, 256, 128), dtype=np.float32) * np.float32(1e30)
+        v = orc.fp32_to_bf16_u16(v32)
     else:
         v = bf16_normal(rng, (8, kv_len, 128), v_scale)
-    with AttentionAccelerator(max_seq_len=kv_len, max_q_len=q_len) as acc:
-        from lara_amd import _lib
-        _lib.check(acc._lib.gqa_set_option(acc._ctx, _lib.GQA_OPT_PREFILL_WGS, 1024), "prefill wgs")
-        acc.load_kv(k, v)
-        out, lse = acc.prefill_chunk(q, q_pos_base=kv_len - q_len, kv_len=kv_len, return_lse=True)
+    outs = []
+    for wgs in (1024, 1):  # many KV segments, then one (no partials)
+        with AttentionAccelerator(max_seq_len=kv_len, max_q_len=q_len) as acc:
+            from lara_amd import _lib
+            _lib.check(acc._lib.gqa_set_option(acc._ctx, _lib.GQA_OPT_PREFILL_WGS, wgs), "prefill wgs")
+            acc.load_kv(k, v)
+            outs.append(acc.prefill_chunk(q, q_pos_base=kv_len - q_len, kv_len=kv_len, return_lse=True))
+    out, lse = outs[0]
     assert np.all(np.isfinite(drv.bf16_u16_to_fp32(out)))
     ref, ref_lse = oracle_for(q, k, v, causal=True, q_pos_base=kv_len - q_len)
     check_rows(out, lse, ref, ref_lse)
+    check_rows(outs[1][0], outs[1][1], ref, ref_lse)
