@@ -560,25 +560,25 @@ __device__ __forceinline__ void lgkm_wait1(T& a) {
     asm volatile("s_waitcnt %1" : "+v"(a) : "i"(0xF | (0x3 << 14) | (0x7 << 4) | (N << 8)));
 }
 
-// NW waves per work-group take the row block's key blocks in turn; NS: stages of each wave's ring.
-template <int D, bool PAGED, int NW, int NS>
+// NW waves per work-group take the row block's key blocks in turn.
+template <int D, bool PAGED, int NW>
 __global__ __launch_bounds__(NW * 64) void prefill_rows_kernel(PrefillArgs a) {
     constexpr int kRowWaves = NW;
-    constexpr int kRowStages = NS;
-    static_assert(NS == 1 || NS == 2, "ring depth");
     constexpr int NCH = D / 8;         // 16-byte chunks per K/V row
     constexpr int KSTEPS = D / 16;     // QK k-steps
     constexpr int MT = D / 32;         // PV result tiles (32 dims each)
     constexpr int TILE = kRowBN * NCH; // 16-byte chunks per K (or V) tile
+    constexpr int KA = KSTEPS > 3 ? 3 : KSTEPS - 1;  // K fragment reads in flight ahead of their MFMA
+    constexpr int VA = 2;                            // V^T steps read ahead of their MFMA
     constexpr int DMA = TILE / 64;     // direct-to-LDS loads per lane per tile
-    constexpr int LPB = 2 * DMA;       // per block (K and V)
     static_assert(DMA >= 1 && DMA * 64 == TILE, "tile shape");
-    static_assert(D * kRows * 4 <= kRowStages * 2 * TILE * 16, "a wave's O^T fits its ring");
+    static_assert(D * kRows * 4 <= 2 * TILE * 16, "a wave's O^T fits its tiles");
 
-    // Per wave: its ring of [stage][K, V] tiles, reused for the wave's O^T after the loop, and its
-    // rows' (m, l).
-    __shared__ __attribute__((aligned(16))) u32x4 lds[kRowWaves][kRowStages][2][TILE];
+    // Per wave: one K and one V tile, reused for the wave's O^T after the loop, and its rows' (m, l);
+    // the row block's Q, loaded once for all waves.
+    __shared__ __attribute__((aligned(16))) u32x4 lds[kRowWaves][2][TILE];
     __shared__ float lds_ml[kRowWaves][2][kRows];
+    __shared__ __attribute__((aligned(16))) u32x4 lds_q[TILE];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -610,9 +610,11 @@ __global__ __launch_bounds__(NW * 64) void prefill_rows_kernel(PrefillArgs a) {
     const u32x4* vn = has_new ? reinterpret_cast<const u32x4*>(a.v_new) + (size_t)h * a.n_new * NCH : nullptr;
     const u32x4* zero = reinterpret_cast<const u32x4*>(a.zero_row);
 
-    // Direct-to-LDS staging of the block at key j0 into this wave's stage st: load instruction i
-    // fills slots i*64 + lane, and each lane loads the 16-byte chunk the swizzled layout wants in its
-    // slot: byte offset koff[i] (K) / voff[i] (V) from the block's first row.  A block whose rows all
+    // Direct-to-LDS staging of the K (kv = 0) or V (kv = 1) tile of the block at key j0: load
+    // instruction i fills slots i*64 + lane, and each lane loads the 16-byte chunk the swizzled layout
+    // wants in its slot: byte offset koff[i] (K) / voff[i] (V) from the block's first row.  The K tile
+    // of the next block is loaded as soon as S^T has read this one, and the V tile as soon as PV has,
+    // so each load has the rest of a block's work to land behind.  A block whose rows all
     // come from one contiguous run -- the cache, or the rows this launch appends -- takes a
     // wave-uniform base and these fixed offsets; a block that straddles the appended rows or ends
     // past kv_len (zero row there: stale words may be NaN) picks each lane's source.
@@ -625,7 +627,7 @@ __global__ __launch_bounds__(NW * 64) void prefill_rows_kernel(PrefillArgs a) {
         voff[i] = 16u * (uint32_t)(key * NCH + ((slot % NCH) ^ v_swz<D>(key)));
     }
     const int new_end = has_new ? a.new_begin + a.n_new : 0;
-    auto issue = [&](int j0, int st) {
+    auto issue = [&](int j0, int kv) {
         // Row j0's K and V, or nullptr where the block's rows do not share one source.
         const u32x4* krow = nullptr;
         const u32x4* vrow = nullptr;
@@ -645,12 +647,9 @@ __global__ __launch_bounds__(NW * 64) void prefill_rows_kernel(PrefillArgs a) {
             }
         }
         if (krow != nullptr) {
-            const uint64_t kb = uniform_address(krow), vb = uniform_address(vrow);
+            const uint64_t base = uniform_address(kv ? vrow : krow);
 #pragma unroll
-            for (int i = 0; i < DMA; ++i) {
-                dma16_sbase(kb, koff[i], lds_addr(&lds[wave][st][0][i * 64]));
-                dma16_sbase(vb, voff[i], lds_addr(&lds[wave][st][1][i * 64]));
-            }
+            for (int i = 0; i < DMA; ++i) dma16_sbase(base, kv ? voff[i] : koff[i], lds_addr(&lds[wave][kv][i * 64]));
             return;
         }
         int64_t pr0 = 0;  // paged: the block's page row (-1: unmapped, zero rows)
@@ -661,40 +660,33 @@ __global__ __launch_bounds__(NW * 64) void prefill_rows_kernel(PrefillArgs a) {
             const int row_idx = j0 + rel;
             const uint32_t kc_off = koff[i] - 16u * (uint32_t)(rel * NCH);  // chunk offset within the row
             const uint32_t vc_off = voff[i] - 16u * (uint32_t)(rel * NCH);
-            const u32x4* sk;
-            const u32x4* sv;
+            const u32x4* src;
             const unsigned r_new = (unsigned)(row_idx - a.new_begin);
             if (row_idx >= a.kv_len || (PAGED && pr0 < 0)) {
-                sk = zero;
-                sv = zero;
+                src = zero;
             } else if (has_new && r_new < (unsigned)a.n_new) {
-                sk = kn + (size_t)r_new * NCH;
-                sv = vn + (size_t)r_new * NCH;
+                src = (kv ? vn : kn) + (size_t)r_new * NCH;
             } else if constexpr (PAGED) {
-                sk = kg + (size_t)(pr0 + rel) * NCH;
-                sv = vg + (size_t)(pr0 + rel) * NCH;
+                src = (kv ? vg : kg) + (size_t)(pr0 + rel) * NCH;
             } else {
-                sk = kg + (size_t)row_idx * NCH;
-                sv = vg + (size_t)row_idx * NCH;
+                src = (kv ? vg : kg) + (size_t)row_idx * NCH;
             }
-            dma16(reinterpret_cast<const uint8_t*>(sk) + kc_off, lds_addr(&lds[wave][st][0][i * 64]));
-            dma16(reinterpret_cast<const uint8_t*>(sv) + vc_off, lds_addr(&lds[wave][st][1][i * 64]));
+            dma16(reinterpret_cast<const uint8_t*>(src) + (kv ? vc_off : kc_off), lds_addr(&lds[wave][kv][i * 64]));
         }
     };
 
-    // Operand addresses in stage 0 of this wave's ring (a stage adds stage_bytes).
-    constexpr uint32_t stage_bytes = 2 * TILE * 16;
+    // Operand addresses in this wave's tiles.
     uint32_t kaddr[KSTEPS];
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks)
-        kaddr[ks] = lds_addr(&lds[wave][0][0][0]) + 16u * (uint32_t)(col * NCH + ((2 * ks + half) ^ k_swz<NCH>(col)));
+        kaddr[ks] = lds_addr(&lds[wave][0][0]) + 16u * (uint32_t)(col * NCH + ((2 * ks + half) ^ k_swz<NCH>(col)));
     uint32_t vaddr[MT];
     {
         const int key_off = (lane & 15) >> 2;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
             const int dim = mt * 32 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-            vaddr[mt] = lds_addr(&lds[wave][0][1][0]) + (uint32_t)((key_off + 4 * half) * (D * 2) +
+            vaddr[mt] = lds_addr(&lds[wave][1][0]) + (uint32_t)((key_off + 4 * half) * (D * 2) +
                                                                    (((dim >> 3) ^ v_swz<D>(key_off)) << 4) +
                                                                    (((dim >> 2) & 1) << 3));
         }
@@ -712,14 +704,21 @@ __global__ __launch_bounds__(NW * 64) void prefill_rows_kernel(PrefillArgs a) {
 
     // Q^T operand (row `row`, dims 16*ks + 8*half .. +7), the wave's first two blocks and this
     // work-group's share of the appended rows are all in flight before the first wait.
-    u32x4 qb[KSTEPS];
-    {
-        const u32x4* qp = reinterpret_cast<const u32x4*>(a.q + ((size_t)hq * a.q_len + row) * D);
-#pragma unroll
-        for (int ks = 0; ks < KSTEPS; ++ks) qb[ks] = row_ok ? qp[2 * ks + half] : u32x4{0u, 0u, 0u, 0u};
+    // Q of the row block goes to LDS once (the K tile's swizzled layout, rows past q_len from the zero
+    // row), each lane one 16-byte chunk, instead of every wave loading all 32 rows.
+    for (int base = wave * 64; base < TILE; base += kRowWaves * 64) {  // base is wave-uniform
+        const int slot = base + lane;
+        const int qrow = slot / NCH;
+        const int chunk = (slot % NCH) ^ k_swz<NCH>(qrow);
+        const u32x4* src = rb * kRows + qrow < a.q_len
+                               ? reinterpret_cast<const u32x4*>(a.q + ((size_t)hq * a.q_len + rb * kRows + qrow) * D) + chunk
+                               : zero + chunk;
+        dma16(src, lds_addr(&lds_q[base]));
     }
-    if (my_blocks > 0) issue(wave * kRowBN, 0);
-    if (kRowStages > 1 && my_blocks > 1) issue((wave + kRowWaves) * kRowBN, kRowStages - 1);
+    if (my_blocks > 0) {
+        issue(wave * kRowBN, 0);
+        issue(wave * kRowBN, 1);
+    }
     // Appended rows of kv head h go to the cache in equal shares over the kv head's work-groups;
     // blocks that hold them read k_new/v_new, so no work-group waits for the copy.  A thread's first
     // word is loaded with Q and the first blocks and stored after the wait below (the loop's own
@@ -741,6 +740,15 @@ __global__ __launch_bounds__(NW * 64) void prefill_rows_kernel(PrefillArgs a) {
         app_v = vn[app_first];
     }
     wait_vmcnt<0>();  // Q, the first blocks and the first appended word
+    __syncthreads();  // every wave's share of Q is in LDS
+    u32x4 qb[KSTEPS];  // Q^T operand: row `row`, dims 16*ks + 8*half .. +7
+    {
+        const uint32_t qbase = lds_addr(&lds_q[0]);
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks)
+            qb[ks] = lds_read128(qbase + 16u * (uint32_t)(col * NCH + ((2 * ks + half) ^ k_swz<NCH>(col))));
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
     if (app_first < app_words) {
         const int64_t dst = app_dst(app_first);
         if (dst >= 0) {
@@ -759,31 +767,32 @@ __global__ __launch_bounds__(NW * 64) void prefill_rows_kernel(PrefillArgs a) {
         // first of those waits (block 1) wait for them as well.
     }
 
+    // vm operations in flight enter the loop in the order K(t), V(t): K(t) (then K(t+1)) is issued
+    // after S^T(t-1) (S^T(t)), V(t) after PV(t-1).
     for (int t = 0; t < my_blocks; ++t) {
-        const int st = t % kRowStages;
         const int j0 = (wave + t * kRowWaves) * kRowBN;
-        if (t >= 1) {  // block t landed once at most the later blocks' loads (a two-stage ring: t+1) remain
-            if (kRowStages > 1 && t + 1 < my_blocks) wait_vmcnt<LPB>(); else wait_vmcnt<0>();
-        }
-        const uint32_t stage_off = (uint32_t)st * stage_bytes;
+        const bool more = t + 1 < my_blocks;
+        if (t >= 1) wait_vmcnt<DMA>();  // K(t) landed; V(t) may still be in flight
 
-        // ---- S^T = K . Q^T (raw scores): one 32x32 tile, K fragments read one step ahead ----
+        // ---- S^T = K . Q^T (raw scores): one 32x32 tile, K fragments read KA steps ahead ----
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         f32x16 sacc;
 #pragma unroll
         for (int i = 0; i < 16; ++i) sacc[i] = 0.f;
         u32x4 kf[KSTEPS];
-        kf[0] = lds_read128(kaddr[0] + stage_off);
-#pragma unroll
-        for (int ks = 0; ks < KSTEPS; ++ks) {
-            if (ks + 1 < KSTEPS) {
-                kf[ks + 1] = lds_read128(kaddr[ks + 1] + stage_off);
-                lgkm_wait1<1>(kf[ks]);
+        static_for<KA>([&](auto c) { kf[decltype(c)::value] = lds_read128(kaddr[decltype(c)::value]); });
+        static_for<KSTEPS>([&](auto c) {
+            constexpr int ks = decltype(c)::value;
+            if constexpr (ks + KA < KSTEPS) {
+                kf[ks + KA] = lds_read128(kaddr[ks + KA]);
+                lgkm_wait1<KA>(kf[ks]);  // reads complete in order: at most the KA later ones remain
             } else {
-                lgkm_wait1<0>(kf[ks]);
+                lgkm_wait1<KSTEPS - 1 - ks>(kf[ks]);
             }
             sacc = mfma32(kf[ks], qb[ks], sacc);
-        }
+        });
+        // Every read of the K tile is complete (lgkmcnt(0) above): it takes the next block's K.
+        if (more) issue(j0 + kRowWaves * kRowBN, 0);
 
         // ---- online softmax (log2 domain, scale folded into the exponent) ----
         const bool need_mask =
@@ -831,38 +840,48 @@ __global__ __launch_bounds__(NW * 64) void prefill_rows_kernel(PrefillArgs a) {
         l_lane += psum;
 
         // ---- O^T += V^T . P^T, transposing V reads one step ahead ----
+        if (t >= 1) {  // V(t) landed; K(t+1) may still be in flight
+            if (more) wait_vmcnt<DMA>(); else wait_vmcnt<0>();
+        }
         constexpr int PV = MT * 2;
         u32x2 vf[PV][2];
         auto read_v = [&](auto step_c) {
             constexpr int i = decltype(step_c)::value;
             constexpr int kb = 16 * (i & 1);  // step's key base within the block (half adds 4)
-            const uint32_t va = vaddr[i >> 1] + stage_off;
+            const uint32_t va = vaddr[i >> 1];
             vf[i][0] = lds_read_tr64<kb * (D * 2)>(va);
             vf[i][1] = lds_read_tr64<(kb + 8) * (D * 2)>(va);
         };
-        read_v(std::integral_constant<int, 0>{});
+        static_for<VA>([&](auto c) { read_v(c); });
         static_for<PV>([&](auto step_c) {
             constexpr int i = decltype(step_c)::value;
-            if constexpr (i + 1 < PV) {
-                read_v(std::integral_constant<int, i + 1>{});
-                lgkm_wait<2>(vf[i][0], vf[i][1]);
+            if constexpr (i + VA < PV) {
+                read_v(std::integral_constant<int, i + VA>{});
+                lgkm_wait<2 * VA>(vf[i][0], vf[i][1]);  // two reads per step
             } else {
-                lgkm_wait<0>(vf[i][0], vf[i][1]);
+                lgkm_wait<2 * (PV - 1 - i)>(vf[i][0], vf[i][1]);
             }
             const u32x4 vw = {vf[i][0].x, vf[i][0].y, vf[i][1].x, vf[i][1].y};
             o[i >> 1] = mfma32(vw, pb[i & 1], o[i >> 1]);
         });
-        // Every read of stage st is complete (lgkmcnt(0) above): it takes block t + NS.
-        if (t + kRowStages < my_blocks) issue((wave + (t + kRowStages) * kRowWaves) * kRowBN, st);
+        // Every read of the V tile is complete (lgkmcnt(0) above): it takes the next block's V.
+        if (more) issue(j0 + kRowWaves * kRowBN, 1);
     }
 
     // ---- merge the waves: each writes (O^T [D][32 rows], m, l) to its own ring (no DMA pending) ----
+    // O^T goes to LDS row-major, [32 rows][D] fp32, as 16-byte granules (four dims) XOR-swizzled by
+    // the row so that neither the writes here nor the reads below conflict on banks.
     const float l_row = l_lane + half_swap(l_lane, half);
-    float* mo = reinterpret_cast<float*>(&lds[wave][0][0][0]);
+    constexpr int GR = D / 4;  // granules per row
+    float4* mo = reinterpret_cast<float4*>(&lds[wave][0][0]);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) mo[(mt * 32 + 8 * (i >> 2) + 4 * half + (i & 3)) * kRows + col] = o[mt][i];
+        for (int i4 = 0; i4 < 4; ++i4) {
+            const int gran = 8 * mt + 2 * i4 + half;  // dims 4*gran .. +3 = mt*32 + 8*i4 + 4*half + 0..3
+            mo[col * GR + (gran ^ (col % GR))] =
+                make_float4(o[mt][4 * i4], o[mt][4 * i4 + 1], o[mt][4 * i4 + 2], o[mt][4 * i4 + 3]);
+        }
     if (half == 0) {
         lds_ml[wave][0][col] = m_run;
         lds_ml[wave][1][col] = l_row;
@@ -889,15 +908,24 @@ __global__ __launch_bounds__(NW * 64) void prefill_rows_kernel(PrefillArgs a) {
     uint16_t* orow = a.out + ((size_t)hq * a.q_len + out_row) * D + dg * DPT;
 #pragma unroll
     for (int d8 = 0; d8 < DPT; d8 += 8) {
-        float v[8];
+        float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        const int g0 = (dg * DPT + d8) / 4;  // first of the two granules of these eight dims
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            float acc = 0.f;
-#pragma unroll
-            for (int w = 0; w < kRowWaves; ++w)
-                acc = fmaf(wt[w], reinterpret_cast<const float*>(&lds[w][0][0][0])[(dg * DPT + d8 + k) * kRows + r], acc);
-            v[k] = acc * inv;
+        for (int w = 0; w < kRowWaves; ++w) {
+            const float4* wo = reinterpret_cast<const float4*>(&lds[w][0][0]) + r * GR;
+            const float4 x0 = wo[g0 ^ (r % GR)];
+            const float4 x1 = wo[(g0 + 1) ^ (r % GR)];
+            v[0] = fmaf(wt[w], x0.x, v[0]);
+            v[1] = fmaf(wt[w], x0.y, v[1]);
+            v[2] = fmaf(wt[w], x0.z, v[2]);
+            v[3] = fmaf(wt[w], x0.w, v[3]);
+            v[4] = fmaf(wt[w], x1.x, v[4]);
+            v[5] = fmaf(wt[w], x1.y, v[5]);
+            v[6] = fmaf(wt[w], x1.z, v[6]);
+            v[7] = fmaf(wt[w], x1.w, v[7]);
         }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] *= inv;
         uint4 wv;
         wv.x = (uint32_t)f32_to_bf16_rne(v[0]) | ((uint32_t)f32_to_bf16_rne(v[1]) << 16);
         wv.y = (uint32_t)f32_to_bf16_rne(v[2]) | ((uint32_t)f32_to_bf16_rne(v[3]) << 16);
@@ -910,9 +938,8 @@ __global__ __launch_bounds__(NW * 64) void prefill_rows_kernel(PrefillArgs a) {
 }
 
 // Row-block kernel shape: 8 waves (two per SIMD: one wave's MFMAs run while the other waits on
-// LDS or loads) with single-stage rings, 128 KiB of LDS at D = 128.
+// LDS or loads), one K and one V tile each: 128 KiB of LDS at D = 128.
 constexpr int kRowWaves = 8;
-constexpr int kRowStages = 1;
 
 template <int D>
 hipError_t launch_prefill_rows_t(const PrefillArgs& a, const Launch& l) {
@@ -920,8 +947,8 @@ hipError_t launch_prefill_rows_t(const PrefillArgs& a, const Launch& l) {
     const int G = a.n_q_heads / a.n_kv_heads;
     dim3 grid(a.n_kv_heads, G * n_rb);
     if (a.block_table != nullptr)
-        return launch_kernel(prefill_rows_kernel<D, true, kRowWaves, kRowStages>, grid, dim3(kRowWaves * 64), l, a);
-    return launch_kernel(prefill_rows_kernel<D, false, kRowWaves, kRowStages>, grid, dim3(kRowWaves * 64), l, a);
+        return launch_kernel(prefill_rows_kernel<D, true, kRowWaves>, grid, dim3(kRowWaves * 64), l, a);
+    return launch_kernel(prefill_rows_kernel<D, false, kRowWaves>, grid, dim3(kRowWaves * 64), l, a);
 }
 
 // Merge of a row's KV segments.  Segment s holds keys [s*seg_len, (s+1)*seg_len); a row
