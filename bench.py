@@ -294,11 +294,11 @@ PAGED_SUFFIX = "-paged"  # a decode workload over a paged cache (64-row pages un
 PAGE_ROWS = 64
 
 
-DECODE_MERGE = {"fused": 0, "launch": 1}  # GQA_DECODE_MERGE_FUSED / _LAUNCH
+DECODE_MERGE = {"auto": 0, "launch": 1, "fused": 2}  # GQA_DECODE_MERGE_AUTO / _LAUNCH / _FUSED
 
 
 def measure(name: str, steps: int, warmup: int, chunk: int = 0, page_rows: int = PAGE_ROWS,
-            merge: str = "fused") -> dict:
+            merge: str = "auto") -> dict:
     from lara_amd.benchmark import HBM_PEAK_GBPS, WORKLOADS, decode_kernel_bytes, decode_step_bytes
 
     paged = name.endswith(PAGED_SUFFIX)
@@ -1024,8 +1024,9 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--workload", default="decode-b64-ctx8192", choices=sorted(WORKLOAD_NAMES))
     parser.add_argument("--chunk", type=int, default=0, help="keys per split-KV work-group (0 = auto)")
-    parser.add_argument("--decode-merge", default="fused", choices=sorted(DECODE_MERGE),
-                        help="split merge of the decode: in the decode launch (fused) or a second launch")
+    parser.add_argument("--decode-merge", default="auto", choices=sorted(DECODE_MERGE),
+                        help="split merge of the decode: in the decode launch (fused), a second launch, or auto "
+                             "(fused while the split grid fits one dispatch round)")
     parser.add_argument("--page-rows", type=int, default=PAGE_ROWS,
                         help="rows per page of the paged-cache workloads (power of two, >= 64)")
     parser.add_argument("--prefill-wgs", type=int, default=0,

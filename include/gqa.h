@@ -85,11 +85,15 @@ extern "C" {
 #define GQA_PREFILL_KERNEL_SHARED 1
 #define GQA_PREFILL_KERNEL_ROWS   2
 
-/* Split merge of the decode (GQA_OPT_DECODE_MERGE).  FUSED (default): the last split of a (sequence,
- * kv head) to finish merges the others' partials inside the decode launch (agent-scope atomics and a
- * per-unit arrival counter; one launch per step).  LAUNCH: a second, log-sum-exp merge launch. */
-#define GQA_DECODE_MERGE_FUSED  0
+/* Split merge of the decode (GQA_OPT_DECODE_MERGE).  FUSED: the last split of a (sequence, kv head) to
+ * finish merges the others' partials inside the decode launch (agent-scope atomics and a per-unit
+ * arrival counter; one launch per step).  LAUNCH: a second, log-sum-exp merge launch.  AUTO (default):
+ * FUSED while the split grid (sequences x kv heads x splits) is at most the GPU's CU count -- every
+ * split ends with an L2 write-back of its XCD, which larger grids pay for many times over -- else
+ * LAUNCH. */
+#define GQA_DECODE_MERGE_AUTO   0
 #define GQA_DECODE_MERGE_LAUNCH 1
+#define GQA_DECODE_MERGE_FUSED  2
 
 /* Numerics of the attention kernels (GQA_OPT_NUMERICS).
  * EXACT: fp32 accumulation, exact exp, exact divide -- within 2 bf16 ulp of exact attention.

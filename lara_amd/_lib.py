@@ -50,8 +50,9 @@ GQA_OPT_PROFILE = 2
 GQA_OPT_PREFILL_WGS = 3
 GQA_OPT_NUMERICS = 4
 GQA_OPT_DECODE_MERGE = 5
-GQA_DECODE_MERGE_FUSED = 0
+GQA_DECODE_MERGE_AUTO = 0
 GQA_DECODE_MERGE_LAUNCH = 1
+GQA_DECODE_MERGE_FUSED = 2
 GQA_OPT_PREFILL_KERNEL = 6
 GQA_PREFILL_KERNEL_AUTO = 0
 GQA_PREFILL_KERNEL_SHARED = 1

@@ -63,7 +63,7 @@ struct gqa_ctx {
     float* part_o = nullptr;
     float* part_ml = nullptr;
     int32_t* arrivals = nullptr;  // [B*H_kv] split arrival counters of the fused merge (zero between launches)
-    int decode_merge = GQA_DECODE_MERGE_FUSED;
+    int decode_merge = GQA_DECODE_MERGE_AUTO;
     int prefill_kernel = GQA_PREFILL_KERNEL_AUTO;
     float* pre_ws = nullptr;     // prefill KV-segment partials (O, then (m, l))
     uint16_t* zero_row = nullptr;  // one zero K/V row: the prefill source of rows past kv_len
@@ -186,6 +186,14 @@ int plan_chunk(int batch, int n_kv_heads, int group, int n_cu, int max_len) {
     return (even + quantum - 1) / quantum * quantum;
 }
 
+// Whether the last split to arrive merges a sequence's splits inside the decode launch.  Each split
+// then ends with an agent-scope release (an L2 write-back of its XCD), which pays for itself only
+// while the split grid fits one dispatch round of the GPU; AUTO fuses up to that size.
+bool fuse_merge(int option, int units, int max_splits, int n_cu) {
+    if (max_splits <= 1 || option == GQA_DECODE_MERGE_LAUNCH) return false;
+    return option == GQA_DECODE_MERGE_FUSED || (int64_t)units * max_splits <= n_cu;
+}
+
 int choose_chunk(const gqa_ctx* c, int max_len) {
     if (c->chunk_opt > 0) return c->chunk_opt;
     return plan_chunk(c->cfg.batch, c->cfg.n_kv_heads, c->group, c->n_cu, max_len);
@@ -254,7 +262,8 @@ int run_decode(gqa_ctx* c, const void* q, const int32_t* lens, const void* k_new
     a.max_pages = c->max_pages;
     a.zero_row = c->zero_row;
     a.longest_first = c->cfg.batch > 1;
-    a.arrivals = c->decode_merge == GQA_DECODE_MERGE_FUSED ? c->arrivals : nullptr;
+    a.arrivals = fuse_merge(c->decode_merge, c->cfg.batch * c->cfg.n_kv_heads, max_splits, c->n_cu) ? c->arrivals
+                                                                                                      : nullptr;
     HIP_TRY(launch_decode(c->cfg.head_dim, c->group, a, timed(c, GQA_TIMER_DECODE, s)));
     if (max_splits > 1 && a.arrivals == nullptr)
         HIP_TRY(launch_combine(c->cfg.head_dim, c->group, a, timed(c, GQA_TIMER_COMBINE, s)));
@@ -931,7 +940,8 @@ int gqa_set_option(gqa_ctx* c, int32_t option, int64_t value) {
             c->prefill_kernel = (int)value;
             return GQA_OK;
         case GQA_OPT_DECODE_MERGE:
-            if (value != GQA_DECODE_MERGE_FUSED && value != GQA_DECODE_MERGE_LAUNCH) return GQA_ERR_RANGE;
+            if (value != GQA_DECODE_MERGE_AUTO && value != GQA_DECODE_MERGE_FUSED && value != GQA_DECODE_MERGE_LAUNCH)
+                return GQA_ERR_RANGE;
             c->decode_merge = (int)value;
             return GQA_OK;
         case GQA_OPT_NUMERICS:
@@ -1284,8 +1294,12 @@ int gqa_decode_append_noalloc(const gqa_config* cfg, void* k_cache, void* v_cach
     a.lse = lse;
     a.zero_row = dev->zero;
     a.longest_first = k.batch > 1;
-    // The same merge as the context entry point's default: fused when the counters cover the units.
-    a.arrivals = (size_t)k.batch * k.n_kv_heads <= (size_t)kNoAllocCounters ? dev->arrivals : nullptr;
+    // The same merge as the context entry point's default (GQA_DECODE_MERGE_AUTO), when the counters
+    // cover the units.
+    const int units = k.batch * k.n_kv_heads;
+    a.arrivals = units <= kNoAllocCounters && fuse_merge(GQA_DECODE_MERGE_AUTO, units, max_splits, dev->n_cu)
+                     ? dev->arrivals
+                     : nullptr;
     Launch l;
     l.stream = (hipStream_t)stream;
     HIP_TRY(launch_decode(k.head_dim, group, a, l));

@@ -29,12 +29,13 @@ def test_full_validation_run_passes(tmp_path):
     assert proc.returncode == 0
     manifest = json.loads((out / "run_manifest.json").read_text())
     assert manifest["status"] == "PASS"
-    assert [s["kind"] for s in manifest["stages"]] == ["init", "functional", "performance"]
+    assert [s["kind"] for s in manifest["stages"]] == ["probe", "functional", "performance"]
     consolidated = json.loads((out / "consolidated_results.json").read_text())
     n = len(list(CASES.glob("case_*.npz")))
+    assert consolidated["overall_status"] == "PASS"
     assert consolidated["functional"]["board"]["passed"] == n
     perf = consolidated["performance"]["cpu1"]
-    assert perf["passed"] == perf["total"] == n and not perf["benchmark_errors"]
+    assert perf["passed"] == perf["total"] == perf["expected"] == n
     report = json.loads((out / "performance" / "cpu1" / "performance.json").read_text())
     assert all(r["correctness"]["gpu_bit_exact_expected"] and r["correctness"]["gpu_bit_exact_kv260_model"]
                for r in report["results"])

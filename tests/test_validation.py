@@ -1,9 +1,9 @@
 """The full-validation orchestrator's host logic (lara_amd/validation.py) on the CPU.
 
-Mirrors what sw/run_board_full_validation.py guarantees: stages run in their own process
-group with their output logged, a stage that overruns is reaped with its children, the run
-directory must be empty, pass counts need every selected case, and a failing stage leaves a
-manifest that says FAIL and why.
+What sw/run_board_full_validation.py guarantees, checked against the step executor: a step's
+output is logged as it arrives, a step past its deadline is ended with its whole session, the run
+directory must be new or empty, pass counts come from the artifacts and need every selected case,
+and a failing step leaves a manifest that says FAIL, why, and the provenance hashes.
 """
 import json
 import os
@@ -19,11 +19,11 @@ from lara_amd import validation as val
 CASES = Path(__file__).resolve().parent / "golden" / "board_cases"
 
 
-def test_stage_logs_output_and_status(tmp_path):
-    ok = val.run_stage([sys.executable, "-c", "print('alpha'); print('beta')"], tmp_path / "a.log")
+def test_execute_logs_output_and_status(tmp_path):
+    ok = val.execute([sys.executable, "-c", "print('alpha'); print('beta')"], tmp_path / "a.log", echo=False)
     assert ok["status"] == "PASS" and ok["return_code"] == 0 and not ok["timed_out"]
     assert (tmp_path / "a.log").read_text().splitlines() == ["alpha", "beta"]
-    bad = val.run_stage([sys.executable, "-c", "import sys; print('x'); sys.exit(3)"], tmp_path / "b.log")
+    bad = val.execute([sys.executable, "-c", "import sys; print('x'); sys.exit(3)"], tmp_path / "b.log", echo=False)
     assert bad["status"] == "FAIL" and bad["return_code"] == 3
 
 
@@ -39,7 +39,7 @@ def _alive(pid: int) -> bool:
         return False
 
 
-def test_overrunning_stage_is_reaped_with_its_children(tmp_path):
+def test_step_past_its_deadline_is_ended_with_its_children(tmp_path):
     pidfile = tmp_path / "child.pid"
     script = textwrap.dedent(f"""
         import subprocess, sys, time
@@ -49,9 +49,10 @@ def test_overrunning_stage_is_reaped_with_its_children(tmp_path):
         time.sleep(60)
     """)
     t0 = time.monotonic()
-    rec = val.run_stage([sys.executable, "-c", script], tmp_path / "c.log", timeout_s=3.0, grace_s=2.0)
+    rec = val.execute([sys.executable, "-c", script], tmp_path / "c.log", deadline_s=3.0, grace_s=2.0, echo=False)
     assert time.monotonic() - t0 < 30
     assert rec["timed_out"] and rec["return_code"] == 124 and rec["status"] == "FAIL"
+    assert "started" in (tmp_path / "c.log").read_text()
     grandchild = int(pidfile.read_text())
     for _ in range(50):
         if not _alive(grandchild):
@@ -60,46 +61,85 @@ def test_overrunning_stage_is_reaped_with_its_children(tmp_path):
     assert not _alive(grandchild)
 
 
-def test_output_directory_must_be_empty(tmp_path):
-    val.require_empty_output(tmp_path / "new")
+def test_step_that_ignores_sigint_is_still_ended(tmp_path):
+    script = "import signal, time; signal.signal(signal.SIGINT, signal.SIG_IGN); print('up', flush=True); time.sleep(60)"
+    t0 = time.monotonic()
+    rec = val.execute([sys.executable, "-c", script], tmp_path / "d.log", deadline_s=2.0, grace_s=1.0, echo=False)
+    assert rec["timed_out"] and time.monotonic() - t0 < 20
+
+
+def test_output_directory_must_be_new_or_empty(tmp_path):
+    val.prepare_output_dir(tmp_path / "new")
+    val.prepare_output_dir(tmp_path / "new")  # still empty
     (tmp_path / "new" / "x").write_text("1")
     with pytest.raises(FileExistsError):
-        val.require_empty_output(tmp_path / "new")
+        val.prepare_output_dir(tmp_path / "new")
 
 
-def test_summaries_need_every_selected_case(tmp_path):
+def test_ledger_is_rewritten_whole(tmp_path):
+    ledger = val.Ledger(tmp_path / "m.json", {"status": "RUNNING", "stages": []})
+    ledger.add_stage({"kind": "probe", "status": "PASS"})
+    ledger.record["status"] = "PASS"
+    ledger.flush()
+    assert json.loads((tmp_path / "m.json").read_text()) == {"status": "PASS",
+                                                             "stages": [{"kind": "probe", "status": "PASS"}]}
+    assert [p.name for p in tmp_path.iterdir()] == ["m.json"]  # no temporary file left behind
+
+
+def _step(kind, path, count):
+    return val.Step(kind, "x", [], path, count)
+
+
+def test_pass_counts_need_every_selected_case(tmp_path):
     f = tmp_path / "summary.json"
-    f.write_text(json.dumps([{"status": "PASS"}, {"status": "PASS"}]))
-    assert val.functional_summary(f, 2)["all_passed"]
-    assert not val.functional_summary(f, 3)["all_passed"]  # a case that never ran is a failure
-    f.write_text(json.dumps([{"status": "PASS"}, {"status": "FAIL"}]))
-    assert val.functional_summary(f, 2)["passed"] == 1
+    f.write_text(json.dumps([{"passed": True}, {"passed": True}]))
+    assert val.tally(_step("functional", f, val.count_functional), 2)["all_passed"]
+    assert not val.tally(_step("functional", f, val.count_functional), 3)["all_passed"]  # a case that never ran
+    f.write_text(json.dumps([{"passed": True}, {"passed": False}]))
+    t = val.tally(_step("functional", f, val.count_functional), 2)
+    assert t["passed"] == 1 and not t["all_passed"]
+    missing = val.tally(_step("functional", tmp_path / "absent.json", val.count_functional), 2)
+    assert missing["passed"] == 0 and not missing["all_passed"]
     p = tmp_path / "performance.json"
     p.write_text(json.dumps({"results": [{"correctness": {"passed": True}}], "benchmark_errors": []}))
-    assert val.performance_summary(p, 1)["all_passed"]
+    assert val.tally(_step("performance", p, val.count_performance), 1)["all_passed"]
     p.write_text(json.dumps({"results": [{"correctness": {"passed": True}}],
                              "benchmark_errors": [{"case_id": "x", "error": "boom"}]}))
-    assert not val.performance_summary(p, 1)["all_passed"]
+    assert not val.tally(_step("performance", p, val.count_performance), 1)["all_passed"]
 
 
 def test_case_selection_and_case_set_parsing():
-    every = val.select_cases(CASES, None, False)
+    every = val.pick_cases(CASES, None, False)
     assert len(every) >= 3
-    lengths = {val._case_meta(p)[0] for p in every}
+    lengths = {val.case_params(p)[0] for p in every}
     one = sorted(lengths)[0]
-    assert all(val._case_meta(p)[0] == one for p in val.select_cases(CASES, [one], False))
-    assert all(val._case_meta(p)[1] for p in val.select_cases(CASES, None, True))
-    sets = val.parse_case_sets([f"a={CASES}", f"b={CASES}"])
+    assert all(val.case_params(p)[0] == one for p in val.pick_cases(CASES, [one], False))
+    assert all(val.case_params(p)[1] for p in val.pick_cases(CASES, None, True))
+    sets = val.case_sets_from([f"a={CASES}", f"b={CASES}"])
     assert list(sets) == ["a", "b"]
     with pytest.raises(ValueError):
-        val.parse_case_sets([str(CASES)])
+        val.case_sets_from([str(CASES)])
     with pytest.raises(ValueError):
-        val.parse_case_sets([f"a={CASES}", f"a={CASES}"])
+        val.case_sets_from([f"a={CASES}", f"a={CASES}"])
 
 
-def test_failed_probe_leaves_a_fail_manifest(tmp_path, monkeypatch):
-    """Without a GPU the init stage fails; the manifest must say FAIL with the reason and the
-    provenance hashes, and no functional stage may run."""
+def test_plan_has_one_step_per_case_set_and_thread_count(tmp_path):
+    args = val.argparse.Namespace(numerics="kv260", causal_only=True, lengths=[16, 32], skip_performance=False,
+                                  cpu_threads=[1, 4], warmup=0, repeats=1)
+    plan = val.build_plan(args, {"a": CASES, "b": CASES}, tmp_path)
+    assert [s.name for s in plan] == ["probe", "functional:a", "functional:b", "performance:cpu1",
+                                      "performance:cpu4"]
+    func = plan[1].argv
+    assert func[func.index("--lengths") + 1:func.index("--lengths") + 3] == ["16", "32"]
+    assert "--causal-only" in func and plan[1].artifact == tmp_path / "functional" / "a" / "summary.json"
+    perf = plan[4].argv
+    assert perf[perf.index("--lengths") + 1] == "16,32" and plan[4].env["OMP_NUM_THREADS"] == "4"
+    assert f"--case-set=b={CASES}" in perf
+
+
+def test_failed_probe_leaves_a_fail_manifest(tmp_path):
+    """Without a GPU the probe step fails; the manifest must say FAIL with the reason and the
+    provenance hashes, and no functional step may run."""
     import torch
 
     if torch.cuda.is_available():
@@ -109,8 +149,11 @@ def test_failed_probe_leaves_a_fail_manifest(tmp_path, monkeypatch):
     assert rc == 1
     manifest = json.loads((out / "run_manifest.json").read_text())
     assert manifest["status"] == "FAIL" and "probe" in manifest["error"]
-    assert [s["kind"] for s in manifest["stages"]] == ["init"]
+    assert [s["kind"] for s in manifest["stages"]] == ["probe"]
+    assert not (out / "consolidated_results.json").exists()
+    for key in ("schema", "started_utc", "ended_utc", "working_directory", "output_directory", "configuration"):
+        assert key in manifest
     names = {Path(f["source"]).name for f in manifest["provenance"]["files"]}
     assert {"attn_driver.py", "validation.py"} <= names
-    assert len(manifest["provenance"]["cases"]["board"]) == len(val.select_cases(CASES, None, False))
+    assert len(manifest["provenance"]["cases"]["board"]) == len(val.pick_cases(CASES, None, False))
     assert all(len(c["sha256"]) == 64 for c in manifest["provenance"]["cases"]["board"])
