@@ -22,12 +22,18 @@
  *   limit, first sub-block of the first KV tile) hw/rtl/core/attn_core.sv:107-154,
  *   hw/rtl/attn_top.sv:785
  *
- * Pinning: the LUT tables against their closed forms and the board ROM images' SHA-256;
- * fp32_add / fp32_mul against IEEE float32 (numpy) on normal operands, where the RTL's
- * rounding is IEEE round-to-nearest-even; hand-derived special cases; the whole transaction
- * against the float64 exact model within the LUT's and the bf16-truncated P's error, and the
- * known answers of one key (output = V exactly) and zero input (output +0).  No board vector
- * exists in the reference snapshot, so agreement with the board itself is not pinned.
+ * Pinning: the LUT tables against their closed forms and the board ROM images' SHA-256, the exp
+ * lookup at its 1024 knots and across every index boundary, the reciprocal lookup at powers of
+ * two and at its 256 bin centres; fp32_add / fp32_mul against IEEE float32 (numpy) on normal
+ * operands, where the RTL's rounding is IEEE round-to-nearest-even; hand-derived special cases.
+ * The composition (P truncated to its upper half, key-0-first sums, one O delta and one rescale
+ * per 16-key sub-block, the R(l) normalise, dimension-0-first Q.K) is pinned word for word by
+ * constructed transactions whose words follow from a few float32 operations and differ under
+ * each alternative; rtl_attention_planted applies those alternatives so the tests can show that
+ * each is rejected.  Whole transactions are also held to the float64 exact model within the
+ * LUT's and the truncated P's error, and to the known answers of one key (output = V exactly)
+ * and zero input (output +0).  No board vector exists in the reference snapshot, so agreement
+ * with the board itself is not pinned.
  * Parity unpinned: the corners where the RTL departs from IEEE (subnormal operands or
  * results, the leading-zero cap of fp32_add, the 8-bit exponent wrap of fp32_mul) follow the
  * RTL source alone; no independent check covers them.
@@ -230,15 +236,43 @@ uint32_t rtl_recip_lookup(uint32_t l, const uint32_t* recip_lut) {
     return s | (((253 - e) & 0xFF) << 23) | (recip_lut[f >> 15] & 0x7FFFFF);
 }
 
-/*
- * One KV260 transaction: q [H_q][L][D], k/v [H_kv][L][D] bf16 words, query head h reads kv
- * head h / (H_q / H_kv).  Writes out [H_q][L][D] bf16 words and, if non-NULL, the final
- * running max m (scaled-score units) and sum l of every row as fp32 bits.
- */
-void rtl_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, int n_q_heads, int n_kv_heads,
-                   int head_dim, int seq_len, int q_pos_base, int kv_pos_base, int causal, uint32_t scale_bits,
-                   const uint32_t* exp_lut, const uint32_t* recip_lut, uint16_t* out, uint32_t* m_out,
-                   uint32_t* l_out) {
+/* Mistakes planted on purpose (test infrastructure): each flag swaps one composition step for a
+ * plausible alternative, so the tests can show that their word-level checks reject it. */
+enum {
+    PLANT_P_RNE = 1,            /* P rounded to bf16 to nearest even instead of truncated       */
+    PLANT_SUM_REVERSED = 2,     /* row sum and PV sum of a sub-block taken from key 15 down     */
+    PLANT_FLAT_ACCUMULATE = 4,  /* O accumulated key by key instead of one delta per sub-block  */
+    PLANT_TILE_RESCALE = 8,     /* running max taken per 64-key tile instead of per sub-block   */
+    PLANT_EXACT_DIVIDE = 16,    /* O divided by l (IEEE) instead of multiplied by R(l)          */
+    PLANT_QK_REVERSED = 32,     /* Q.K summed from the last dimension down                      */
+};
+
+static uint32_t f32_div_bits(uint32_t a, uint32_t b) {
+    float x, y;
+    memcpy(&x, &a, 4);
+    memcpy(&y, &b, 4);
+    x = x / y;
+    uint32_t r;
+    memcpy(&r, &x, 4);
+    return r;
+}
+
+/* Scaled score of one key (hw/rtl/core/attn_tile.sv: sequential fp32 sum over d, then x scale),
+ * or -inf for a key that is masked or past the sequence. */
+static uint32_t key_score(const uint16_t* qr, const uint16_t* kr, int D, int live, uint32_t scale_bits, int plant) {
+    if (!live) return NEG_INF_BITS;
+    uint32_t acc = 0;
+    if (plant & PLANT_QK_REVERSED)
+        for (int d = D - 1; d >= 0; --d) acc = rtl_fp32_add(acc, rtl_bf16_mul(qr[d], kr[d]));
+    else
+        for (int d = 0; d < D; ++d) acc = rtl_fp32_add(acc, rtl_bf16_mul(qr[d], kr[d]));
+    return rtl_fp32_mul(acc, scale_bits);
+}
+
+static void attention_impl(const uint16_t* q, const uint16_t* k, const uint16_t* v, int n_q_heads, int n_kv_heads,
+                           int head_dim, int seq_len, int q_pos_base, int kv_pos_base, int causal,
+                           uint32_t scale_bits, const uint32_t* exp_lut, const uint32_t* recip_lut, uint16_t* out,
+                           uint32_t* m_out, uint32_t* l_out, int plant) {
     const int D = head_dim, L = seq_len, G = n_q_heads / n_kv_heads;
     const int n_kv_tiles = (L + 63) / 64;
     uint32_t O[512];
@@ -261,41 +295,56 @@ void rtl_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, int 
             for (int d = 0; d < D; ++d) O[d] = 0;
             int first = 1;
             for (int jt = 0; jt <= last_tile; ++jt) {
+                uint32_t tile_max = NEG_INF_BITS;
+                if (plant & PLANT_TILE_RESCALE)
+                    for (int key = jt * 64; key < jt * 64 + 64 && key < L; ++key)
+                        tile_max = rtl_fp32_max(tile_max, key_score(qr, k + ((size_t)hk * L + key) * D, D,
+                                                                    !(causal && q_pos < kv_pos_base + key),
+                                                                    scale_bits, plant));
                 for (int sb = 0; sb < 4; ++sb) {
                     const int c0 = jt * 64 + sb * 16;
                     if (c0 >= L) break; /* sub-blocks past the sequence are not issued */
-                    uint32_t row_max = NEG_INF_BITS;
+                    uint32_t row_max = tile_max;
                     int masked[16];
                     for (int c = 0; c < 16; ++c) {
                         const int key = c0 + c;
                         masked[c] = key >= L || (causal && q_pos < kv_pos_base + key);
-                        uint32_t val = NEG_INF_BITS;
-                        if (key < L) {
-                            const uint16_t* kr = k + ((size_t)hk * L + key) * D;
-                            uint32_t acc = 0;
-                            for (int d = 0; d < D; ++d) acc = rtl_fp32_add(acc, rtl_bf16_mul(qr[d], kr[d]));
-                            if (!masked[c]) val = rtl_fp32_mul(acc, scale_bits);
-                        }
-                        s[c] = val;
-                        row_max = rtl_fp32_max(row_max, val);
+                        s[c] = key < L ? key_score(qr, k + ((size_t)hk * L + key) * D, D, !masked[c], scale_bits,
+                                                   plant)
+                                       : NEG_INF_BITS;
+                        row_max = rtl_fp32_max(row_max, s[c]);
                     }
                     const uint32_t m_old = first ? NEG_INF_BITS : m;
                     const uint32_t l_old = first ? 0u : l;
                     const uint32_t m_new = rtl_fp32_max(m_old, row_max);
                     const uint32_t corr = first ? 0u : rtl_exp_lookup(rtl_fp32_sub(m_old, m_new), exp_lut);
                     uint32_t row_sum = 0;
-                    for (int c = 0; c < 16; ++c) {
+                    for (int c = 0; c < 16; ++c)
                         p[c] = masked[c] ? 0u : rtl_exp_lookup(rtl_fp32_sub(s[c], m_new), exp_lut);
-                        row_sum = rtl_fp32_add(row_sum, p[c]);
-                    }
+                    for (int i = 0; i < 16; ++i) row_sum = rtl_fp32_add(row_sum, p[plant & PLANT_SUM_REVERSED ? 15 - i : i]);
                     l = first ? row_sum : rtl_fp32_add(rtl_fp32_mul(l_old, corr), row_sum);
                     m = m_new;
+                    /* the PV operand is the upper half of the fp32 P word (attn_top.sv:653-658) */
+                    uint16_t pv[16];
+                    for (int c = 0; c < 16; ++c)
+                        pv[c] = (plant & PLANT_P_RNE) ? rtl_fp32_to_bf16(p[c]) : (uint16_t)(p[c] >> 16);
                     for (int d = 0; d < D; ++d) {
+                        if (plant & PLANT_FLAT_ACCUMULATE) {
+                            uint32_t o = rtl_fp32_mul(O[d], corr);
+                            for (int c = 0; c < 16; ++c) {
+                                const int key = c0 + c;
+                                const uint16_t vw = key < L ? v[((size_t)hk * L + key) * D + d] : 0;
+                                o = rtl_fp32_add(o, rtl_bf16_mul(pv[c], vw));
+                            }
+                            O[d] = o;
+                            continue;
+                        }
                         uint32_t delta = 0;
-                        for (int c = 0; c < 16; ++c) {
+                        for (int i = 0; i < 16; ++i) {
+                            const int c = plant & PLANT_SUM_REVERSED ? 15 - i : i;
                             const int key = c0 + c;
                             const uint16_t vw = key < L ? v[((size_t)hk * L + key) * D + d] : 0;
-                            delta = rtl_fp32_add(delta, rtl_bf16_mul((uint16_t)(p[c] >> 16), vw));
+                            delta = rtl_fp32_add(delta, rtl_bf16_mul(pv[c], vw));
                         }
                         O[d] = rtl_fp32_add(rtl_fp32_mul(O[d], corr), delta);
                     }
@@ -304,11 +353,36 @@ void rtl_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, int 
             }
             uint16_t* orow = out + ((size_t)hq * L + r) * D;
             const uint32_t rl = rtl_recip_lookup(l, recip_lut);
-            for (int d = 0; d < D; ++d) orow[d] = is_zero(l) ? 0 : rtl_fp32_to_bf16(rtl_fp32_mul(O[d], rl));
+            for (int d = 0; d < D; ++d) {
+                const uint32_t o = (plant & PLANT_EXACT_DIVIDE) ? f32_div_bits(O[d], l) : rtl_fp32_mul(O[d], rl);
+                orow[d] = is_zero(l) ? 0 : rtl_fp32_to_bf16(o);
+            }
             if (m_out) m_out[(size_t)hq * L + r] = m;
             if (l_out) l_out[(size_t)hq * L + r] = l;
         }
     }
+}
+
+/*
+ * One KV260 transaction: q [H_q][L][D], k/v [H_kv][L][D] bf16 words, query head h reads kv
+ * head h / (H_q / H_kv).  Writes out [H_q][L][D] bf16 words and, if non-NULL, the final
+ * running max m (scaled-score units) and sum l of every row as fp32 bits.
+ */
+void rtl_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, int n_q_heads, int n_kv_heads,
+                   int head_dim, int seq_len, int q_pos_base, int kv_pos_base, int causal, uint32_t scale_bits,
+                   const uint32_t* exp_lut, const uint32_t* recip_lut, uint16_t* out, uint32_t* m_out,
+                   uint32_t* l_out) {
+    attention_impl(q, k, v, n_q_heads, n_kv_heads, head_dim, seq_len, q_pos_base, kv_pos_base, causal, scale_bits,
+                   exp_lut, recip_lut, out, m_out, l_out, 0);
+}
+
+/* The same transaction with the PLANT_* mistakes of `plant` applied (tests only). */
+void rtl_attention_planted(const uint16_t* q, const uint16_t* k, const uint16_t* v, int n_q_heads, int n_kv_heads,
+                           int head_dim, int seq_len, int q_pos_base, int kv_pos_base, int causal,
+                           uint32_t scale_bits, const uint32_t* exp_lut, const uint32_t* recip_lut, uint16_t* out,
+                           uint32_t* m_out, uint32_t* l_out, int plant) {
+    attention_impl(q, k, v, n_q_heads, n_kv_heads, head_dim, seq_len, q_pos_base, kv_pos_base, causal, scale_bits,
+                   exp_lut, recip_lut, out, m_out, l_out, plant);
 }
 
 /* Element-wise batch forms, for the checks that sweep many operands through ctypes. */

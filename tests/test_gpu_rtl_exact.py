@@ -9,6 +9,7 @@ import pytest
 from lara_amd.attn_driver import AttentionAccelerator
 from oracle import gqa_oracle as orc
 from oracle import rtl_exact as rtl
+from tests import _kv260_cases as kc
 from tests._gen import bf16_normal
 
 pytestmark = pytest.mark.gpu
@@ -51,6 +52,17 @@ def test_kv260_mode_bit_exact_long_and_d64():
     v = bf16_normal(rng, (2, 96, 64))
     out, want = run_both(q, k, v, causal=False, qb=0, kb=0)
     assert np.array_equal(out, want)
+
+
+@pytest.mark.parametrize("name", [c.name for c in kc.all_cases()])
+def test_kv260_mode_constructed_composition_cases(name):
+    """The engine's output words on the transactions built so that each composition step of the
+    board's arithmetic decides a word, against the words derived by hand."""
+    case = {c.name: c for c in kc.all_cases()}[name]
+    q, k, v = case.tensors()
+    out, _ = run_both(q, k, v, causal=False, qb=0, kb=0)
+    bad = np.argwhere(out != case.expected_out())
+    assert bad.size == 0, f"{name}: {len(bad)} words differ, first at {tuple(bad[0])}"
 
 
 def test_kv260_mode_edges():
