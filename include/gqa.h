@@ -74,6 +74,8 @@ extern "C" {
 #define GQA_OPT_NUMERICS     4 /* GQA_NUMERICS_*: arithmetic of prefill / transactions (decode: EXACT only) */
 #define GQA_OPT_DECODE_MERGE 5 /* GQA_DECODE_MERGE_*: how split-KV decode merges a sequence's splits */
 #define GQA_OPT_PREFILL_KERNEL 6 /* GQA_PREFILL_KERNEL_*: decomposition of prefill / transaction launches */
+#define GQA_OPT_LAYER        7 /* layered paged context: the cache layer every entry point reads and writes
+                                  (0 .. n_layers-1; gqa_create_paged_layers) */
 
 /* Prefill decomposition (GQA_OPT_PREFILL_KERNEL).  SHARED: a work-group per kv head and 8 (32-row
  * block, query head) tasks shares each K/V tile over its GQA group; launches smaller than the GPU are
@@ -156,6 +158,24 @@ int gqa_paged_evict_lru(gqa_ctx* ctx, int32_t n_free_pages, const int32_t* pinne
 int gqa_paged_info(gqa_ctx* ctx, int32_t* page_size, int32_t* n_pages, int32_t* n_free,
                    int32_t* max_pages);
 int gqa_paged_table(gqa_ctx* ctx, int32_t b, int32_t* out, int32_t n);
+
+/* ---- multi-layer paged K/V cache ---------------------------------------------
+ * No reference counterpart: the board runs one layer per transaction and reloads its cache each
+ * time (attn_driver.py:552-586).  gqa_create_paged_layers is gqa_create_paged for a model of
+ * n_layers attention layers (1 .. GQA_MAX_LAYERS) sharing one block table per sequence and one
+ * page allocator: a page index names the same token rows in every layer, so reserve, release and
+ * evict map and unmap a run of tokens for all layers at once.  Each layer has its own pools
+ * (layout [n_layers][n_pages][H_kv][page_size][D], K and V apart).  GQA_OPT_LAYER selects the
+ * layer that decode, prefill, append, load, read, the layer stage and gqa_cache_pointers address
+ * (default 0); switching is a host-side pointer change, ordered with the launches already queued
+ * (each launch keeps the pools it was given).  A transaction reads the layer that was active when
+ * it was submitted; a captured graph, the layer active at capture.  gqa_paged_layers returns
+ * n_layers and the active layer (GQA_ERR_UNSUPPORTED on a contiguous context; gqa_create_paged
+ * contexts have one layer). */
+#define GQA_MAX_LAYERS 1024
+int gqa_create_paged_layers(const gqa_config* cfg, int32_t page_size, int32_t n_pages, int32_t n_layers,
+                            gqa_ctx** out_ctx);
+int gqa_paged_layers(gqa_ctx* ctx, int32_t* n_layers, int32_t* layer);
 
 /* ---- K/V cache --------------------------------------------------------------
  * gqa_load_kv replaces the KV branch of _service_request + _transfer(DEST_K_CACHE /

@@ -54,6 +54,8 @@ GQA_DECODE_MERGE_AUTO = 0
 GQA_DECODE_MERGE_LAUNCH = 1
 GQA_DECODE_MERGE_FUSED = 2
 GQA_OPT_PREFILL_KERNEL = 6
+GQA_OPT_LAYER = 7
+GQA_MAX_LAYERS = 1024
 GQA_PREFILL_KERNEL_AUTO = 0
 GQA_PREFILL_KERNEL_SHARED = 1
 GQA_PREFILL_KERNEL_ROWS = 2
@@ -91,6 +93,8 @@ _CTX = c_void_p
 _SIGNATURES = {
     "gqa_create": [POINTER(GqaConfig), POINTER(c_void_p)],
     "gqa_create_paged": [POINTER(GqaConfig), c_int32, c_int32, POINTER(c_void_p)],
+    "gqa_create_paged_layers": [POINTER(GqaConfig), c_int32, c_int32, c_int32, POINTER(c_void_p)],
+    "gqa_paged_layers": [_CTX, _P32, _P32],
     "gqa_destroy": [_CTX],
     "gqa_get_config": [_CTX, POINTER(GqaConfig)],
     "gqa_set_option": [_CTX, c_int32, c_int64],

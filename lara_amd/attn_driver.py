@@ -304,6 +304,7 @@ class AttentionAccelerator:
         numerics: str = "exact",
         page_size: int | None = None,
         n_pages: int | None = None,
+        n_layers: int | None = None,
     ) -> None:
         self._closed = True
         self._ctx = ctypes.c_void_p()
@@ -325,10 +326,17 @@ class AttentionAccelerator:
                              self.max_q_len, float(scale or 0.0), int(device))
         lib = _lib.lib()
         self.paged = page_size is not None
+        if n_layers is not None and not self.paged:
+            raise ValueError("a multi-layer cache is paged: give page_size with n_layers")
+        self.n_layers = int(n_layers) if n_layers is not None else 1
         if self.paged:
             if n_pages is None:
                 n_pages = self.batch * -(-self.max_seq_len // int(page_size))
-            rc = lib.gqa_create_paged(ctypes.byref(cfg), int(page_size), int(n_pages), ctypes.byref(self._ctx))
+            if n_layers is not None:
+                rc = lib.gqa_create_paged_layers(ctypes.byref(cfg), int(page_size), int(n_pages), self.n_layers,
+                                                 ctypes.byref(self._ctx))
+            else:
+                rc = lib.gqa_create_paged(ctypes.byref(cfg), int(page_size), int(n_pages), ctypes.byref(self._ctx))
         else:
             rc = lib.gqa_create(ctypes.byref(cfg), ctypes.byref(self._ctx))
         if rc != _lib.GQA_OK:
@@ -562,6 +570,22 @@ class AttentionAccelerator:
             raise MemoryError(f"cannot free {n_free_pages} pages without evicting a pinned sequence")
         _lib.check(rc, "gqa_paged_evict_lru")
         return [int(x) for x in out[: n.value]]
+
+    def select_layer(self, layer: int) -> None:
+        """Make ``layer`` the cache layer that every later call reads and writes (multi-layer
+        paged engines; the block tables and the page pool are shared by all layers)."""
+        if not 0 <= int(layer) < self.n_layers:
+            raise ValueError(f"layer {layer} outside 0..{self.n_layers - 1}")
+        self._call("gqa_set_option", _lib.GQA_OPT_LAYER, int(layer))
+
+    @property
+    def layer(self) -> int:
+        """The active cache layer (0 on a single-layer engine)."""
+        if not self.paged:
+            return 0
+        n, cur = ctypes.c_int32(0), ctypes.c_int32(0)
+        self._call("gqa_paged_layers", ctypes.byref(n), ctypes.byref(cur))
+        return int(cur.value)
 
     def page_info(self) -> dict[str, int]:
         """Page size, pool size, free pages and block-table width of a paged engine."""

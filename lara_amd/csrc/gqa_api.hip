@@ -28,6 +28,7 @@ struct Txn {
     int valid = 0;     // a transaction has been submitted (configure + Q staged)
     int running = 0;   // launched, completion not yet observed
     int32_t b = 0, q_len = 0, q_pos_base = 0, kv_len = 0, kv_pos_base = 0, causal = 1;
+    int layer = 0;     // cache layer active at submission; the transaction reads that layer
     float kernel_us = 0.f, total_us = 0.f, copy_us = 0.f;
 };
 
@@ -58,8 +59,11 @@ struct gqa_ctx {
     int max_splits_cap = 0;
     float scale = 0.f;
     hipStream_t stream = nullptr;
-    uint16_t* k_cache = nullptr;
+    uint16_t* k_cache = nullptr;  // the active layer's K pool (k_pool + layer * kv_words)
     uint16_t* v_cache = nullptr;
+    uint16_t* k_pool = nullptr;   // the allocations: n_layers pools back to back
+    uint16_t* v_pool = nullptr;
+    int n_layers = 1, layer = 0;
     float* part_o = nullptr;
     float* part_ml = nullptr;
     int32_t* arrivals = nullptr;  // [B*H_kv] split arrival counters of the fused merge (zero between launches)
@@ -643,7 +647,7 @@ size_t prefill_workspace_need(const gqa_ctx* c, int target_wgs) {
     return need;
 }
 
-int create_ctx(const gqa_config* cfg, int32_t page_size, int32_t n_pages, gqa_ctx** out_ctx) {
+int create_ctx(const gqa_config* cfg, int32_t page_size, int32_t n_pages, int32_t n_layers, gqa_ctx** out_ctx) {
     if (!cfg || !out_ctx) return GQA_ERR_NULL;
     *out_ctx = nullptr;
     const gqa_config& k = *cfg;
@@ -681,6 +685,7 @@ int create_ctx(const gqa_config* cfg, int32_t page_size, int32_t n_pages, gqa_ct
         c->max_pages = (k.max_seq_len + page_size - 1) / page_size;
         c->pages = PageTable(k.batch, c->max_pages, n_pages);
     }
+    c->n_layers = n_layers;
     const size_t D = (size_t)k.head_dim;
     const size_t units = (size_t)k.batch * k.n_kv_heads;
     c->stage_words = (size_t)k.n_q_heads * D * (size_t)(k.batch > k.max_q_len ? k.batch : k.max_q_len);
@@ -691,8 +696,10 @@ int create_ctx(const gqa_config* cfg, int32_t page_size, int32_t n_pages, gqa_ct
         if (rc != GQA_OK) return;
         if (hipMalloc(p, bytes) != hipSuccess) rc = GQA_ERR_OOM;
     };
-    alloc((void**)&c->k_cache, kv_words(c) * 2);
-    alloc((void**)&c->v_cache, kv_words(c) * 2);
+    alloc((void**)&c->k_pool, kv_words(c) * 2 * (size_t)n_layers);
+    alloc((void**)&c->v_pool, kv_words(c) * 2 * (size_t)n_layers);
+    c->k_cache = c->k_pool;
+    c->v_cache = c->v_pool;
     alloc((void**)&c->part_o, units * c->max_splits_cap * group * D * sizeof(float));
     alloc((void**)&c->part_ml, units * c->max_splits_cap * group * 2 * sizeof(float));
     alloc((void**)&c->arrivals, units * sizeof(int32_t));
@@ -864,22 +871,32 @@ int gqa_device_count(int32_t* out_count) {
     return GQA_OK;
 }
 
-int gqa_create(const gqa_config* cfg, gqa_ctx** out_ctx) { return create_ctx(cfg, 0, 0, out_ctx); }
+int gqa_create(const gqa_config* cfg, gqa_ctx** out_ctx) { return create_ctx(cfg, 0, 0, 1, out_ctx); }
 
 int gqa_create_paged(const gqa_config* cfg, int32_t page_size, int32_t n_pages, gqa_ctx** out_ctx) {
     if (!cfg || !out_ctx) return GQA_ERR_NULL;
     *out_ctx = nullptr;
     if (page_size < 64 || page_size > (1 << 16) || (page_size & (page_size - 1)) != 0 || n_pages < 1)
         return GQA_ERR_BAD_CFG;
-    return create_ctx(cfg, page_size, n_pages, out_ctx);
+    return create_ctx(cfg, page_size, n_pages, 1, out_ctx);
+}
+
+int gqa_create_paged_layers(const gqa_config* cfg, int32_t page_size, int32_t n_pages, int32_t n_layers,
+                            gqa_ctx** out_ctx) {
+    if (!cfg || !out_ctx) return GQA_ERR_NULL;
+    *out_ctx = nullptr;
+    if (page_size < 64 || page_size > (1 << 16) || (page_size & (page_size - 1)) != 0 || n_pages < 1 ||
+        n_layers < 1 || n_layers > GQA_MAX_LAYERS)
+        return GQA_ERR_BAD_CFG;
+    return create_ctx(cfg, page_size, n_pages, n_layers, out_ctx);
 }
 
 int gqa_destroy(gqa_ctx* c) {
     if (!c) return GQA_ERR_NULL;
     (void)hipSetDevice(c->cfg.device);
     if (c->stream) (void)hipStreamSynchronize(c->stream);
-    (void)hipFree(c->k_cache);
-    (void)hipFree(c->v_cache);
+    (void)hipFree(c->k_pool);
+    (void)hipFree(c->v_pool);
     (void)hipFree(c->part_o);
     (void)hipFree(c->part_ml);
     (void)hipFree(c->arrivals);
@@ -944,6 +961,14 @@ int gqa_set_option(gqa_ctx* c, int32_t option, int64_t value) {
                 return GQA_ERR_RANGE;
             c->decode_merge = (int)value;
             return GQA_OK;
+        case GQA_OPT_LAYER: {
+            if (value < 0 || value >= c->n_layers) return GQA_ERR_RANGE;
+            const size_t off = kv_words(c) * (size_t)value;
+            c->layer = (int)value;
+            c->k_cache = c->k_pool + off;
+            c->v_cache = c->v_pool + off;
+            return GQA_OK;
+        }
         case GQA_OPT_NUMERICS:
             if (value != GQA_NUMERICS_EXACT && value != GQA_NUMERICS_KV260) return GQA_ERR_RANGE;
             if (value == GQA_NUMERICS_KV260 && ((c->cfg.head_dim != 64 && c->cfg.head_dim != 128) || c->paged))
@@ -1043,6 +1068,14 @@ int gqa_paged_info(gqa_ctx* c, int32_t* page_size, int32_t* n_pages, int32_t* n_
     if (n_pages) *n_pages = c->n_pages;
     if (n_free) *n_free = c->pages.free_pages();
     if (max_pages) *max_pages = c->max_pages;
+    return GQA_OK;
+}
+
+int gqa_paged_layers(gqa_ctx* c, int32_t* n_layers, int32_t* layer) {
+    if (!c) return GQA_ERR_NULL;
+    if (!c->paged) return GQA_ERR_UNSUPPORTED;
+    if (n_layers) *n_layers = c->n_layers;
+    if (layer) *layer = c->layer;
     return GQA_OK;
 }
 
@@ -1392,6 +1425,7 @@ int gqa_submit(gqa_ctx* c, int32_t b, const uint16_t* q, int32_t q_len, int32_t 
     if (!prefill_supported(c->cfg.head_dim, c->group)) return GQA_ERR_UNSUPPORTED;
     HIP_TRY(hipSetDevice(c->cfg.device));
     c->txn = Txn();
+    c->txn.layer = c->layer;
     c->txn.b = b;
     c->txn.q_len = q_len;
     c->txn.q_pos_base = q_pos_base;
@@ -1448,6 +1482,7 @@ int gqa_submit_layer(gqa_ctx* c, int32_t b, const uint16_t* x, int32_t n_tokens,
     uint8_t* dwv = dwk + wkb;
     uint8_t* dg = dwq + pad(wqb + 2 * wkb);
     c->txn = Txn();
+    c->txn.layer = c->layer;
     c->txn.b = b;
     c->txn.q_len = n_tokens;
     c->txn.q_pos_base = q_pos_base;
@@ -1549,8 +1584,15 @@ int gqa_start(gqa_ctx* c) {
     HIP_TRY(hipSetDevice(c->cfg.device));
     const Txn& t = c->txn;
     HIP_TRY(hipEventRecord(c->ev_t[1], c->stream));
+    // The transaction reads the layer it was submitted on, whichever layer is active now.
+    uint16_t* const k_active = c->k_cache;
+    uint16_t* const v_active = c->v_cache;
+    c->k_cache = c->k_pool + kv_words(c) * (size_t)t.layer;
+    c->v_cache = c->v_pool + kv_words(c) * (size_t)t.layer;
     int rc = run_prefill(c, t.b, c->q_dev, t.q_len, t.q_pos_base, t.kv_len, t.kv_pos_base, t.causal, c->o_dev,
                          nullptr, c->stream);
+    c->k_cache = k_active;
+    c->v_cache = v_active;
     if (rc != GQA_OK) return rc;
     HIP_TRY(hipEventRecord(c->ev_t[2], c->stream));
     const size_t owords = (size_t)c->cfg.n_q_heads * t.q_len * c->cfg.head_dim;

@@ -55,7 +55,13 @@ def test_create_rejects_bad_config_before_device():
     assert lib.gqa_create(ctypes.byref(_cfg(head_dim=96)), ctypes.byref(ctx)) == _lib.GQA_ERR_UNSUPPORTED
     assert lib.gqa_create(ctypes.byref(_cfg(n_q_heads=96, n_kv_heads=3)), ctypes.byref(ctx)) == _lib.GQA_ERR_UNSUPPORTED
     assert lib.gqa_create(None, ctypes.byref(ctx)) == _lib.GQA_ERR_NULL
+    for n_layers in (0, _lib.GQA_MAX_LAYERS + 1):
+        assert lib.gqa_create_paged_layers(ctypes.byref(_cfg()), 64, 8, n_layers, ctypes.byref(ctx)) == \
+            _lib.GQA_ERR_BAD_CFG
+    assert lib.gqa_create_paged_layers(ctypes.byref(_cfg()), 48, 8, 2, ctypes.byref(ctx)) == _lib.GQA_ERR_BAD_CFG
     assert not ctx.value
+    with pytest.raises(ValueError):  # a multi-layer cache is a paged one
+        drv.AttentionAccelerator(n_layers=2)
 
 
 def test_null_context_is_rejected():
