@@ -514,6 +514,35 @@ class LayerBench:
         self.lib.gqa_destroy(self.ctx)
 
 
+def copy_same_bytes(n_bytes: int, pairs: int = 8, launches: int = 40) -> dict:
+    """A plain device copy (torch copy_, the runtime's copy kernel) moving n_bytes in and n_bytes out,
+    the reference for a streaming kernel of that size: ``launches`` copies back to back behind a
+    bounded gate, rotating over ``pairs`` source/destination pairs so that no copy finds its data in
+    the L2 the previous one left behind (the footprint, 2 x pairs x n_bytes, exceeds the L2)."""
+    import torch
+
+    stream = bench_stream(torch.device("cuda", 0))
+    bufs = [(torch.empty(n_bytes, dtype=torch.uint8, device="cuda"), torch.empty(n_bytes, dtype=torch.uint8,
+                                                                                device="cuda")) for _ in range(pairs)]
+    for src, _ in bufs:
+        src.random_(0, 255)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        for src, dst in bufs:
+            dst.copy_(src)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(int(min(launches * 40.0, MAX_GATE_US) * sleep_rate(stream)))  # host queues ahead
+        e0.record(stream)
+        for i in range(launches):
+            src, dst = bufs[i % pairs]
+            dst.copy_(src)
+        e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / launches
+    return {"bytes_each_way": n_bytes, "us": us, "gbps": 2 * n_bytes / (us * 1e-6) / 1e9,
+            "method": f"torch copy_ back to back over {pairs} rotating buffer pairs, {launches} launches"}
+
+
 def measure_layer(name: str, steps: int, warmup: int, target_wgs: int = 0) -> dict:
     from lara_amd.benchmark import BF16_DENSE_TFLOPS, HBM_PEAK_GBPS, LAYER_WORKLOADS, layer_projection_flops, \
         prefill_flops, valid_pairs
@@ -550,14 +579,22 @@ def measure_layer(name: str, steps: int, warmup: int, target_wgs: int = 0) -> di
         "tokens_per_s": w.tokens / (r["wall_us"] * 1e-6),
         "gate_held": r["gate_held"],
     }
+    copies = {"rms_norm": copy_same_bytes(w.tokens * w.hidden * 2),
+              "rope_scatter": copy_same_bytes(rope_bytes // 2)}
     for k in ("rms_norm", "rope_scatter"):
         out[f"{k}_frac_of_hbm_peak"] = out[f"{k}_gbps"] / HBM_PEAK_GBPS if out[f"{k}_gbps"] else None
+        out[f"{k}_copy_same_bytes"] = copies[k]
+        out[f"{k}_frac_of_copy"] = copies[k]["us"] / out[f"{k}_us"] if out[f"{k}_us"] > 0 else None
     out["qkv_projection_frac_of_bf16_peak"] = (out["qkv_projection_tflops"] / BF16_DENSE_TFLOPS
                                                if out["qkv_projection_tflops"] else None)
     log(f"{name}: {out['us_per_layer']:.1f} us/layer: norm {norm_us:.1f} us = {out['rms_norm_gbps'] or 0:.0f} GB/s, "
         f"QKV GEMM {proj_us:.1f} us = {out['qkv_projection_tflops'] or 0:.0f} TFLOP/s, RoPE {rope_us:.1f} us = "
         f"{out['rope_scatter_gbps'] or 0:.0f} GB/s, attention {attn_us:.1f} us = {out['attention_tflops'] or 0:.0f} "
         "TFLOP/s")
+    log(f"{name}: a device copy of the same bytes takes {copies['rms_norm']['us']:.1f} us "
+        f"({copies['rms_norm']['gbps']:.0f} GB/s; norm at {out['rms_norm_frac_of_copy']:.0%} of it) and "
+        f"{copies['rope_scatter']['us']:.1f} us ({copies['rope_scatter']['gbps']:.0f} GB/s; RoPE at "
+        f"{out['rope_scatter_frac_of_copy']:.0%})")
     return out
 
 

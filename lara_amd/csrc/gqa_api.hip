@@ -529,7 +529,10 @@ int run_layer_qkv(gqa_ctx* c, int32_t b, const void* x, int32_t n_tokens, int32_
     const int D = c->cfg.head_dim, nq = c->cfg.n_q_heads * D, nkv = c->cfg.n_kv_heads * D;
     const int ld = nq + 2 * nkv;
     const size_t y_bytes = gamma ? ((size_t)n_tokens * hidden * 2 + 255) / 256 * 256 : 0;
-    int rc = ensure_buffer(&c->layer_tmp, &c->layer_tmp_bytes, y_bytes + (size_t)n_tokens * ld * 2);
+    const size_t qkv_bytes = ((size_t)n_tokens * ld * 2 + 255) / 256 * 256;
+    const int cs_sets = rope ? (kv_pos_base == q_pos_base ? 1 : 2) : 0;  // RoPE cos/sin table sets
+    const size_t cs_bytes = (size_t)cs_sets * n_tokens * (D / 2) * 2 * sizeof(float);
+    int rc = ensure_buffer(&c->layer_tmp, &c->layer_tmp_bytes, y_bytes + qkv_bytes + cs_bytes);
     if (rc != GQA_OK) return rc;
     if (!c->lt) {
         const hipblasStatus_t st = hipblasLtCreate(&c->lt);
@@ -549,7 +552,9 @@ int run_layer_qkv(gqa_ctx* c, int32_t b, const void* x, int32_t n_tokens, int32_
     if (proj_events.start) HIP_TRY(hipEventRecord(proj_events.start, s));
     HIP_TRY(mark(0));
     const uint16_t* src = (const uint16_t*)x;
-    if (gamma) {
+    float* cs = rope ? reinterpret_cast<float*>(c->layer_tmp + y_bytes + qkv_bytes) : nullptr;
+    if (gamma || rope) {
+        // The RMSNorm launch also fills the RoPE table (the table alone without normalisation).
         NormArgs na{};
         na.x = (const uint16_t*)x;
         na.gamma = (const uint16_t*)gamma;
@@ -557,8 +562,15 @@ int run_layer_qkv(gqa_ctx* c, int32_t b, const void* x, int32_t n_tokens, int32_
         na.n_tokens = n_tokens;
         na.hidden = hidden;
         na.eps = eps;
+        na.table.cs = cs;
+        na.table.sets = cs_sets;
+        na.table.pairs = D / 2;
+        na.table.n_tokens = n_tokens;
+        na.table.q_pos_base = q_pos_base;
+        na.table.kv_pos_base = kv_pos_base;
+        for (int p = 0; p < D / 2; ++p) na.table.theta[p] = (float)pow(kRopeBase, -2.0 * p / D);
         HIP_TRY(launch_rms_norm(na, stage_events ? Launch{s} : timed(c, GQA_TIMER_NORM, s)));
-        src = na.y;
+        if (gamma) src = na.y;
     }
     HIP_TRY(mark(1));
     uint16_t* qkv = (uint16_t*)(c->layer_tmp + y_bytes);
@@ -605,9 +617,9 @@ int run_layer_qkv(gqa_ctx* c, int32_t b, const void* x, int32_t n_tokens, int32_
     ra.n_q_heads = c->cfg.n_q_heads;
     ra.n_kv_heads = c->cfg.n_kv_heads;
     ra.head_dim = D;
-    ra.q_pos_base = q_pos_base;
-    ra.kv_pos_base = kv_pos_base;
     ra.rope = rope ? 1 : 0;
+    ra.cs = cs;
+    ra.cs_k_set = cs_sets == 2 ? 1 : 0;
     ra.q_out = (uint16_t*)q_out;
     const size_t seq = c->paged ? 0 : (size_t)b * c->cfg.n_kv_heads * c->l_cap * D;
     ra.kc = c->k_cache + seq;
@@ -616,7 +628,6 @@ int run_layer_qkv(gqa_ctx* c, int32_t b, const void* x, int32_t n_tokens, int32_
     ra.page_shift = c->page_shift;
     ra.l_cap = c->l_cap;
     ra.row0 = row0;
-    for (int p = 0; p < D / 2; ++p) ra.theta[p] = (float)pow(kRopeBase, -2.0 * p / D);
     HIP_TRY(launch_rope_scatter(ra, stage_events ? Launch{s} : timed(c, GQA_TIMER_ROPE, s)));
     HIP_TRY(mark(3));
     c->layer_timed = stage_events;

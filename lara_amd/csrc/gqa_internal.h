@@ -174,28 +174,41 @@ hipError_t launch_append(const uint16_t* k_rows, const uint16_t* v_rows, const i
 // Layer input stage of run_layer (sw/attn_driver.py:552-576): RMSNorm of the hidden states
 // and, after the QKV projection GEMM, RoPE plus the head-major scatter of Q and of K/V into
 // the cache.
+constexpr int kMaxRopePairs = 64;  // head_dim <= 128
+
+// cos/sin table of the RoPE stage: [sets][n_tokens][pairs][cos, sin] fp32, set 0 for the Q
+// positions q_pos_base + t, set 1 for the K positions kv_pos_base + t (only when they differ).
+struct RopeTable {
+    float* cs;           // nullptr: no table to compute
+    int sets, pairs, n_tokens;
+    int q_pos_base, kv_pos_base;
+    float theta[kMaxRopePairs];  // rotation frequency of pair (2p, 2p+1)
+};
+
 struct NormArgs {
     const uint16_t* x;      // [n_tokens][hidden] bf16
-    const uint16_t* gamma;  // [hidden] bf16
+    const uint16_t* gamma;  // [hidden] bf16; nullptr: no rows to normalise (the table only)
     uint16_t* y;            // [n_tokens][hidden] bf16
     int n_tokens, hidden;
     float eps;
+    int table_wgs;          // the launch's first table_wgs work-groups fill `table`
+    RopeTable table;
 };
 hipError_t launch_rms_norm(const NormArgs& a, const Launch& l);
 
-constexpr int kMaxRopePairs = 64;  // head_dim <= 128
 struct RopeArgs {
     const uint16_t* qkv;   // [n_tokens][ld] bf16: Q heads, then K heads, then V heads, D columns each
     int ld;
     int n_tokens, n_q_heads, n_kv_heads, head_dim;
-    int q_pos_base, kv_pos_base, rope;
+    int rope;              // rotate Q and K with `cs`
+    const float* cs;       // the RopeTable of this call (filled by the RMSNorm launch before it)
+    int cs_k_set;          // 1: K positions have their own set, 0: K uses the Q set
     uint16_t* q_out;       // [n_q_heads][n_tokens][D]
     uint16_t* kc;          // cache of one sequence: [n_kv_heads][l_cap][D], rows row0 ..
     uint16_t* vc;          //   (paged: the pools, addressed through block_table)
     int l_cap, row0;
     const int32_t* block_table;  // paged: the sequence's page indices; nullptr = contiguous
     int page_shift;
-    float theta[kMaxRopePairs];  // rotation frequency of pair (2p, 2p+1)
 };
 hipError_t launch_rope_scatter(const RopeArgs& a, const Launch& l);
 
