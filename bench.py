@@ -704,6 +704,42 @@ def read_ceiling(gib: int = 4, launches: int = 10) -> dict:
                       f"{launches} launches back to back between two events per configuration"}
 
 
+def launch_floor(launches: int = 200) -> dict:
+    """Device time per launch of a kernel that does almost nothing (the read probe over 16 bytes),
+    back to back behind a bounded gate on one stream: the fixed cost every step pays per launch
+    (dispatch, wave launch and the end-of-kernel cache maintenance), beside which the launch-bound
+    workloads (C1, C2) are read.  Measured with 1 and with 256 work-groups."""
+    import torch
+    from lara_amd import _lib
+
+    lib = _lib.lib()
+    stream = bench_stream(torch.device("cuda", 0))
+    sptr = ctypes.c_void_p(stream.cuda_stream)
+    src = torch.zeros(4096, dtype=torch.uint8, device="cuda")
+    sink = torch.zeros(256, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    out = {}
+    for wgs in (1, 256):
+        call = lambda: _lib.check(lib.gqa_stream_read_device(  # noqa: E731
+            ctypes.c_void_p(src.data_ptr()), 16 * wgs, wgs, 1, ctypes.c_void_p(sink.data_ptr()), sptr), "probe")
+        for _ in range(10):
+            call()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            torch.cuda._sleep(int(min(launches * 20.0, MAX_GATE_US) * sleep_rate(stream)))  # host queues ahead
+            e0.record(stream)
+            for _ in range(launches):
+                call()
+            e1.record(stream)
+        torch.cuda.synchronize()
+        out[f"us_per_launch_{wgs}_wg"] = e0.elapsed_time(e1) * 1e3 / launches
+    out["method"] = (f"{launches} back-to-back launches of the 16-byte-per-work-group read probe "
+                     "(gqa_stream_read_device) behind a bounded gate, one event pair around them")
+    log(f"launch floor: {out['us_per_launch_1_wg']:.2f} us per launch (1 work-group), "
+        f"{out['us_per_launch_256_wg']:.2f} us (256 work-groups)")
+    return out
+
+
 def cpu_threads_all() -> int:
     """Host threads of the all-cores pass: the affinity set, capped by OMP_NUM_THREADS when set."""
     aff = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
@@ -1138,6 +1174,7 @@ def main() -> int:
                         merge=args.decode_merge)
             others[name] = {k: r[k] for k in decode_keys if k in r}
     ceiling = None if args.no_read_ceiling else read_ceiling()
+    floor = launch_floor()
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baselines(args.workload, args.cpu_seconds, args.cpu_seconds_other)
@@ -1200,6 +1237,7 @@ def main() -> int:
         "kernels_us": {"decode_step": main_r["decode_us"]},
         "roofline": roofline,
         "read_ceiling": ceiling,
+        "launch_floor": floor,
         "cpu_baseline": cpu,
         "environment": collect_environment(),
         "other_workloads": others,

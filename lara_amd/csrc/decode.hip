@@ -23,11 +23,12 @@
 //      stays fp32 (fp32 FMAs); from G = 8 on the PV FMAs would bound the kernel, so p is
 //      rounded to bf16 and v_dot2 takes two keys per instruction.
 // At the end the waves merge in LDS.  A sequence that fits in one split writes the
-// bf16 output directly; otherwise each split writes an fp32 partial (O, m, l) and
-// decode_combine_kernel merges the splits with log-sum-exp weights.  (Merging inside the
-// split kernel -- the last split to arrive combines -- needs a device-scope release per
-// split, i.e. an L2 write-back per wave on this multi-XCD part, and measured 2.7x slower
-// at batch 64 x 8 kv heads x 8192 keys than the second launch.)
+// bf16 output directly; otherwise each split writes an fp32 partial (O, m, l) and the
+// splits merge with log-sum-exp weights: inside the launch, by the last split of the
+// (sequence, kv head) to arrive (an agent-scope release per split: an L2 write-back of its
+// XCD, worth it while the split grid fits one dispatch round, as for one long sequence), or
+// by decode_combine_kernel, a second launch (larger grids, where every split's write-back
+// would cost more than the launch).
 //
 // Fused append: when k_new/v_new are given, split 0 of every (sequence, kv head) writes
 // the new row to cache row positions[b], and any split whose key range contains that row
@@ -182,64 +183,109 @@ __device__ int rank_to_sequence(const DecodeArgs& a, int rank) {
     return rank;
 }
 
-// Log-sum-exp merge of the split partials of one (sequence, kv head) for query head g of the group
-// and dim d: the (m, l) pairs and dim d of the partial O of kCombineBatch splits are loaded together
-// and folded into a running (M, O, l) with one rescale per batch, so a sequence pays one memory
-// round trip per batch of splits.  COHERENT: agent-scope atomic loads (the partials were written by
-// other work-groups of the same launch); the merge inside the split kernel runs on its critical
-// path, so it takes twice the batch.
-template <bool COHERENT>
-constexpr int combine_batch() {
-    return COHERENT ? 32 : 16;
-}
+// Log-sum-exp merge of the split partials of one (sequence, kv head), split-parallel: wave w
+// folds splits w, w + NW, ... with lane e (and e + 64, ...) owning 8 consecutive dims of one
+// head (16-byte loads of the partial O, one 8-byte load of (m, l)), kMergeBatch splits per
+// memory round trip; then the waves' (M, O, l) fold through LDS and thread (g, d) writes the
+// output.  The split kernel's fused merge (the last split to arrive, after its acquire of the
+// other splits' partials, reusing the LDS of its own wave merge) and decode_combine_kernel run
+// this same code with the same NW, so both fold in the same order and give the same words.
+constexpr int kMergeBatch = 4;
 
-template <bool COHERENT>
-__device__ __forceinline__ float load_partial(const float* p) {
-    if constexpr (COHERENT) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return *p;
-}
-
-template <int D, int G, bool COHERENT>
-__device__ __forceinline__ void merge_splits(const DecodeArgs& a, int unit, int b, int h, int g, int d, int n_splits) {
-    const size_t base = (size_t)unit * a.max_splits * G + g;  // partial index of split 0
-    const float* ml = a.part_ml + base * 2;
-    const float* po = a.part_o + base * D + d;
-    const size_t stride = (size_t)G;  // partial rows between consecutive splits
-    float M = -INFINITY, O = 0.f, Ls = 0.f;
-    constexpr int kCombineBatch = combine_batch<COHERENT>();
-    for (int s0 = 0; s0 < n_splits; s0 += kCombineBatch) {
-        float em[kCombineBatch], el[kCombineBatch], v[kCombineBatch];
+template <int D, int G, int NW>
+__device__ __forceinline__ void merge_splits_parallel(const DecodeArgs& a, int unit, int b, int h, int n_splits,
+                                                      float (*lds_o)[G][D], float (*lds_m)[G], float (*lds_l)[G]) {
+    constexpr int E = G * D / 8;               // 8-dim entries of the group's output
+    constexpr int EPL = (E + 63) / 64;         // entries per lane
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const float4* po = reinterpret_cast<const float4*>(a.part_o);
+    const float2* pml = reinterpret_cast<const float2*>(a.part_ml);
+    const size_t base = (size_t)unit * a.max_splits * G;  // partial row of (split 0, head 0)
+    float M[EPL], L[EPL], O[EPL][8];
 #pragma unroll
-        for (int j = 0; j < kCombineBatch; ++j) {
-            if (s0 + j < n_splits) {
-                const size_t r = (size_t)(s0 + j) * stride;
-                em[j] = load_partial<COHERENT>(ml + r * 2);
-                el[j] = load_partial<COHERENT>(ml + r * 2 + 1);
-                v[j] = load_partial<COHERENT>(po + r * D);
-            } else {
-                em[j] = -INFINITY;
-                el[j] = 0.f;
-                v[j] = 0.f;
+    for (int k = 0; k < EPL; ++k) {
+        M[k] = -INFINITY;
+        L[k] = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) O[k][i] = 0.f;
+    }
+    for (int s0 = wave; s0 < n_splits; s0 += NW * kMergeBatch) {
+#pragma unroll
+        for (int k = 0; k < EPL; ++k) {
+            const int e = lane + 64 * k;
+            if (e >= E) break;
+            const int g = e / (D / 8), c = e - g * (D / 8);
+            float2 ml[kMergeBatch];
+            float4 lo[kMergeBatch], hi[kMergeBatch];
+#pragma unroll
+            for (int j = 0; j < kMergeBatch; ++j) {
+                const int sp = s0 + j * NW;
+                if (sp < n_splits) {
+                    const size_t row = base + (size_t)sp * G + g;
+                    ml[j] = pml[row];
+                    lo[j] = po[(row * D + 8 * c) / 4];
+                    hi[j] = po[(row * D + 8 * c) / 4 + 1];
+                } else {
+                    ml[j] = make_float2(-INFINITY, 0.f);
+                    lo[j] = hi[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+                }
+            }
+            float bm = M[k];
+#pragma unroll
+            for (int j = 0; j < kMergeBatch; ++j) bm = fmaxf(bm, ml[j].x);
+            if (bm == -INFINITY) continue;  // no valid key in these splits yet
+            const float corr = fast_exp2(M[k] - bm);  // 0 while M = -inf
+            L[k] *= corr;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) O[k][i] *= corr;
+#pragma unroll
+            for (int j = 0; j < kMergeBatch; ++j) {
+                const float w = fast_exp2(ml[j].x - bm);  // 0 for a split past n_splits
+                L[k] = fmaf(w, ml[j].y, L[k]);
+                O[k][0] = fmaf(w, lo[j].x, O[k][0]);
+                O[k][1] = fmaf(w, lo[j].y, O[k][1]);
+                O[k][2] = fmaf(w, lo[j].z, O[k][2]);
+                O[k][3] = fmaf(w, lo[j].w, O[k][3]);
+                O[k][4] = fmaf(w, hi[j].x, O[k][4]);
+                O[k][5] = fmaf(w, hi[j].y, O[k][5]);
+                O[k][6] = fmaf(w, hi[j].z, O[k][6]);
+                O[k][7] = fmaf(w, hi[j].w, O[k][7]);
+            }
+            M[k] = bm;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < EPL; ++k) {
+        const int e = lane + 64 * k;
+        if (e >= E) break;
+        const int g = e / (D / 8), c = e - g * (D / 8);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) lds_o[wave][g][8 * c + i] = O[k][i];
+        if (c == 0) {
+            lds_m[wave][g] = M[k];
+            lds_l[wave][g] = L[k];
+        }
+    }
+    __syncthreads();
+    const int H_q = a.n_kv_heads * G;
+    for (int idx = threadIdx.x; idx < G * D; idx += NW * 64) {
+        const int g = idx / D, d = idx - g * D;
+        float Mx = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) Mx = fmaxf(Mx, lds_m[w][g]);
+        float Ov = 0.f, Ls = 0.f;
+        if (Mx != -INFINITY) {
+#pragma unroll
+            for (int w = 0; w < NW; ++w) {
+                const float sc = fast_exp2(lds_m[w][g] - Mx);  // 0 for a wave without splits
+                Ov = fmaf(sc, lds_o[w][g][d], Ov);
+                Ls = fmaf(sc, lds_l[w][g], Ls);
             }
         }
-        float bm = M;
-#pragma unroll
-        for (int j = 0; j < kCombineBatch; ++j) bm = fmaxf(bm, em[j]);
-        if (bm == -INFINITY) continue;  // no valid key in the splits so far
-        const float corr = fast_exp2(M - bm);  // 0 while M = -inf
-        O *= corr;
-        Ls *= corr;
-#pragma unroll
-        for (int j = 0; j < kCombineBatch; ++j) {
-            const float w = fast_exp2(em[j] - bm);  // 0 for a split past n_splits
-            O = fmaf(w, v[j], O);
-            Ls = fmaf(w, el[j], Ls);
-        }
-        M = bm;
+        const size_t row = (size_t)b * H_q + h * G + g;
+        a.out[row * D + d] = f32_to_bf16_rne(Ls > 0.f ? Ov / Ls : 0.f);
+        if (d == 0 && a.lse != nullptr) a.lse[row] = Ls > 0.f ? (Mx + log2f(Ls)) * kLn2 : -INFINITY;
     }
-    const size_t row = (size_t)b * a.n_kv_heads * G + h * G + g;
-    a.out[row * D + d] = f32_to_bf16_rne(Ls > 0.f ? O / Ls : 0.f);
-    if (d == 0 && a.lse != nullptr) a.lse[row] = Ls > 0.f ? (M + log2f(Ls)) * kLn2 : -INFINITY;
 }
 
 template <int D, int G, int NW, bool PAGED>
@@ -581,19 +627,7 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
     }
     __syncthreads();
     if (!is_last) return;
-    for (int idx = threadIdx.x; idx < G * D; idx += NW * 64)
-        merge_splits<D, G, true>(a, unit, b, h, idx / D, idx % D, n_splits);
-}
-
-template <int D, int G>
-__global__ __launch_bounds__(D) void decode_combine_kernel(DecodeArgs a) {
-    const int unit = blockIdx.x;
-    const int b = unit / a.n_kv_heads;
-    const int h = unit - b * a.n_kv_heads;
-    const int L = clamp_len(a.lens[b], a.l_max);
-    const int n_splits = decode_split_count(L, a.chunk);
-    if (n_splits <= 1) return;  // written directly by the split kernel
-    merge_splits<D, G, false>(a, unit, b, h, blockIdx.y, threadIdx.x, n_splits);
+    merge_splits_parallel<D, G, NW>(a, unit, b, h, n_splits, lds_o, lds_m, lds_l);
 }
 
 // Waves per split work-group.  Up to G = 8 a wave fits in 256 registers, so 8-wave
@@ -606,6 +640,20 @@ constexpr int decode_waves_t() {
     return G <= 8 ? 8 : 4;
 }
 
+template <int D, int G, int NW>
+__global__ __launch_bounds__(NW * 64) void decode_combine_kernel(DecodeArgs a) {
+    const int unit = blockIdx.x;
+    const int b = unit / a.n_kv_heads;
+    const int h = unit - b * a.n_kv_heads;
+    const int L = clamp_len(a.lens[b], a.l_max);
+    const int n_splits = decode_split_count(L, a.chunk);
+    if (n_splits <= 1) return;  // written directly by the split kernel
+    __shared__ float lds_o[NW][G][D];
+    __shared__ float lds_m[NW][G];
+    __shared__ float lds_l[NW][G];
+    merge_splits_parallel<D, G, NW>(a, unit, b, h, n_splits, lds_o, lds_m, lds_l);
+}
+
 template <int D, int G>
 hipError_t launch_decode_t(const DecodeArgs& a, const Launch& l) {
     constexpr int NW = decode_waves_t<G>();
@@ -616,7 +664,8 @@ hipError_t launch_decode_t(const DecodeArgs& a, const Launch& l) {
 
 template <int D, int G>
 hipError_t launch_combine_t(const DecodeArgs& a, const Launch& l) {
-    return launch_kernel(decode_combine_kernel<D, G>, dim3(a.batch * a.n_kv_heads, G), dim3(D), l, a);
+    constexpr int NW = decode_waves_t<G>();
+    return launch_kernel(decode_combine_kernel<D, G, NW>, dim3(a.batch * a.n_kv_heads), dim3(NW * 64), l, a);
 }
 
 }  // namespace
