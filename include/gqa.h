@@ -330,8 +330,11 @@ int gqa_layer_qkv_device(gqa_ctx* ctx, int32_t b, const void* x, int32_t n_token
 int gqa_layer_times(gqa_ctx* ctx, float* out_us, int32_t n);
 
 /* ---- HIP graphs -------------------------------------------------------------------
- * No reference counterpart (the board's transaction is driven by CSR writes).  For
- * launch-bound serving loops (small batches): gqa_graph_capture_decode_append records one
+ * No reference counterpart (the board's transaction is driven by CSR writes).  For callers that
+ * must capture (a serving loop that replays a whole captured step, harnesses that only accept
+ * graphs): on this ROCm a replay costs the host more than the eager launches of the same step,
+ * so eager calls are the faster path (B1 x 4097 keys: 25-45 us per replayed step against 12.5 us
+ * eager, back to back).  gqa_graph_capture_decode_append records one
  * gqa_decode_append_device step (k_rows = v_rows = positions = NULL: gqa_decode_device) with
  * these device pointers into a HIP graph; gqa_graph_launch replays it on `stream` (NULL = the
  * context stream), reading q, rows, positions and ctx_lens and writing o, lse and the cache at
