@@ -10,18 +10,24 @@
 // for all G query heads of the GQA group, so every K/V byte is read from HBM once.
 //
 // Work decomposition inside a work-group: keys are taken in rounds of RK rows; wave w
-// owns rounds w, w+NW, ...  Per round a wave
-//   1. has the round's K and V rows in registers (coalesced 16-byte loads, 1 KiB per
-//      wave instruction) and prefetches the next round's rows behind the math;
-//   2. writes K to a wave-private, XOR-swizzled LDS tile and reads it back transposed so
+// owns rounds w, w+NW, ...  Per round a wave has the round's K and V rows in registers
+// (coalesced 16-byte loads, 1 KiB per wave instruction) and prefetches the next round's rows
+// behind the math.  Up to G = 4 (HBM-bound: the VALU work hides behind the loads) it
+//   1. writes K to a wave-private, XOR-swizzled LDS tile and reads it back transposed so
 //      that lane (g, k) owns the full dot product of head g with key k (v_dot2_f32_bf16,
 //      exact bf16 products, fp32 accumulation; no cross-lane reduction);
-//   3. updates the online softmax in the log2 domain (v_exp_f32) with a DPP max over the
+//   2. updates the online softmax in the log2 domain (v_exp_f32) with a DPP max over the
 //      lanes of a head, moving the running max only when a score passes it by 2^8;
-//   4. hands p to the PV layout through LDS and accumulates O in fp32 registers, lane
-//      (r, c) owning dims 8c..8c+7 of every head for rows r, r+RPL, ...  Up to G = 4 p
-//      stays fp32 (fp32 FMAs); from G = 8 on the PV FMAs would bound the kernel, so p is
-//      rounded to bf16 and v_dot2 takes two keys per instruction.
+//   3. hands p to the PV layout through LDS and accumulates O in fp32 registers, lane
+//      (r, c) owning dims 8c..8c+7 of every head for rows r, r+RPL, ...
+// From G = 8 on that VALU work would bound the kernel, so the products run on the matrix
+// cores: K and V go to two wave-private LDS tiles; S^T [16 keys x 16 heads] = K . Q^T is four
+// (D = 128) v_mfma_f32_16x16x32_bf16 with K read as operand A and Q^T held in registers (heads
+// past G are zero); its result leaves lane l the scores of keys 4(l/16) .. +3 of head l % 16,
+// which after the softmax (the same lazy log2-domain update, per lane) is exactly the B
+// operand of P^T, rounded to bf16 as on the board (attn_top.sv:653-658); O^T [D x 16] +=
+// V^T . P^T is eight v_mfma_f32_16x16x16_bf16 with V^T read by the transposing LDS read
+// (ds_read_b64_tr_b16).  l sums the fp32 p.
 // At the end the waves merge in LDS.  A sequence that fits in one split writes the
 // bf16 output directly; otherwise each split writes an fp32 partial (O, m, l) and the
 // splits merge with log-sum-exp weights: inside the launch, by the last split of the
@@ -110,6 +116,44 @@ __device__ __forceinline__ void unpack_bf16x8(const u32x4& w, float* v) {
         v[2 * i] = __uint_as_float(w[i] << 16);
         v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
     }
+}
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Matrix-core products of the G >= 8 path.  16x16 outputs: register i of lane l holds row
+// 4*(l/16) + i, column l % 16; operand A row / operand B column l % 16 with the k-values
+// KPL*(l/16) .. KPL*(l/16) + KPL-1 (KPL = 8 for k = 32, 4 for k = 16).
+__device__ __forceinline__ f32x4 mfma_16x16x32(const u32x4& a, const u32x4& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
+                                                   0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma_16x16x16(const u32x2& a, const u32x2& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4_t, a), __builtin_bit_cast(bf16x4_t, b),
+                                                     c, 0, 0, 0);
+}
+// Transposing LDS read: lane i of each 16-lane group receives element i % 4 of the 8-byte piece
+// addressed by lane 4j + i/4 of its group, for j = 0..3.
+__device__ __forceinline__ u32x2 lds_read_tr16(const void* p) {
+    typedef __attribute__((address_space(3))) i16x4_t lds_i16x4;
+    const i16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+    return __builtin_bit_cast(u32x2, v);
+}
+
+// LDS swizzles of the G >= 8 tiles (16 rows of D bf16).  K: the A-operand read covers rows 0..15
+// at one 16-byte chunk per 16 lanes, so the chunk is XORed with the row's position inside a
+// 256-byte bank period (D = 128: rows are 256 B; D = 64: two rows per period).  V: a transposing
+// read covers 8 keys per half-wave at one 32-byte run, so the run is XORed likewise.
+template <int D>
+__device__ __forceinline__ int mf_kswz(int row) {
+    return D == 128 ? (row & 15) : ((row >> 1) & 7);
+}
+template <int D>
+__device__ __forceinline__ int mf_vswz(int row) {
+    return D == 128 ? (row & 7) : ((row >> 1) & 3);
 }
 
 __device__ __forceinline__ int clamp_len(int len, int l_max) {
@@ -297,11 +341,11 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
     constexpr int RPL = 64 / NCH;            // rows covered by one wave-wide 1 KiB load
     constexpr int NLD = RK / RPL;            // wave loads per round, for K and for V
     constexpr int ROWS_PER_PERIOD = (2 * D >= 256) ? 1 : 256 / (2 * D);
-    // G >= 8: the PV product is VALU-bound, so P enters it as bf16 (as on the board,
-    // attn_top.sv:653-658) and one v_dot2 covers two keys; l still sums the fp32 p.
-    constexpr bool PBF16 = G >= 8;
+    // G >= 8: QK and PV run on the matrix cores (a VALU dot-product loop would bound the kernel),
+    // and P enters PV as bf16 (as on the board, attn_top.sv:653-658); l still sums the fp32 p.
+    constexpr bool MF = G >= 8;
     static_assert(NLD >= 1 && NSUB >= 1, "tile shape");
-    static_assert(!PBF16 || (NSUB % 2 == 0 && NLD % 2 == 0), "key pairs (row, row + RK/2) share a lane");
+    static_assert(!MF || (RK == 16 && G <= 16), "matrix-core rounds: 16 keys x up to 16 heads");
 
     const int split = blockIdx.x;
     const int h = blockIdx.y % a.n_kv_heads;
@@ -338,18 +382,32 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
         }
     }
 
-    __shared__ __attribute__((aligned(16))) u32x4 lds_k[NW][RK * NCH];
-    __shared__ __attribute__((aligned(16))) float lds_p[NW][RK * G];
-    uint32_t* const lds_pw = reinterpret_cast<uint32_t*>(&lds_p[wave][0]);  // bf16 pairs (G >= 8)
-    __shared__ float lds_o[NW][G][D];
+    // LDS: G <= 4, a K tile and the p values per wave, then the waves' O for the merge; G >= 8, a
+    // K and a V tile per wave, whose space the merge's O reuses once every wave is done with them.
+    constexpr int KV_TILE = 16 * NCH;  // 16-byte words of one 16-key K (or V) tile
+    constexpr size_t O_BYTES = sizeof(float) * NW * G * D;
+    constexpr size_t KV_BYTES = MF ? 16 * 2 * NW * KV_TILE : 0;
+    __shared__ __attribute__((aligned(16))) uint8_t lds_raw[KV_BYTES > O_BYTES ? KV_BYTES : O_BYTES];
+    float(*const lds_o)[G][D] = reinterpret_cast<float(*)[G][D]>(lds_raw);
+    u32x4* const lds_kv = reinterpret_cast<u32x4*>(lds_raw);
+    __shared__ __attribute__((aligned(16))) u32x4 lds_k[MF ? 1 : NW][RK * NCH];
+    __shared__ __attribute__((aligned(16))) float lds_p[MF ? 1 : NW][RK * G];
     __shared__ float lds_m[NW][G];
     __shared__ float lds_l[NW][G];
 
-    // QK layout: lane = gq * QKG + kk holds all of q[head gq] as bf16 pairs.
+    // QK layout (G <= 4): lane = gq * QKG + kk holds all of q[head gq] as bf16 pairs.
+    // G >= 8: lane l holds dims 32t + 8(l/16) .. +7 of head l % 16 for every t (the B operand of
+    // S^T = K Q^T; heads past G are zero).
     const int gq = lane / QKG;
     const int kk = lane - gq * QKG;
-    uint32_t qw[D / 2];
-    {
+    uint32_t qw[MF ? 1 : D / 2];
+    u32x4 qb[MF ? D / 32 : 1];
+    if constexpr (MF) {
+        const int hq = lane & 15;
+        const u32x4* qp = reinterpret_cast<const u32x4*>(a.q + ((size_t)b * H_q + h * G + (hq < G ? hq : 0)) * D);
+#pragma unroll
+        for (int t = 0; t < D / 32; ++t) qb[t] = hq < G ? qp[4 * t + (lane >> 4)] : u32x4{0u, 0u, 0u, 0u};
+    } else {
         const u32x4* qp = reinterpret_cast<const u32x4*>(a.q + ((size_t)b * H_q + h * G + gq) * D);
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
@@ -364,13 +422,20 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
     // PV layout: lane = rpv * NCH + cpv holds dims 8*cpv..8*cpv+7 of rows rpv + RPL*j.
     const int rpv = lane / NCH;
     const int cpv = lane - rpv * NCH;
-    float acc[G][8];
+    // G >= 8: o_acc[t] holds O^T rows (dims) 16t + 4(l/16) + i, column (head) l % 16.
+    float acc[MF ? 1 : G][8];
+    f32x4 o_acc[MF ? D / 16 : 1];
+    if constexpr (MF) {
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+        for (int t = 0; t < D / 16; ++t) o_acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    } else {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[g][i] = 0.f;
-    float m_run = -INFINITY;  // running max (log2 units) of head gq, uniform over its lanes
-    float l_lane = 0.f;       // this lane's share of the running sum of head gq
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[g][i] = 0.f;
+    }
+    float m_run = -INFINITY;  // running max (log2 units) of this lane's head, uniform over its lanes
+    float l_lane = 0.f;       // this lane's share of the running sum of its head
 
     const u32x4* kbase = reinterpret_cast<const u32x4*>(a.kc) + (PAGED ? 0 : row0 * NCH);
     const u32x4* vbase = reinterpret_cast<const u32x4*>(a.vc) + (PAGED ? 0 : row0 * NCH);
@@ -443,130 +508,180 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
     if (r < n_rounds) load_round(k_begin + r * RK, kr, vr);
     for (; r < n_rounds; r += NW) {
         const int key0 = k_begin + r * RK;
-        // 1. K -> LDS, swizzled so that the transposed reads below are conflict-free.
-#pragma unroll
-        for (int j = 0; j < NLD; ++j) {
-            const int row = j * RPL + rpv;
-            lds_k[wave][row * NCH + (cpv ^ ((row / ROWS_PER_PERIOD) % NCH))] = kr[j];
-        }
-        u32x4 vcur[NLD];
-#pragma unroll
-        for (int j = 0; j < NLD; ++j) vcur[j] = vr[j];
-        // Prefetch the next round of this wave.
-        if (r + NW < n_rounds) load_round(key0 + NW * RK, kr, vr);
-        wave_lds_sync();
-
-        // 2. Scores: lane (gq, kk) dots q[gq] with key row sub*QKG + kk.
-        float s[NSUB];
-#pragma unroll
-        for (int sub = 0; sub < NSUB; ++sub) {
-            const int row = sub * QKG + kk;
-            const int swz = (row / ROWS_PER_PERIOD) % NCH;
-            float dot = 0.f;
-#pragma unroll
-            for (int c = 0; c < NCH; ++c) {
-                const u32x4 kw = lds_k[wave][row * NCH + (c ^ swz)];
-                dot = dot2_bf16(qw[4 * c + 0], kw[0], dot);
-                dot = dot2_bf16(qw[4 * c + 1], kw[1], dot);
-                dot = dot2_bf16(qw[4 * c + 2], kw[2], dot);
-                dot = dot2_bf16(qw[4 * c + 3], kw[3], dot);
-            }
-            s[sub] = (key0 + row < k_end) ? dot * a.scale_log2 : -INFINITY;
-        }
-
-        // 3. Online softmax for head gq, rescaled lazily (kRescaleSlack): the branch is
-        //    wave-uniform and, when taken, moves every head of the wave to its current max.
-        float mx = s[0];
-#pragma unroll
-        for (int sub = 1; sub < NSUB; ++sub) mx = fmaxf(mx, s[sub]);
-        mx = group_max<QKG>(mx);
-        const float m_cand = fmaxf(m_run, mx);
-        if (__ballot(m_cand > m_run + kRescaleSlack) != 0) {
-            // m_cand == -inf: every key of this head so far is masked and O, l are still 0.
-            const float corr = (m_cand == -INFINITY) ? 1.f : fast_exp2(m_run - m_cand);
-            m_run = m_cand;
-            l_lane *= corr;
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const float cg = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(corr), g * QKG));
-#pragma unroll
-                for (int i = 0; i < 8; ++i) acc[g][i] *= cg;
-            }
-        }
-        float p[NSUB];
-        float psum = 0.f;
-#pragma unroll
-        for (int sub = 0; sub < NSUB; ++sub) {
-            p[sub] = (s[sub] == -INFINITY) ? 0.f : fast_exp2(s[sub] - m_run);
-            psum += p[sub];
-        }
-        l_lane += psum;
-        if constexpr (PBF16) {
-            // Word [row][g] = bf16 p of (row, head g) and of (row + RK/2, head g).
-#pragma unroll
-            for (int sub = 0; sub < NSUB / 2; ++sub)
-                lds_pw[(sub * QKG + kk) * G + gq] = pack_bf16x2(p[sub], p[sub + NSUB / 2]);
-        } else {
-#pragma unroll
-            for (int sub = 0; sub < NSUB; ++sub) lds_p[wave][(sub * QKG + kk) * G + gq] = p[sub];
-        }
-        wave_lds_sync();
-
-        // 4. O += p * V in the PV layout.
-        if constexpr (PBF16) {
-            // Rows j and j + NLD/2 of this lane are keys row and row + RK/2: one v_dot2 per
-            // (head, dim) takes both, on bf16 p and the V halves paired by v_perm.
-#pragma unroll
-            for (int j = 0; j < NLD / 2; ++j) {
-                const int row = j * RPL + rpv;
-                uint32_t pp[G];
-#pragma unroll
-                for (int g = 0; g < G; ++g) pp[g] = lds_pw[row * G + g];
-#pragma unroll
-                for (int w = 0; w < 4; ++w) {
-                    const uint32_t lo = pair_lo(vcur[j][w], vcur[j + NLD / 2][w]);
-                    const uint32_t hi = pair_hi(vcur[j][w], vcur[j + NLD / 2][w]);
-#pragma unroll
-                    for (int g = 0; g < G; ++g) {
-                        acc[g][2 * w] = dot2_bf16(lo, pp[g], acc[g][2 * w]);
-                        acc[g][2 * w + 1] = dot2_bf16(hi, pp[g], acc[g][2 * w + 1]);
-                    }
-                }
-            }
-        } else {
+        if constexpr (MF) {
+            // K and V rows of the round into the wave's two LDS tiles: K swizzled so that the
+            // A-operand reads below (row l % 16, 16 bytes) are conflict-free, V in 32-byte runs
+            // swizzled so that a transposing read's 8 keys of one half-wave hit 8 different runs.
+            u32x4* const tk = lds_kv + (size_t)(2 * wave) * KV_TILE;
+            u32x4* const tv = tk + KV_TILE;
 #pragma unroll
             for (int j = 0; j < NLD; ++j) {
                 const int row = j * RPL + rpv;
-                float pv[G];
+                tk[row * NCH + (cpv ^ mf_kswz<D>(row))] = kr[j];
+                tv[row * NCH + 2 * ((cpv >> 1) ^ mf_vswz<D>(row)) + (cpv & 1)] = vr[j];
+            }
+            // Prefetch the next round of this wave.
+            if (r + NW < n_rounds) load_round(key0 + NW * RK, kr, vr);
+            wave_lds_sync();
+
+            // 2. S^T [16 keys x 16 heads] = K [16 x D] . Q^T [D x 16]: lane l gets keys
+            //    4(l/16) .. +3 of head l % 16.
+            const int m16 = lane & 15, grp = lane >> 4;
+            f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
+            for (int t = 0; t < D / 32; ++t)
+                sacc = mfma_16x16x32(tk[m16 * NCH + ((4 * t + grp) ^ mf_kswz<D>(m16))], qb[t], sacc);
+
+            // 3. Online softmax of head l % 16 over its 16 keys (4 per lane, 4 lanes), rescaled
+            //    lazily as below.
+            float sv[4];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                sv[i] = (key0 + 4 * grp + i < k_end) ? sacc[i] * a.scale_log2 : -INFINITY;
+                mx = fmaxf(mx, sv[i]);
+            }
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const float m_cand = fmaxf(m_run, mx);
+            if (__ballot(m_cand > m_run + kRescaleSlack) != 0) {
+                const float corr = (m_cand == -INFINITY) ? 1.f : fast_exp2(m_run - m_cand);
+                m_run = m_cand;
+                l_lane *= corr;
+#pragma unroll
+                for (int t = 0; t < D / 16; ++t) o_acc[t] *= corr;
+            }
+            float pf[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                pf[i] = (sv[i] == -INFINITY) ? 0.f : fast_exp2(sv[i] - m_run);
+                l_lane += pf[i];
+            }
+            // The S^T result layout is the B-operand layout of P^T (keys 4(l/16) .. +3, head l % 16).
+            const u32x2 pb = {pack_bf16x2(pf[0], pf[1]), pack_bf16x2(pf[2], pf[3])};
+
+            // 4. O^T [D x 16 heads] += V^T [D x 16 keys] . P^T: per 16-dim tile, lane l of half-wave
+            //    group g addresses key 4g + (l%16)/4, dims 16t + 4(l%4) .. +3 and receives dim
+            //    16t + l % 16 of keys 4g .. 4g + 3.
+            const int vkey = 4 * grp + (m16 >> 2);
+            const uint8_t* const vrow = reinterpret_cast<const uint8_t*>(tv + vkey * NCH) + 8 * (lane & 3);
+#pragma unroll
+            for (int t = 0; t < D / 16; ++t)
+                o_acc[t] = mfma_16x16x16(lds_read_tr16(vrow + 32 * (t ^ mf_vswz<D>(vkey))), pb, o_acc[t]);
+        } else {
+            // 1. K -> LDS, swizzled so that the transposed reads below are conflict-free.
+    #pragma unroll
+            for (int j = 0; j < NLD; ++j) {
+                const int row = j * RPL + rpv;
+                lds_k[wave][row * NCH + (cpv ^ ((row / ROWS_PER_PERIOD) % NCH))] = kr[j];
+            }
+            u32x4 vcur[NLD];
+    #pragma unroll
+            for (int j = 0; j < NLD; ++j) vcur[j] = vr[j];
+            // Prefetch the next round of this wave.
+            if (r + NW < n_rounds) load_round(key0 + NW * RK, kr, vr);
+            wave_lds_sync();
+
+            // 2. Scores: lane (gq, kk) dots q[gq] with key row sub*QKG + kk.
+            float s[NSUB];
+    #pragma unroll
+            for (int sub = 0; sub < NSUB; ++sub) {
+                const int row = sub * QKG + kk;
+                const int swz = (row / ROWS_PER_PERIOD) % NCH;
+                float dot = 0.f;
+    #pragma unroll
+                for (int c = 0; c < NCH; ++c) {
+                    const u32x4 kw = lds_k[wave][row * NCH + (c ^ swz)];
+                    dot = dot2_bf16(qw[4 * c + 0], kw[0], dot);
+                    dot = dot2_bf16(qw[4 * c + 1], kw[1], dot);
+                    dot = dot2_bf16(qw[4 * c + 2], kw[2], dot);
+                    dot = dot2_bf16(qw[4 * c + 3], kw[3], dot);
+                }
+                s[sub] = (key0 + row < k_end) ? dot * a.scale_log2 : -INFINITY;
+            }
+
+            // 3. Online softmax for head gq, rescaled lazily (kRescaleSlack): the branch is
+            //    wave-uniform and, when taken, moves every head of the wave to its current max.
+            float mx = s[0];
+    #pragma unroll
+            for (int sub = 1; sub < NSUB; ++sub) mx = fmaxf(mx, s[sub]);
+            mx = group_max<QKG>(mx);
+            const float m_cand = fmaxf(m_run, mx);
+            if (__ballot(m_cand > m_run + kRescaleSlack) != 0) {
+                // m_cand == -inf: every key of this head so far is masked and O, l are still 0.
+                const float corr = (m_cand == -INFINITY) ? 1.f : fast_exp2(m_run - m_cand);
+                m_run = m_cand;
+                l_lane *= corr;
+    #pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    const float cg = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(corr), g * QKG));
+    #pragma unroll
+                    for (int i = 0; i < 8; ++i) acc[g][i] *= cg;
+                }
+            }
+            float p[NSUB];
+            float psum = 0.f;
+    #pragma unroll
+            for (int sub = 0; sub < NSUB; ++sub) {
+                p[sub] = (s[sub] == -INFINITY) ? 0.f : fast_exp2(s[sub] - m_run);
+                psum += p[sub];
+            }
+            l_lane += psum;
+    #pragma unroll
+            for (int sub = 0; sub < NSUB; ++sub) lds_p[wave][(sub * QKG + kk) * G + gq] = p[sub];
+            wave_lds_sync();
+
+            // 4. O += p * V in the PV layout.
+    #pragma unroll
+            for (int j = 0; j < NLD; ++j) {
+                const int row = j * RPL + rpv;
+                float pv[G];
+    #pragma unroll
                 for (int g = 0; g < G; ++g) pv[g] = lds_p[wave][row * G + g];
                 float v[8];
                 unpack_bf16x8(vcur[j], v);
-#pragma unroll
+    #pragma unroll
                 for (int g = 0; g < G; ++g)
-#pragma unroll
+    #pragma unroll
                     for (int i = 0; i < 8; ++i) acc[g][i] = fmaf(pv[g], v[i], acc[g][i]);
             }
         }
     }
 
     // ---- merge the waves of this work-group ----
-    const float l_head = group_sum<QKG>(l_lane);
+    if constexpr (MF) {
+        __syncthreads();  // every wave is done with its K/V tiles, whose space lds_o reuses
+        float l_head = l_lane + __shfl_xor(l_lane, 16);
+        l_head += __shfl_xor(l_head, 32);
+        const int hq = lane & 15, grp = lane >> 4;
+        if (hq < G) {
 #pragma unroll
-    for (int off = NCH; off < 64; off <<= 1)
+            for (int t = 0; t < D / 16; ++t)
 #pragma unroll
-        for (int g = 0; g < G; ++g)
+                for (int i = 0; i < 4; ++i) lds_o[wave][hq][16 * t + 4 * grp + i] = o_acc[t][i];
+            if (grp == 0) {
+                lds_m[wave][hq] = m_run;
+                lds_l[wave][hq] = l_head;
+            }
+        }
+    } else {
+        const float l_head = group_sum<QKG>(l_lane);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) acc[g][i] += __shfl_xor(acc[g][i], off);
-    if (rpv == 0) {
+        for (int off = NCH; off < 64; off <<= 1)
 #pragma unroll
-        for (int g = 0; g < G; ++g)
+            for (int g = 0; g < G; ++g)
 #pragma unroll
-            for (int i = 0; i < 8; ++i) lds_o[wave][g][cpv * 8 + i] = acc[g][i];
-    }
-    if (kk == 0) {
-        lds_m[wave][gq] = m_run;
-        lds_l[wave][gq] = l_head;
+                for (int i = 0; i < 8; ++i) acc[g][i] += __shfl_xor(acc[g][i], off);
+        if (rpv == 0) {
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) lds_o[wave][g][cpv * 8 + i] = acc[g][i];
+        }
+        if (kk == 0) {
+            lds_m[wave][gq] = m_run;
+            lds_l[wave][gq] = l_head;
+        }
     }
     __syncthreads();
 
