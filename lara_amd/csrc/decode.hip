@@ -12,7 +12,7 @@
 // Work decomposition inside a work-group: keys are taken in rounds of RK rows; wave w
 // owns rounds w, w+NW, ...  Per round a wave has the round's K and V rows in registers
 // (coalesced 16-byte loads, 1 KiB per wave instruction) and prefetches the next round's rows
-// behind the math.  Up to G = 4 (HBM-bound: the VALU work hides behind the loads) it
+// behind the math.  For G = 2 it
 //   1. writes K to a wave-private, XOR-swizzled LDS tile and reads it back transposed so
 //      that lane (g, k) owns the full dot product of head g with key k (v_dot2_f32_bf16,
 //      exact bf16 products, fp32 accumulation; no cross-lane reduction);
@@ -20,8 +20,8 @@
 //      lanes of a head, moving the running max only when a score passes it by 2^8;
 //   3. hands p to the PV layout through LDS and accumulates O in fp32 registers, lane
 //      (r, c) owning dims 8c..8c+7 of every head for rows r, r+RPL, ...
-// From G = 8 on that VALU work would bound the kernel, so the products run on the matrix
-// cores: K and V go to two wave-private LDS tiles; S^T [16 keys x 16 heads] = K . Q^T is four
+// From G = 4 on the products run on the matrix cores (at G = 8 the VALU loop bounded the kernel,
+// and at G = 4 the matrix-core form streams faster as well): K and V go to two wave-private LDS tiles; S^T [16 keys x 16 heads] = K . Q^T is four
 // (D = 128) v_mfma_f32_16x16x32_bf16 with K read as operand A and Q^T held in registers (heads
 // past G are zero); its result leaves lane l the scores of keys 4(l/16) .. +3 of head l % 16,
 // which after the softmax (the same lazy log2-domain update, per lane) is exactly the B
@@ -341,9 +341,10 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
     constexpr int RPL = 64 / NCH;            // rows covered by one wave-wide 1 KiB load
     constexpr int NLD = RK / RPL;            // wave loads per round, for K and for V
     constexpr int ROWS_PER_PERIOD = (2 * D >= 256) ? 1 : 256 / (2 * D);
-    // G >= 8: QK and PV run on the matrix cores (a VALU dot-product loop would bound the kernel),
-    // and P enters PV as bf16 (as on the board, attn_top.sv:653-658); l still sums the fp32 p.
-    constexpr bool MF = G >= 8;
+    // G >= 4: QK and PV run on the matrix cores (G >= 8: a VALU dot-product loop would bound the
+    // kernel; G = 4: measured faster too), and P enters PV as bf16 (as on the board,
+    // attn_top.sv:653-658); l still sums the fp32 p.
+    constexpr bool MF = G >= 4;
     static_assert(NLD >= 1 && NSUB >= 1, "tile shape");
     static_assert(!MF || (RK == 16 && G <= 16), "matrix-core rounds: 16 keys x up to 16 heads");
 
@@ -382,7 +383,7 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
         }
     }
 
-    // LDS: G <= 4, a K tile and the p values per wave, then the waves' O for the merge; G >= 8, a
+    // LDS: G = 2, a K tile and the p values per wave, then the waves' O for the merge; G >= 4, a
     // K and a V tile per wave, whose space the merge's O reuses once every wave is done with them.
     constexpr int KV_TILE = 16 * NCH;  // 16-byte words of one 16-key K (or V) tile
     constexpr size_t O_BYTES = sizeof(float) * NW * G * D;
@@ -395,8 +396,8 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
     __shared__ float lds_m[NW][G];
     __shared__ float lds_l[NW][G];
 
-    // QK layout (G <= 4): lane = gq * QKG + kk holds all of q[head gq] as bf16 pairs.
-    // G >= 8: lane l holds dims 32t + 8(l/16) .. +7 of head l % 16 for every t (the B operand of
+    // QK layout (G = 2): lane = gq * QKG + kk holds all of q[head gq] as bf16 pairs.
+    // G >= 4: lane l holds dims 32t + 8(l/16) .. +7 of head l % 16 for every t (the B operand of
     // S^T = K Q^T; heads past G are zero).
     const int gq = lane / QKG;
     const int kk = lane - gq * QKG;
@@ -422,7 +423,7 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
     // PV layout: lane = rpv * NCH + cpv holds dims 8*cpv..8*cpv+7 of rows rpv + RPL*j.
     const int rpv = lane / NCH;
     const int cpv = lane - rpv * NCH;
-    // G >= 8: o_acc[t] holds O^T rows (dims) 16t + 4(l/16) + i, column (head) l % 16.
+    // G >= 4: o_acc[t] holds O^T rows (dims) 16t + 4(l/16) + i, column (head) l % 16.
     float acc[MF ? 1 : G][8];
     f32x4 o_acc[MF ? D / 16 : 1];
     if constexpr (MF) {
