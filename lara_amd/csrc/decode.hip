@@ -9,25 +9,18 @@
 // NW waves owns a contiguous chunk of keys of one (sequence, kv head) -- a "split" --
 // for all G query heads of the GQA group, so every K/V byte is read from HBM once.
 //
-// Work decomposition inside a work-group: keys are taken in rounds of RK rows; wave w
-// owns rounds w, w+NW, ...  Per round a wave has the round's K and V rows in registers
-// (coalesced 16-byte loads, 1 KiB per wave instruction) and prefetches the next round's rows
-// behind the math.  For G = 2 it
-//   1. writes K to a wave-private, XOR-swizzled LDS tile and reads it back transposed so
-//      that lane (g, k) owns the full dot product of head g with key k (v_dot2_f32_bf16,
-//      exact bf16 products, fp32 accumulation; no cross-lane reduction);
-//   2. updates the online softmax in the log2 domain (v_exp_f32) with a DPP max over the
-//      lanes of a head, moving the running max only when a score passes it by 2^8;
-//   3. hands p to the PV layout through LDS and accumulates O in fp32 registers, lane
-//      (r, c) owning dims 8c..8c+7 of every head for rows r, r+RPL, ...
-// From G = 4 on the products run on the matrix cores (at G = 8 the VALU loop bounded the kernel,
-// and at G = 4 the matrix-core form streams faster as well): K and V go to two wave-private LDS tiles; S^T [16 keys x 16 heads] = K . Q^T is four
-// (D = 128) v_mfma_f32_16x16x32_bf16 with K read as operand A and Q^T held in registers (heads
-// past G are zero); its result leaves lane l the scores of keys 4(l/16) .. +3 of head l % 16,
-// which after the softmax (the same lazy log2-domain update, per lane) is exactly the B
+// Work decomposition inside a work-group: keys are taken in rounds of 16 rows; wave w owns
+// rounds w, w+NW, ...  Per round a wave has the round's K and V rows in registers (coalesced
+// 16-byte loads, 1 KiB per wave instruction) and prefetches the next round's rows behind the
+// math; the products run on the matrix cores: K and V go to two wave-private LDS tiles;
+// S^T [16 keys x 16 heads] = K . Q^T is D/32 v_mfma_f32_16x16x32_bf16 with K read as operand A
+// and Q^T held in registers (heads past G are zero); its result leaves lane l the scores of keys
+// 4(l/16) .. +3 of head l % 16, so the online softmax (log2 domain, v_exp_f32, the running max
+// moved only when a score passes it by 2^8) runs per lane, and its p values are exactly the B
 // operand of P^T, rounded to bf16 as on the board (attn_top.sv:653-658); O^T [D x 16] +=
-// V^T . P^T is eight v_mfma_f32_16x16x16_bf16 with V^T read by the transposing LDS read
-// (ds_read_b64_tr_b16).  l sums the fp32 p.
+// V^T . P^T is D/16 v_mfma_f32_16x16x16_bf16 with V^T read by the transposing LDS read
+// (ds_read_b64_tr_b16).  l sums the fp32 p.  (A VALU form -- v_dot2 dot products over a
+// transposed K tile, FMAs for PV -- bounded the kernel at G = 8 and streamed slower at G = 4.)
 // At the end the waves merge in LDS.  A sequence that fits in one split writes the
 // bf16 output directly; otherwise each split writes an fp32 partial (O, m, l) and the
 // splits merge with log-sum-exp weights: inside the launch, by the last split of the
@@ -58,50 +51,12 @@ constexpr float kLn2 = 0.693147180559945309f;
 // rescale of O.  The result is the same softmax; only fp32 rounding differs.
 constexpr float kRescaleSlack = 8.0f;
 
-__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
-                                           __builtin_bit_cast(bf16x2_t, b), c, false);
-}
-
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     const bf16x2_t v = {(__bf16)lo, (__bf16)hi};  // v_cvt_pk_bf16_f32, round to nearest even
     return __builtin_bit_cast(uint32_t, v);
 }
 
-// Two bf16 words -> (lo half of a, lo half of b) and (hi half of a, hi half of b).
-__device__ __forceinline__ uint32_t pair_lo(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
-__device__ __forceinline__ uint32_t pair_hi(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
-
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
-template <int CTRL>
-__device__ __forceinline__ float dpp(float x) {
-    return __builtin_amdgcn_update_dpp(0.0f, x, CTRL, 0xF, 0xF, false);
-}
-
-// All-reduce over aligned groups of W consecutive lanes, W in {4, 8, 16, 32}.
-template <int W>
-__device__ __forceinline__ float group_max(float x) {
-    static_assert(W == 4 || W == 8 || W == 16 || W == 32, "group width");
-    x = fmaxf(x, dpp<0xB1>(x));                       // quad_perm [1,0,3,2]
-    x = fmaxf(x, dpp<0x4E>(x));                       // quad_perm [2,3,0,1]
-    if constexpr (W >= 8) x = fmaxf(x, dpp<0x141>(x)); // row_half_mirror
-    if constexpr (W >= 16) x = fmaxf(x, dpp<0x140>(x)); // row_mirror
-    if constexpr (W >= 32)
-        x = fmaxf(x, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x401F)));
-    return x;
-}
-
-template <int W>
-__device__ __forceinline__ float group_sum(float x) {
-    static_assert(W == 4 || W == 8 || W == 16 || W == 32, "group width");
-    x += dpp<0xB1>(x);
-    x += dpp<0x4E>(x);
-    if constexpr (W >= 8) x += dpp<0x141>(x);
-    if constexpr (W >= 16) x += dpp<0x140>(x);
-    if constexpr (W >= 32) x += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x401F));
-    return x;
-}
 
 // Orders a wave's LDS writes before its subsequent LDS reads of other lanes' data.
 __device__ __forceinline__ void wave_lds_sync() {
@@ -110,21 +65,13 @@ __device__ __forceinline__ void wave_lds_sync() {
     asm volatile("" ::: "memory");
 }
 
-__device__ __forceinline__ void unpack_bf16x8(const u32x4& w, float* v) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        v[2 * i] = __uint_as_float(w[i] << 16);
-        v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
-    }
-}
-
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-// Matrix-core products of the G >= 8 path.  16x16 outputs: register i of lane l holds row
+// Matrix-core products of the decode rounds.  16x16 outputs: register i of lane l holds row
 // 4*(l/16) + i, column l % 16; operand A row / operand B column l % 16 with the k-values
 // KPL*(l/16) .. KPL*(l/16) + KPL-1 (KPL = 8 for k = 32, 4 for k = 16).
 __device__ __forceinline__ f32x4 mfma_16x16x32(const u32x4& a, const u32x4& b, const f32x4& c) {
@@ -143,7 +90,7 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const void* p) {
     return __builtin_bit_cast(u32x2, v);
 }
 
-// LDS swizzles of the G >= 8 tiles (16 rows of D bf16).  K: the A-operand read covers rows 0..15
+// LDS swizzles of the round tiles (16 rows of D bf16).  K: the A-operand read covers rows 0..15
 // at one 16-byte chunk per 16 lanes, so the chunk is XORed with the row's position inside a
 // 256-byte bank period (D = 128: rows are 256 B; D = 64: two rows per period).  V: a transposing
 // read covers 8 keys per half-wave at one 32-byte run, so the run is XORed likewise.
@@ -334,19 +281,11 @@ __device__ __forceinline__ void merge_splits_parallel(const DecodeArgs& a, int u
 
 template <int D, int G, int NW, bool PAGED>
 __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
-    constexpr int NCH = D / 8;               // 16-byte words per K/V row
-    constexpr int QKG = 64 / G;              // lanes (keys) per head in the QK layout
-    constexpr int RK = QKG > 16 ? QKG : 16;  // keys per wave round
-    constexpr int NSUB = RK / QKG;           // QK sub-rounds per round
-    constexpr int RPL = 64 / NCH;            // rows covered by one wave-wide 1 KiB load
-    constexpr int NLD = RK / RPL;            // wave loads per round, for K and for V
-    constexpr int ROWS_PER_PERIOD = (2 * D >= 256) ? 1 : 256 / (2 * D);
-    // G >= 4: QK and PV run on the matrix cores (G >= 8: a VALU dot-product loop would bound the
-    // kernel; G = 4: measured faster too), and P enters PV as bf16 (as on the board,
-    // attn_top.sv:653-658); l still sums the fp32 p.
-    constexpr bool MF = G >= 4;
-    static_assert(NLD >= 1 && NSUB >= 1, "tile shape");
-    static_assert(!MF || (RK == 16 && G <= 16), "matrix-core rounds: 16 keys x up to 16 heads");
+    constexpr int NCH = D / 8;           // 16-byte words per K/V row
+    constexpr int RK = 16;               // keys per wave round
+    constexpr int RPL = 64 / NCH;        // rows covered by one wave-wide 1 KiB load
+    constexpr int NLD = RK / RPL;        // wave loads per round, for K and for V
+    static_assert(NLD >= 1 && G <= 16, "16-key rounds, up to 16 heads per group");
 
     const int split = blockIdx.x;
     const int h = blockIdx.y % a.n_kv_heads;
@@ -383,58 +322,31 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
         }
     }
 
-    // LDS: G = 2, a K tile and the p values per wave, then the waves' O for the merge; G >= 4, a
-    // K and a V tile per wave, whose space the merge's O reuses once every wave is done with them.
-    constexpr int KV_TILE = 16 * NCH;  // 16-byte words of one 16-key K (or V) tile
+    // LDS: a K and a V tile per wave; the merge's O reuses their space once every wave is done.
+    constexpr int KV_TILE = RK * NCH;  // 16-byte words of one K (or V) tile
     constexpr size_t O_BYTES = sizeof(float) * NW * G * D;
-    constexpr size_t KV_BYTES = MF ? 16 * 2 * NW * KV_TILE : 0;
+    constexpr size_t KV_BYTES = 16 * 2 * NW * KV_TILE;
     __shared__ __attribute__((aligned(16))) uint8_t lds_raw[KV_BYTES > O_BYTES ? KV_BYTES : O_BYTES];
     float(*const lds_o)[G][D] = reinterpret_cast<float(*)[G][D]>(lds_raw);
     u32x4* const lds_kv = reinterpret_cast<u32x4*>(lds_raw);
-    __shared__ __attribute__((aligned(16))) u32x4 lds_k[MF ? 1 : NW][RK * NCH];
-    __shared__ __attribute__((aligned(16))) float lds_p[MF ? 1 : NW][RK * G];
     __shared__ float lds_m[NW][G];
     __shared__ float lds_l[NW][G];
 
-    // QK layout (G = 2): lane = gq * QKG + kk holds all of q[head gq] as bf16 pairs.
-    // G >= 4: lane l holds dims 32t + 8(l/16) .. +7 of head l % 16 for every t (the B operand of
-    // S^T = K Q^T; heads past G are zero).
-    const int gq = lane / QKG;
-    const int kk = lane - gq * QKG;
-    uint32_t qw[MF ? 1 : D / 2];
-    u32x4 qb[MF ? D / 32 : 1];
-    if constexpr (MF) {
+    // Q^T operand: lane l holds dims 32t + 8(l/16) .. +7 of head l % 16 for every t (heads past G
+    // are zero).  O^T accumulators: o_acc[t] holds rows (dims) 16t + 4(l/16) + i, column (head)
+    // l % 16.  Lane (cpv, rpv) of the loads holds 16-byte chunk cpv of rows rpv, rpv + RPL, ...
+    u32x4 qb[D / 32];
+    {
         const int hq = lane & 15;
         const u32x4* qp = reinterpret_cast<const u32x4*>(a.q + ((size_t)b * H_q + h * G + (hq < G ? hq : 0)) * D);
 #pragma unroll
         for (int t = 0; t < D / 32; ++t) qb[t] = hq < G ? qp[4 * t + (lane >> 4)] : u32x4{0u, 0u, 0u, 0u};
-    } else {
-        const u32x4* qp = reinterpret_cast<const u32x4*>(a.q + ((size_t)b * H_q + h * G + gq) * D);
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-            const u32x4 t = qp[c];
-            qw[4 * c + 0] = t[0];
-            qw[4 * c + 1] = t[1];
-            qw[4 * c + 2] = t[2];
-            qw[4 * c + 3] = t[3];
-        }
     }
-
-    // PV layout: lane = rpv * NCH + cpv holds dims 8*cpv..8*cpv+7 of rows rpv + RPL*j.
     const int rpv = lane / NCH;
     const int cpv = lane - rpv * NCH;
-    // G >= 4: o_acc[t] holds O^T rows (dims) 16t + 4(l/16) + i, column (head) l % 16.
-    float acc[MF ? 1 : G][8];
-    f32x4 o_acc[MF ? D / 16 : 1];
-    if constexpr (MF) {
+    f32x4 o_acc[D / 16];
 #pragma unroll
-        for (int t = 0; t < D / 16; ++t) o_acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    } else {
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-#pragma unroll
-            for (int i = 0; i < 8; ++i) acc[g][i] = 0.f;
-    }
+    for (int t = 0; t < D / 16; ++t) o_acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m_run = -INFINITY;  // running max (log2 units) of this lane's head, uniform over its lanes
     float l_lane = 0.f;       // this lane's share of the running sum of its head
 
@@ -509,149 +421,70 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
     if (r < n_rounds) load_round(k_begin + r * RK, kr, vr);
     for (; r < n_rounds; r += NW) {
         const int key0 = k_begin + r * RK;
-        if constexpr (MF) {
-            // K and V rows of the round into the wave's two LDS tiles: K swizzled so that the
-            // A-operand reads below (row l % 16, 16 bytes) are conflict-free, V in 32-byte runs
-            // swizzled so that a transposing read's 8 keys of one half-wave hit 8 different runs.
-            u32x4* const tk = lds_kv + (size_t)(2 * wave) * KV_TILE;
-            u32x4* const tv = tk + KV_TILE;
+        // K and V rows of the round into the wave's two LDS tiles: K swizzled so that the
+        // A-operand reads below (row l % 16, 16 bytes) are conflict-free, V in 32-byte runs
+        // swizzled so that a transposing read's 8 keys of one half-wave hit 8 different runs.
+        u32x4* const tk = lds_kv + (size_t)(2 * wave) * KV_TILE;
+        u32x4* const tv = tk + KV_TILE;
 #pragma unroll
-            for (int j = 0; j < NLD; ++j) {
-                const int row = j * RPL + rpv;
-                tk[row * NCH + (cpv ^ mf_kswz<D>(row))] = kr[j];
-                tv[row * NCH + 2 * ((cpv >> 1) ^ mf_vswz<D>(row)) + (cpv & 1)] = vr[j];
-            }
-            // Prefetch the next round of this wave.
-            if (r + NW < n_rounds) load_round(key0 + NW * RK, kr, vr);
-            wave_lds_sync();
-
-            // 2. S^T [16 keys x 16 heads] = K [16 x D] . Q^T [D x 16]: lane l gets keys
-            //    4(l/16) .. +3 of head l % 16.
-            const int m16 = lane & 15, grp = lane >> 4;
-            f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int t = 0; t < D / 32; ++t)
-                sacc = mfma_16x16x32(tk[m16 * NCH + ((4 * t + grp) ^ mf_kswz<D>(m16))], qb[t], sacc);
-
-            // 3. Online softmax of head l % 16 over its 16 keys (4 per lane, 4 lanes), rescaled
-            //    lazily as below.
-            float sv[4];
-            float mx = -INFINITY;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                sv[i] = (key0 + 4 * grp + i < k_end) ? sacc[i] * a.scale_log2 : -INFINITY;
-                mx = fmaxf(mx, sv[i]);
-            }
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const float m_cand = fmaxf(m_run, mx);
-            if (__ballot(m_cand > m_run + kRescaleSlack) != 0) {
-                const float corr = (m_cand == -INFINITY) ? 1.f : fast_exp2(m_run - m_cand);
-                m_run = m_cand;
-                l_lane *= corr;
-#pragma unroll
-                for (int t = 0; t < D / 16; ++t) o_acc[t] *= corr;
-            }
-            float pf[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                pf[i] = (sv[i] == -INFINITY) ? 0.f : fast_exp2(sv[i] - m_run);
-                l_lane += pf[i];
-            }
-            // The S^T result layout is the B-operand layout of P^T (keys 4(l/16) .. +3, head l % 16).
-            const u32x2 pb = {pack_bf16x2(pf[0], pf[1]), pack_bf16x2(pf[2], pf[3])};
-
-            // 4. O^T [D x 16 heads] += V^T [D x 16 keys] . P^T: per 16-dim tile, lane l of half-wave
-            //    group g addresses key 4g + (l%16)/4, dims 16t + 4(l%4) .. +3 and receives dim
-            //    16t + l % 16 of keys 4g .. 4g + 3.
-            const int vkey = 4 * grp + (m16 >> 2);
-            const uint8_t* const vrow = reinterpret_cast<const uint8_t*>(tv + vkey * NCH) + 8 * (lane & 3);
-#pragma unroll
-            for (int t = 0; t < D / 16; ++t)
-                o_acc[t] = mfma_16x16x16(lds_read_tr16(vrow + 32 * (t ^ mf_vswz<D>(vkey))), pb, o_acc[t]);
-        } else {
-            // 1. K -> LDS, swizzled so that the transposed reads below are conflict-free.
-    #pragma unroll
-            for (int j = 0; j < NLD; ++j) {
-                const int row = j * RPL + rpv;
-                lds_k[wave][row * NCH + (cpv ^ ((row / ROWS_PER_PERIOD) % NCH))] = kr[j];
-            }
-            u32x4 vcur[NLD];
-    #pragma unroll
-            for (int j = 0; j < NLD; ++j) vcur[j] = vr[j];
-            // Prefetch the next round of this wave.
-            if (r + NW < n_rounds) load_round(key0 + NW * RK, kr, vr);
-            wave_lds_sync();
-
-            // 2. Scores: lane (gq, kk) dots q[gq] with key row sub*QKG + kk.
-            float s[NSUB];
-    #pragma unroll
-            for (int sub = 0; sub < NSUB; ++sub) {
-                const int row = sub * QKG + kk;
-                const int swz = (row / ROWS_PER_PERIOD) % NCH;
-                float dot = 0.f;
-    #pragma unroll
-                for (int c = 0; c < NCH; ++c) {
-                    const u32x4 kw = lds_k[wave][row * NCH + (c ^ swz)];
-                    dot = dot2_bf16(qw[4 * c + 0], kw[0], dot);
-                    dot = dot2_bf16(qw[4 * c + 1], kw[1], dot);
-                    dot = dot2_bf16(qw[4 * c + 2], kw[2], dot);
-                    dot = dot2_bf16(qw[4 * c + 3], kw[3], dot);
-                }
-                s[sub] = (key0 + row < k_end) ? dot * a.scale_log2 : -INFINITY;
-            }
-
-            // 3. Online softmax for head gq, rescaled lazily (kRescaleSlack): the branch is
-            //    wave-uniform and, when taken, moves every head of the wave to its current max.
-            float mx = s[0];
-    #pragma unroll
-            for (int sub = 1; sub < NSUB; ++sub) mx = fmaxf(mx, s[sub]);
-            mx = group_max<QKG>(mx);
-            const float m_cand = fmaxf(m_run, mx);
-            if (__ballot(m_cand > m_run + kRescaleSlack) != 0) {
-                // m_cand == -inf: every key of this head so far is masked and O, l are still 0.
-                const float corr = (m_cand == -INFINITY) ? 1.f : fast_exp2(m_run - m_cand);
-                m_run = m_cand;
-                l_lane *= corr;
-    #pragma unroll
-                for (int g = 0; g < G; ++g) {
-                    const float cg = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(corr), g * QKG));
-    #pragma unroll
-                    for (int i = 0; i < 8; ++i) acc[g][i] *= cg;
-                }
-            }
-            float p[NSUB];
-            float psum = 0.f;
-    #pragma unroll
-            for (int sub = 0; sub < NSUB; ++sub) {
-                p[sub] = (s[sub] == -INFINITY) ? 0.f : fast_exp2(s[sub] - m_run);
-                psum += p[sub];
-            }
-            l_lane += psum;
-    #pragma unroll
-            for (int sub = 0; sub < NSUB; ++sub) lds_p[wave][(sub * QKG + kk) * G + gq] = p[sub];
-            wave_lds_sync();
-
-            // 4. O += p * V in the PV layout.
-    #pragma unroll
-            for (int j = 0; j < NLD; ++j) {
-                const int row = j * RPL + rpv;
-                float pv[G];
-    #pragma unroll
-                for (int g = 0; g < G; ++g) pv[g] = lds_p[wave][row * G + g];
-                float v[8];
-                unpack_bf16x8(vcur[j], v);
-    #pragma unroll
-                for (int g = 0; g < G; ++g)
-    #pragma unroll
-                    for (int i = 0; i < 8; ++i) acc[g][i] = fmaf(pv[g], v[i], acc[g][i]);
-            }
+        for (int j = 0; j < NLD; ++j) {
+            const int row = j * RPL + rpv;
+            tk[row * NCH + (cpv ^ mf_kswz<D>(row))] = kr[j];
+            tv[row * NCH + 2 * ((cpv >> 1) ^ mf_vswz<D>(row)) + (cpv & 1)] = vr[j];
         }
+        // Prefetch the next round of this wave.
+        if (r + NW < n_rounds) load_round(key0 + NW * RK, kr, vr);
+        wave_lds_sync();
+
+        // 2. S^T [16 keys x 16 heads] = K [16 x D] . Q^T [D x 16]: lane l gets keys
+        //    4(l/16) .. +3 of head l % 16.
+        const int m16 = lane & 15, grp = lane >> 4;
+        f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < D / 32; ++t)
+            sacc = mfma_16x16x32(tk[m16 * NCH + ((4 * t + grp) ^ mf_kswz<D>(m16))], qb[t], sacc);
+
+        // 3. Online softmax of head l % 16 over its 16 keys (4 per lane, 4 lanes), rescaled
+        //    lazily as below.
+        float sv[4];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            sv[i] = (key0 + 4 * grp + i < k_end) ? sacc[i] * a.scale_log2 : -INFINITY;
+            mx = fmaxf(mx, sv[i]);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_cand = fmaxf(m_run, mx);
+        if (__ballot(m_cand > m_run + kRescaleSlack) != 0) {
+            const float corr = (m_cand == -INFINITY) ? 1.f : fast_exp2(m_run - m_cand);
+            m_run = m_cand;
+            l_lane *= corr;
+#pragma unroll
+            for (int t = 0; t < D / 16; ++t) o_acc[t] *= corr;
+        }
+        float pf[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            pf[i] = (sv[i] == -INFINITY) ? 0.f : fast_exp2(sv[i] - m_run);
+            l_lane += pf[i];
+        }
+        // The S^T result layout is the B-operand layout of P^T (keys 4(l/16) .. +3, head l % 16).
+        const u32x2 pb = {pack_bf16x2(pf[0], pf[1]), pack_bf16x2(pf[2], pf[3])};
+
+        // 4. O^T [D x 16 heads] += V^T [D x 16 keys] . P^T: per 16-dim tile, lane l of half-wave
+        //    group g addresses key 4g + (l%16)/4, dims 16t + 4(l%4) .. +3 and receives dim
+        //    16t + l % 16 of keys 4g .. 4g + 3.
+        const int vkey = 4 * grp + (m16 >> 2);
+        const uint8_t* const vrow = reinterpret_cast<const uint8_t*>(tv + vkey * NCH) + 8 * (lane & 3);
+#pragma unroll
+        for (int t = 0; t < D / 16; ++t)
+            o_acc[t] = mfma_16x16x16(lds_read_tr16(vrow + 32 * (t ^ mf_vswz<D>(vkey))), pb, o_acc[t]);
     }
 
     // ---- merge the waves of this work-group ----
-    if constexpr (MF) {
-        __syncthreads();  // every wave is done with its K/V tiles, whose space lds_o reuses
+    __syncthreads();  // every wave is done with its K/V tiles, whose space lds_o reuses
+    {
         float l_head = l_lane + __shfl_xor(l_lane, 16);
         l_head += __shfl_xor(l_head, 32);
         const int hq = lane & 15, grp = lane >> 4;
@@ -664,24 +497,6 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
                 lds_m[wave][hq] = m_run;
                 lds_l[wave][hq] = l_head;
             }
-        }
-    } else {
-        const float l_head = group_sum<QKG>(l_lane);
-#pragma unroll
-        for (int off = NCH; off < 64; off <<= 1)
-#pragma unroll
-            for (int g = 0; g < G; ++g)
-#pragma unroll
-                for (int i = 0; i < 8; ++i) acc[g][i] += __shfl_xor(acc[g][i], off);
-        if (rpv == 0) {
-#pragma unroll
-            for (int g = 0; g < G; ++g)
-#pragma unroll
-                for (int i = 0; i < 8; ++i) lds_o[wave][g][cpv * 8 + i] = acc[g][i];
-        }
-        if (kk == 0) {
-            lds_m[wave][gq] = m_run;
-            lds_l[wave][gq] = l_head;
         }
     }
     __syncthreads();
@@ -746,14 +561,13 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
     merge_splits_parallel<D, G, NW>(a, unit, b, h, n_splits, lds_o, lds_m, lds_l);
 }
 
-// Waves per split work-group.  Up to G = 8 a wave fits in 256 registers, so 8-wave
-// work-groups keep two waves per SIMD and give one (sequence, kv head) twice the loads in
-// flight of a 4-wave one (ragged batches finish their long sequences sooner, and a long
-// context is cut into half as many splits); G = 16 needs more than 256 registers per wave
-// and keeps 4 waves.
+// Waves per split work-group: 8 for every group size (at most 150 registers per lane with the
+// matrix-core rounds, so two waves per SIMD), which gives one (sequence, kv head) twice the loads in
+// flight of a 4-wave work-group: ragged batches finish their long sequences sooner, and a long
+// context is cut into half as many splits.
 template <int G>
 constexpr int decode_waves_t() {
-    return G <= 8 ? 8 : 4;
+    return 8;
 }
 
 template <int D, int G, int NW>
@@ -786,10 +600,7 @@ hipError_t launch_combine_t(const DecodeArgs& a, const Launch& l) {
 
 }  // namespace
 
-int decode_round_keys(int group) {
-    const int qkg = 64 / group;  // keys per head in the QK layout (RK of decode_split_kernel)
-    return qkg > 16 ? qkg : 16;
-}
+int decode_round_keys(int) { return 16; }  // RK of decode_split_kernel, every group size
 
 int decode_waves(int group) {
     return group <= 4 ? decode_waves_t<4>() : group <= 8 ? decode_waves_t<8>() : decode_waves_t<16>();
