@@ -192,12 +192,17 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int h = blockIdx.y;  // kv head
+    // Work-group -> (kv head, task group): consecutive work-groups take consecutive kv heads, so
+    // with the dispatcher's round robin over the 8 XCDs every XCD serves one kv head (or a fixed
+    // subset of them) and its L2 holds only that head's K/V tiles.
+    const int lin = blockIdx.y * gridDim.x + blockIdx.x;  // position within the segment's grid
+    const int h = lin % a.n_kv_heads;                    // kv head
+    const int wx = lin / a.n_kv_heads;                   // task group of the head
     const int n_rb = (a.q_len + kRows - 1) / kRows;
     const int n_tasks = n_rb * G;
     // Causal row blocks grow in work with their index: the largest go to the work-groups the
     // dispatcher starts first (longest first), so a grid larger than the GPU balances.
-    const int wg_x = a.causal ? (int)(gridDim.x - 1 - blockIdx.x) : (int)blockIdx.x;
+    const int wg_x = a.causal ? (int)(gridDim.x - 1 - wx) : wx;
     const int task = wg_x * kWaves + wave;
     const bool active = task < n_tasks;
     const int g = task % G;
@@ -223,7 +228,7 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
         const u32x4* vs = reinterpret_cast<const u32x4*>(a.v_new) + (size_t)h * a.n_new * NCH;
         const int words = a.n_new * NCH;
         const int n_threads = gridDim.x * gridDim.z * (kWaves * 64);
-        const int first = (blockIdx.z * gridDim.x + blockIdx.x) * (kWaves * 64) + tid;
+        const int first = (blockIdx.z * gridDim.x + wx) * (kWaves * 64) + tid;
         if constexpr (PAGED) {
             for (int i = first; i < words; i += n_threads) {
                 const int64_t r = paged_row(a.block_table, a.page_shift, a.n_kv_heads, h, a.new_begin + i / NCH);
