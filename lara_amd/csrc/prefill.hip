@@ -125,6 +125,23 @@ __device__ __forceinline__ u32x4 lds_read128(uint32_t addr) {
     return v;
 }
 
+// 16-byte global load into VGPRs from inline assembly: the compiler adds no s_waitcnt for it, so
+// it can stay in flight behind later direct-to-LDS loads.  The result is valid only after vm_wait.
+__device__ __forceinline__ u32x4 load16_untracked(const void* p) {
+    u32x4 v;
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p) : "memory");
+    return v;
+}
+
+// s_waitcnt vmcnt(N) (lgkm and export counters untouched) that the compiler sees as producing a
+// and b (results of load16_untracked), so no use of them can move above it.
+template <int N, typename T>
+__device__ __forceinline__ void vm_wait(T& a, T& b) {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt %2" : "+v"(a), "+v"(b) : "i"((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8))
+                 : "memory");
+}
+
 // s_waitcnt lgkmcnt(N) (vm and export counters untouched) that the compiler sees as
 // producing a and b, so no use of them can move above it.  Only this kernel's own LDS reads
 // are outstanding when it is used (the stage DMA counts on vmcnt).
@@ -707,27 +724,10 @@ __global__ __launch_bounds__(NW * 64) void prefill_rows_kernel(PrefillArgs a) {
     constexpr float kLazyLog2 = 8.0f;  // the reference max moves only when passed by more than this
     const float c = a.scale_log2;
 
-    // Q^T operand (row `row`, dims 16*ks + 8*half .. +7), the wave's first two blocks and this
-    // work-group's share of the appended rows are all in flight before the first wait.
-    // Q of the row block goes to LDS once (the K tile's swizzled layout, rows past q_len from the zero
-    // row), each lane one 16-byte chunk, instead of every wave loading all 32 rows.
-    for (int base = wave * 64; base < TILE; base += kRowWaves * 64) {  // base is wave-uniform
-        const int slot = base + lane;
-        const int qrow = slot / NCH;
-        const int chunk = (slot % NCH) ^ k_swz<NCH>(qrow);
-        const u32x4* src = rb * kRows + qrow < a.q_len
-                               ? reinterpret_cast<const u32x4*>(a.q + ((size_t)hq * a.q_len + rb * kRows + qrow) * D) + chunk
-                               : zero + chunk;
-        dma16(src, lds_addr(&lds_q[base]));
-    }
-    if (my_blocks > 0) {
-        issue(wave * kRowBN, 0);
-        issue(wave * kRowBN, 1);
-    }
     // Appended rows of kv head h go to the cache in equal shares over the kv head's work-groups;
     // blocks that hold them read k_new/v_new, so no work-group waits for the copy.  A thread's first
-    // word is loaded with Q and the first blocks and stored after the wait below (the loop's own
-    // waits then cover the store); any further words (more appended rows than threads) follow.
+    // word is loaded first of all and stored after the wait below (the loop's own waits then cover
+    // the store); any further words (more appended rows than threads) follow.
     const int app_words = has_new ? a.n_new * NCH : 0;
     const int app_stride = gridDim.y * (kRowWaves * 64);
     const int app_first = blockIdx.y * (kRowWaves * 64) + tid;
@@ -739,12 +739,31 @@ __global__ __launch_bounds__(NW * 64) void prefill_rows_kernel(PrefillArgs a) {
             return ((int64_t)h * a.l_cap + a.new_begin) * NCH + i;
         }
     };
-    u32x4 app_k{}, app_v{};
-    if (app_first < app_words) {
-        app_k = kn[app_first];
-        app_v = vn[app_first];
+    // Every lane loads (past the appended words: the zero row), so the loads' results need no
+    // merge with another value before the wait below that makes them valid.
+    u32x4 app_k = load16_untracked(app_first < app_words ? kn + app_first : zero);
+    u32x4 app_v = load16_untracked(app_first < app_words ? vn + app_first : zero);
+    // Then Q^T's rows (row `row`, dims 16*ks + 8*half .. +7) and the wave's first K and V tiles.
+    // Q of the row block goes to LDS once (the K tile's swizzled layout, rows past q_len from the zero
+    // row), each lane one 16-byte chunk, instead of every wave loading all 32 rows.
+    for (int base = wave * 64; base < TILE; base += kRowWaves * 64) {  // base is wave-uniform
+        const int slot = base + lane;
+        const int qrow = slot / NCH;
+        const int chunk = (slot % NCH) ^ k_swz<NCH>(qrow);
+        const u32x4* src = rb * kRows + qrow < a.q_len
+                               ? reinterpret_cast<const u32x4*>(a.q + ((size_t)hq * a.q_len + rb * kRows + qrow) * D) + chunk
+                               : zero + chunk;
+        dma16(src, lds_addr(&lds_q[base]));
     }
-    wait_vmcnt<0>();  // Q, the first blocks and the first appended word
+    // Loads complete in issue order, so at most V(0)'s DMA loads in flight means the appended word,
+    // Q and K(0) have landed: V(0) lands behind the first S^T (the loop waits for it before PV).
+    if (my_blocks > 0) {
+        issue(wave * kRowBN, 0);
+        issue(wave * kRowBN, 1);
+    } else {
+        wait_vmcnt<0>();
+    }
+    vm_wait<DMA>(app_k, app_v);
     __syncthreads();  // every wave's share of Q is in LDS
     u32x4 qb[KSTEPS];  // Q^T operand: row `row`, dims 16*ks + 8*half .. +7
     {
@@ -769,7 +788,7 @@ __global__ __launch_bounds__(NW * 64) void prefill_rows_kernel(PrefillArgs a) {
             }
         }
         // The stores stay in flight: the loop's vmcnt waits also count them, which only makes the
-        // first of those waits (block 1) wait for them as well.
+        // first of those waits (V(0), before the first PV) wait for them as well.
     }
 
     // vm operations in flight enter the loop in the order K(t), V(t): K(t) (then K(t+1)) is issued
@@ -845,9 +864,7 @@ __global__ __launch_bounds__(NW * 64) void prefill_rows_kernel(PrefillArgs a) {
         l_lane += psum;
 
         // ---- O^T += V^T . P^T, transposing V reads one step ahead ----
-        if (t >= 1) {  // V(t) landed; K(t+1) may still be in flight
-            if (more) wait_vmcnt<DMA>(); else wait_vmcnt<0>();
-        }
+        if (more) wait_vmcnt<DMA>(); else wait_vmcnt<0>();  // V(t) landed; K(t+1) may still be in flight
         constexpr int PV = MT * 2;
         u32x2 vf[PV][2];
         auto read_v = [&](auto step_c) {
