@@ -555,7 +555,6 @@ int run_layer_qkv(gqa_ctx* c, int32_t b, const void* x, int32_t n_tokens, int32_
     // While profiling (device calls), the projection's hipBLASLt kernels are bracketed by the next
     // event pair of its timer slot; RMSNorm and RoPE have event pairs bound to their launches.
     const Launch proj_events = stage_events ? Launch{s} : timed(c, GQA_TIMER_PROJECTION, s);
-    if (proj_events.start) HIP_TRY(hipEventRecord(proj_events.start, s));
     HIP_TRY(mark(0));
     const uint16_t* src = (const uint16_t*)x;
     float* cs = rope ? reinterpret_cast<float*>(c->layer_tmp + y_bytes + qkv_bytes) : nullptr;
@@ -579,6 +578,7 @@ int run_layer_qkv(gqa_ctx* c, int32_t b, const void* x, int32_t n_tokens, int32_
         if (gamma) src = na.y;
     }
     HIP_TRY(mark(1));
+    if (proj_events.start) HIP_TRY(hipEventRecord(proj_events.start, s));  // after the norm launch
     uint16_t* qkv = (uint16_t*)(c->layer_tmp + y_bytes);
     const float one = 1.f, zero = 0.f;
     const void* ws[3] = {wq, wk, wv};
