@@ -290,7 +290,7 @@ class DecodeBench:
 
 
 LAUNCH_BOUND = ("decode-b1-d64-ctx256", "decode-b1-ctx4097")  # workloads whose step is also timed as a replayed HIP graph
-PAGED_SUFFIX = "-paged"  # a decode workload over a paged cache (64-row pages unless --page-rows)
+PAGED_SUFFIX = "-paged"  # a decode or chunked-prefill workload over a paged cache (64-row pages unless --page-rows)
 PAGE_ROWS = 64
 
 
@@ -346,7 +346,7 @@ def measure(name: str, steps: int, warmup: int, chunk: int = 0, page_rows: int =
 class PrefillBench:
     """Chunked causal prefill: every chunk appends its K/V rows, then attends the growing cache."""
 
-    def __init__(self, w, device: int = 0, target_wgs: int = 0):
+    def __init__(self, w, device: int = 0, target_wgs: int = 0, page_size: int = 0):
         import torch
         from lara_amd import _lib
 
@@ -354,9 +354,20 @@ class PrefillBench:
         self.lib = _lib.lib()
         self._lib = _lib
         self.w = w
-        cfg = _lib.GqaConfig(1, w.n_q_heads, w.n_kv_heads, w.head_dim, w.prompt, w.chunk, 0.0, device)
         self.ctx = ctypes.c_void_p()
-        _lib.check(self.lib.gqa_create(ctypes.byref(cfg), ctypes.byref(self.ctx)), "gqa_create")
+        if page_size:
+            # Paged cache: the prompt's pages alternate with a second sequence's, so its rows are
+            # scattered over the pool as in a shared one.
+            cfg = _lib.GqaConfig(2, w.n_q_heads, w.n_kv_heads, w.head_dim, w.prompt, w.chunk, 0.0, device)
+            pages = -(-w.prompt // page_size)
+            _lib.check(self.lib.gqa_create_paged(ctypes.byref(cfg), page_size, 2 * pages, ctypes.byref(self.ctx)),
+                       "gqa_create_paged")
+            for p in range(1, pages + 1):
+                for b in range(2):
+                    _lib.check(self.lib.gqa_paged_reserve(self.ctx, b, min(w.prompt, p * page_size)), "reserve")
+        else:
+            cfg = _lib.GqaConfig(1, w.n_q_heads, w.n_kv_heads, w.head_dim, w.prompt, w.chunk, 0.0, device)
+            _lib.check(self.lib.gqa_create(ctypes.byref(cfg), ctypes.byref(self.ctx)), "gqa_create")
         if target_wgs:
             _lib.check(self.lib.gqa_set_option(self.ctx, _lib.GQA_OPT_PREFILL_WGS, target_wgs), "prefill wgs")
         dev = torch.device("cuda", device)
@@ -408,13 +419,14 @@ class PrefillBench:
         self.lib.gqa_destroy(self.ctx)
 
 
-def measure_prefill(name: str, steps: int, warmup: int, target_wgs: int = 0) -> dict:
+def measure_prefill(name: str, steps: int, warmup: int, target_wgs: int = 0, page_rows: int = PAGE_ROWS) -> dict:
     from lara_amd.benchmark import BF16_DENSE_TFLOPS, PREFILL_WORKLOADS, prefill_chunk_schedule, prefill_flops, \
         valid_pairs
 
-    w = PREFILL_WORKLOADS[name]
+    paged = name.endswith(PAGED_SUFFIX)
+    w = PREFILL_WORKLOADS[name[: -len(PAGED_SUFFIX)] if paged else name]
     log(f"{name}: chunked prefill set-up")
-    bench = PrefillBench(w, target_wgs=target_wgs)
+    bench = PrefillBench(w, target_wgs=target_wgs, page_size=page_rows if paged else 0)
     try:
         r = bench.run(steps, warmup)
     finally:
@@ -1133,7 +1145,7 @@ def main() -> int:
     from lara_amd.benchmark import LAYER_WORKLOADS, PREFILL_WORKLOADS
 
     known = set(WORKLOAD_NAMES) | {n + PAGED_SUFFIX for n in WORKLOAD_NAMES} | set(PREFILL_WORKLOADS) | \
-        set(LAYER_WORKLOADS) | set(ONESHOT_PREFILL)
+        {n + PAGED_SUFFIX for n in PREFILL_WORKLOADS} | set(LAYER_WORKLOADS) | set(ONESHOT_PREFILL)
     unknown = [x for x in args.others.split(",") if x and x not in known]
     if unknown:
         parser.error(f"--others: unknown workload(s) {', '.join(unknown)}; known: {', '.join(sorted(known))}")
@@ -1163,8 +1175,9 @@ def main() -> int:
                    "decode_kernel_gbps", "decode_kernel_frac_of_peak", "kernels_gbps", "tokens_per_s",
                    "graph_us_per_step", "gate_held")
     for name in [x for x in args.others.split(",") if x and x != args.workload]:
-        if name in PREFILL_WORKLOADS:
-            others[name] = measure_prefill(name, max(10, args.steps // 2), max(2, args.warmup // 2), args.prefill_wgs)
+        if name.removesuffix(PAGED_SUFFIX) in PREFILL_WORKLOADS:
+            others[name] = measure_prefill(name, max(10, args.steps // 2), max(2, args.warmup // 2), args.prefill_wgs,
+                                           args.page_rows)
         elif name in ONESHOT_PREFILL:
             others[name] = measure_prefill_oneshot(name, max(5, args.steps // 10), 2)
         elif name in LAYER_WORKLOADS:

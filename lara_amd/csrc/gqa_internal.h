@@ -104,6 +104,19 @@ __device__ __forceinline__ int64_t paged_row(const int32_t* table_row, int page_
     return (((int64_t)page * n_kv_heads + h) << page_shift) + (t & ((1 << page_shift) - 1));
 }
 
+// paged_row for a wave-uniform t: the table entry comes through the scalar cache (s_load, counted by
+// lgkmcnt), so the wait for it does not also wait for the vector loads in flight (which a table
+// read by a vector load would, since the compiler cannot see the kernels' direct-to-LDS loads).  The
+// table is read-only while a kernel runs.
+__device__ __forceinline__ int64_t paged_row_uniform(const int32_t* table_row, int page_shift, int n_kv_heads, int h,
+                                                     int t) {
+    typedef const __attribute__((address_space(4))) int32_t* const_i32_ptr;
+    const const_i32_ptr row = (const_i32_ptr)(uintptr_t)table_row;
+    const int page = row[t >> page_shift];
+    if (page < 0) return -1;
+    return (((int64_t)page * n_kv_heads + h) << page_shift) + (t & ((1 << page_shift) - 1));
+}
+
 // KV segmentation of a prefill launch: (seg_len, n_segs) for q_len query rows whose
 // attended key span is kv_span, sized so the launch has about target_wgs work-groups.
 struct PrefillPlan {

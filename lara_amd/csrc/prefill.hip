@@ -318,7 +318,7 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
         const u32x4* vb0 = vg;
         int stride = NCH;
         if constexpr (PAGED) {
-            const int64_t pr = paged_row(a.block_table, a.page_shift, a.n_kv_heads, h, j0);
+            const int64_t pr = paged_row_uniform(a.block_table, a.page_shift, a.n_kv_heads, h, j0);
             if (pr < 0) {
                 kb0 = zero;
                 vb0 = zero;
@@ -659,7 +659,7 @@ __global__ __launch_bounds__(NW * 64) void prefill_rows_kernel(PrefillArgs a) {
                 vrow = vn + (size_t)(j0 - a.new_begin) * NCH;
             } else if (!has_new || j0 + kRowBN <= a.new_begin || j0 >= new_end) {
                 if constexpr (PAGED) {  // j0 and the page size are multiples of 32: one page per block
-                    const int64_t pr = paged_row(a.block_table, a.page_shift, a.n_kv_heads, h, j0);
+                    const int64_t pr = paged_row_uniform(a.block_table, a.page_shift, a.n_kv_heads, h, j0);
                     krow = pr < 0 ? nullptr : kg + (size_t)pr * NCH;
                     vrow = pr < 0 ? nullptr : vg + (size_t)pr * NCH;
                 } else {
@@ -675,7 +675,7 @@ __global__ __launch_bounds__(NW * 64) void prefill_rows_kernel(PrefillArgs a) {
             return;
         }
         int64_t pr0 = 0;  // paged: the block's page row (-1: unmapped, zero rows)
-        if constexpr (PAGED) pr0 = paged_row(a.block_table, a.page_shift, a.n_kv_heads, h, j0);
+        if constexpr (PAGED) pr0 = paged_row_uniform(a.block_table, a.page_shift, a.n_kv_heads, h, j0);
 #pragma unroll
         for (int i = 0; i < DMA; ++i) {
             const int rel = (int)(koff[i] >> 4) / NCH;  // key of this lane's slot within the block
