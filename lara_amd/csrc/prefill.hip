@@ -649,7 +649,9 @@ __global__ __launch_bounds__(NW * 64) void prefill_rows_kernel(PrefillArgs a) {
         voff[i] = 16u * (uint32_t)(key * NCH + ((slot % NCH) ^ v_swz<D>(key)));
     }
     const int new_end = has_new ? a.new_begin + a.n_new : 0;
-    auto issue = [&](int j0, int kv) {
+    // pr: paged, the block's page row (paged_row_uniform of j0, looked up by the caller ahead of
+    // time so the scalar load's latency hides behind other work; -1: unmapped, zero rows).
+    auto issue = [&](int j0, int kv, int64_t pr) {
         // Row j0's K and V, or nullptr where the block's rows do not share one source.
         const u32x4* krow = nullptr;
         const u32x4* vrow = nullptr;
@@ -659,7 +661,6 @@ __global__ __launch_bounds__(NW * 64) void prefill_rows_kernel(PrefillArgs a) {
                 vrow = vn + (size_t)(j0 - a.new_begin) * NCH;
             } else if (!has_new || j0 + kRowBN <= a.new_begin || j0 >= new_end) {
                 if constexpr (PAGED) {  // j0 and the page size are multiples of 32: one page per block
-                    const int64_t pr = paged_row_uniform(a.block_table, a.page_shift, a.n_kv_heads, h, j0);
                     krow = pr < 0 ? nullptr : kg + (size_t)pr * NCH;
                     vrow = pr < 0 ? nullptr : vg + (size_t)pr * NCH;
                 } else {
@@ -674,8 +675,7 @@ __global__ __launch_bounds__(NW * 64) void prefill_rows_kernel(PrefillArgs a) {
             for (int i = 0; i < DMA; ++i) dma16_sbase(base, kv ? voff[i] : koff[i], lds_addr(&lds[wave][kv][i * 64]));
             return;
         }
-        int64_t pr0 = 0;  // paged: the block's page row (-1: unmapped, zero rows)
-        if constexpr (PAGED) pr0 = paged_row_uniform(a.block_table, a.page_shift, a.n_kv_heads, h, j0);
+        const int64_t pr0 = pr;
 #pragma unroll
         for (int i = 0; i < DMA; ++i) {
             const int rel = (int)(koff[i] >> 4) / NCH;  // key of this lane's slot within the block
@@ -758,8 +758,9 @@ __global__ __launch_bounds__(NW * 64) void prefill_rows_kernel(PrefillArgs a) {
     // Loads complete in issue order, so at most V(0)'s DMA loads in flight means the appended word,
     // Q and K(0) have landed: V(0) lands behind the first S^T (the loop waits for it before PV).
     if (my_blocks > 0) {
-        issue(wave * kRowBN, 0);
-        issue(wave * kRowBN, 1);
+        const int64_t pr = PAGED ? paged_row_uniform(a.block_table, a.page_shift, a.n_kv_heads, h, wave * kRowBN) : 0;
+        issue(wave * kRowBN, 0, pr);
+        issue(wave * kRowBN, 1, pr);
     } else {
         wait_vmcnt<0>();
     }
@@ -796,6 +797,9 @@ __global__ __launch_bounds__(NW * 64) void prefill_rows_kernel(PrefillArgs a) {
     for (int t = 0; t < my_blocks; ++t) {
         const int j0 = (wave + t * kRowWaves) * kRowBN;
         const bool more = t + 1 < my_blocks;
+        // Paged: the next block's page row, needed after this block's S^T.
+        const int64_t pr_next =
+            PAGED && more ? paged_row_uniform(a.block_table, a.page_shift, a.n_kv_heads, h, j0 + kRowWaves * kRowBN) : 0;
         if (t >= 1) wait_vmcnt<DMA>();  // K(t) landed; V(t) may still be in flight
 
         // ---- S^T = K . Q^T (raw scores): one 32x32 tile, K fragments read KA steps ahead ----
@@ -816,7 +820,7 @@ __global__ __launch_bounds__(NW * 64) void prefill_rows_kernel(PrefillArgs a) {
             sacc = mfma32(kf[ks], qb[ks], sacc);
         });
         // Every read of the K tile is complete (lgkmcnt(0) above): it takes the next block's K.
-        if (more) issue(j0 + kRowWaves * kRowBN, 0);
+        if (more) issue(j0 + kRowWaves * kRowBN, 0, pr_next);
 
         // ---- online softmax (log2 domain, scale folded into the exponent) ----
         const bool need_mask =
@@ -887,7 +891,7 @@ __global__ __launch_bounds__(NW * 64) void prefill_rows_kernel(PrefillArgs a) {
             o[i >> 1] = mfma32(vw, pb[i & 1], o[i >> 1]);
         });
         // Every read of the V tile is complete (lgkmcnt(0) above): it takes the next block's V.
-        if (more) issue(j0 + kRowWaves * kRowBN, 1);
+        if (more) issue(j0 + kRowWaves * kRowBN, 1, pr_next);
     }
 
     // ---- merge the waves: each writes (O^T [D][32 rows], m, l) to its own ring (no DMA pending) ----
