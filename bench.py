@@ -612,7 +612,8 @@ def measure_layer(name: str, steps: int, warmup: int, target_wgs: int = 0) -> di
 
 ONESHOT_PREFILL = {"prefill-8192": 8192}  # one causal prefill launch of this many tokens (32 q / 8 kv heads, D 128)
 DEFAULT_OTHERS = ("decode-b1-ctx4097", "decode-b64-ragged", "decode-b4-ctx131072", "prefill-chunked-2048",
-                  "prefill-8192", "layer-2048", "decode-b64-ctx8192" + PAGED_SUFFIX)
+                  "prefill-8192", "layer-2048", "decode-b64-ctx8192" + PAGED_SUFFIX,
+                  "prefill-chunked-2048" + PAGED_SUFFIX)
 
 
 def measure_prefill_oneshot(name: str, steps: int, warmup: int) -> dict:
