@@ -297,6 +297,20 @@ PAGE_ROWS = 64
 DECODE_MERGE = {"auto": 0, "launch": 1, "fused": 2}  # GQA_DECODE_MERGE_AUTO / _LAUNCH / _FUSED
 
 
+INFINITY_CACHE_BYTES = 256 * 2**20  # MI355X last-level (MALL) cache
+
+
+def residency(working_set: int, byte_rate: bool = True) -> dict:
+    """Whether a workload's bytes fit the 256 MiB Infinity Cache: a step that does is served from it
+    after warm-up, so a byte rate measured on it is not an HBM rate."""
+    resident = working_set <= INFINITY_CACHE_BYTES
+    note = "cache-resident: the working set fits the 256 MiB Infinity Cache"
+    if resident and byte_rate:
+        note += ", so the GB/s figure is not an HBM rate (the step is latency-bound)"
+    return {"working_set_bytes": int(working_set), "cache_resident": resident,
+            "residency": note if resident else "HBM: the working set exceeds the 256 MiB Infinity Cache"}
+
+
 def measure(name: str, steps: int, warmup: int, chunk: int = 0, page_rows: int = PAGE_ROWS,
             merge: str = "auto") -> dict:
     from lara_amd.benchmark import HBM_PEAK_GBPS, WORKLOADS, decode_kernel_bytes, decode_step_bytes
@@ -333,6 +347,7 @@ def measure(name: str, steps: int, warmup: int, chunk: int = 0, page_rows: int =
     r["step_frac_of_peak"] = r["step_gbps"] / HBM_PEAK_GBPS
     if r["decode_kernel_gbps"]:
         r["decode_kernel_frac_of_peak"] = r["decode_kernel_gbps"] / HBM_PEAK_GBPS
+    r.update(residency(step_bytes))
     log(f"{name}: {us:.1f} us/step (device {r['gpu_us_per_step']:.1f}, gated {r['gated_gpu_us_per_step']:.1f}; "
         f"kernels median {r['step_us']['median']:.1f}, p95 {r['step_us']['p95']:.1f}), step {r['step_gbps']:.0f} GB/s; "
         f"decode kernel {r['decode_us']:.1f} us = "
@@ -456,6 +471,9 @@ def measure_prefill(name: str, steps: int, warmup: int, target_wgs: int = 0, pag
         "gate_held": r["gate_held"],
         "tokens_per_s": w.prompt / (r["wall_us_per_prompt"] * 1e-6),
     }
+    # K/V cache, the prompt's Q and its O.
+    out.update(residency(2 * w.n_kv_heads * w.prompt * w.head_dim * 2 + 2 * w.n_q_heads * w.prompt * w.head_dim * 2,
+                         byte_rate=False))
     out["mfma_frac_of_bf16_peak"] = out["kernel_tflops"] / BF16_DENSE_TFLOPS if out["kernel_tflops"] else None
     out["mfma_frac_incl_merge"] = (out["kernels_tflops_incl_merge"] / BF16_DENSE_TFLOPS
                                    if out["kernels_tflops_incl_merge"] else None)
@@ -1174,7 +1192,7 @@ def main() -> int:
     decode_keys = ("us_per_step", "gpu_us_per_step", "gated_gpu_us_per_step", "step_us", "step_gbps", "step_frac_of_peak", "decode_us",
                    "combine_us", "merges_per_step", "kernels_us_per_step", "decode_kernel_bytes",
                    "decode_kernel_gbps", "decode_kernel_frac_of_peak", "kernels_gbps", "tokens_per_s",
-                   "graph_us_per_step", "gate_held")
+                   "graph_us_per_step", "gate_held", "working_set_bytes", "cache_resident", "residency")
     for name in [x for x in args.others.split(",") if x and x != args.workload]:
         if name.removesuffix(PAGED_SUFFIX) in PREFILL_WORKLOADS:
             others[name] = measure_prefill(name, max(10, args.steps // 2), max(2, args.warmup // 2), args.prefill_wgs,
@@ -1247,6 +1265,8 @@ def main() -> int:
             "step": "append 1 K/V row per sequence fused into the split-KV decode launch (a second LSE-merge "
                     "launch only when a sequence spans several splits; none at this shape)",
             "accumulate": "fp32",
+            "working_set_bytes": main_r["working_set_bytes"],
+            "residency": main_r["residency"],
         },
         "kernels_us": {"decode_step": main_r["decode_us"]},
         "roofline": roofline,
