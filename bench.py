@@ -1130,7 +1130,7 @@ def main() -> int:
     parser.add_argument("--chunk", type=int, default=0, help="keys per split-KV work-group (0 = auto)")
     parser.add_argument("--decode-merge", default="auto", choices=sorted(DECODE_MERGE),
                         help="split merge of the decode: in the decode launch (fused), a second launch, or auto "
-                             "(fused while the split grid fits one dispatch round)")
+                             "(fused while the split grid fills at most half the CUs)")
     parser.add_argument("--page-rows", type=int, default=PAGE_ROWS,
                         help="rows per page of the paged-cache workloads (power of two, >= 64)")
     parser.add_argument("--prefill-wgs", type=int, default=0,

@@ -90,10 +90,10 @@ extern "C" {
 /* Split merge of the decode (GQA_OPT_DECODE_MERGE).  FUSED: the last split of a (sequence, kv head) to
  * finish merges the others' partials inside the decode launch (agent-scope atomics and a per-unit
  * arrival counter; one launch per step).  LAUNCH: a second, log-sum-exp merge launch.  AUTO (default):
- * FUSED while the split grid (sequences x kv heads x splits) is at most the GPU's CU count and a
+ * FUSED while the split grid (sequences x kv heads x splits) is at most half the GPU's CU count and a
  * sequence has at most 8 splits -- every split ends with an L2 write-back of its XCD and an increment
- * of its sequence's counter, which larger grids and more splits per counter pay for more than a
- * launch -- else LAUNCH.  Both fold the splits in the same order (the same output words). */
+ * of its sequence's counter, which saves the launch for short steps but slows the streaming of larger
+ * grids more than a launch costs -- else LAUNCH.  Both fold the splits in the same order (the same output words). */
 #define GQA_DECODE_MERGE_AUTO   0
 #define GQA_DECODE_MERGE_LAUNCH 1
 #define GQA_DECODE_MERGE_FUSED  2

@@ -25,9 +25,9 @@
 // bf16 output directly; otherwise each split writes an fp32 partial (O, m, l) and the
 // splits merge with log-sum-exp weights: inside the launch, by the last split of the
 // (sequence, kv head) to arrive (an agent-scope release per split: an L2 write-back of its
-// XCD, worth it while the split grid fits one dispatch round, as for one long sequence), or
-// by decode_combine_kernel, a second launch (larger grids, where every split's write-back
-// would cost more than the launch).
+// XCD, worth it while the split grid is small and the step short, as for one short sequence), or
+// by decode_combine_kernel, a second launch (larger grids, whose write-backs slow the other
+// splits' streaming more than the launch costs).
 //
 // Fused append: when k_new/v_new are given, split 0 of every (sequence, kv head) writes
 // the new row to cache row positions[b], and any split whose key range contains that row

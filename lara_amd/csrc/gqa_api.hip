@@ -192,16 +192,19 @@ int plan_chunk(int batch, int n_kv_heads, int group, int n_cu, int max_len) {
 
 // Whether the last split to arrive merges a sequence's splits inside the decode launch.  Each split
 // then ends with an agent-scope release (an L2 write-back of its XCD) and an increment of its
-// sequence's arrival counter, which pays for itself only while the split grid fits one dispatch
-// round and few splits share a counter; AUTO fuses up to kFusedMergeSplits splits per sequence
-// within one round (measured: 2 splits 6.2 vs 7.4 us per step for the merge launch, 8 splits even,
-// 32 splits 10.3 vs 9.3 us).
+// sequence's arrival counter, and the last one with an acquire (an L2 invalidate): that saves the
+// merge launch where the step is a short latency chain, but the L2 maintenance of many work-groups
+// slows the streaming of the others.  AUTO fuses up to kFusedMergeSplits splits per sequence while
+// the split grid fills at most half the CUs (measured, kernel time per step, fused vs launch: 4
+// work-groups (2 splits of 128 keys) 5.1 vs 8.1 us, 64 work-groups (8 splits of 512) 9.4 vs 11.7 us;
+// 256 work-groups: 8 splits of 16384 keys 314.1 vs 311.5 us, 4 of 8192 161 vs 160 us, 2 of 4096
+// 83-86 vs 81-82 us, 2 of 512 16.7 vs 16.1 us; 32 splits of 128 keys 10.3 vs 9.3 us).
 constexpr int kFusedMergeSplits = 8;
 
 bool fuse_merge(int option, int units, int max_splits, int n_cu) {
     if (max_splits <= 1 || option == GQA_DECODE_MERGE_LAUNCH) return false;
     return option == GQA_DECODE_MERGE_FUSED ||
-           ((int64_t)units * max_splits <= n_cu && max_splits <= kFusedMergeSplits);
+           (2 * (int64_t)units * max_splits <= n_cu && max_splits <= kFusedMergeSplits);
 }
 
 int choose_chunk(const gqa_ctx* c, int max_len) {
