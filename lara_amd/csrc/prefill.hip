@@ -118,10 +118,13 @@ __device__ __forceinline__ uint64_t uniform_address(const void* p) {
 
 // 16-byte LDS read issued from inline assembly, so it stays where it is written: the
 // compiler's scheduler, short of registers, would otherwise move every read next to its use
-// and make each MFMA wait for its own read.  The result is valid only after lgkm_wait.
+// and make each MFMA wait for its own read.  The result is valid only after lgkm_wait.  Reads
+// addr + OFF (OFF in the instruction's 16-bit offset field).
+template <int OFF = 0>
 __device__ __forceinline__ u32x4 lds_read128(uint32_t addr) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset range");
     u32x4 v;
-    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr) : "memory");
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF) : "memory");
     return v;
 }
 
@@ -165,6 +168,7 @@ __device__ __forceinline__ void static_for(F&& f) {
 // Transposing 8-byte LDS read (ds_read_b64_tr_b16) from inline assembly, at addr + OFF.
 template <int OFF>
 __device__ __forceinline__ u32x2 lds_read_tr64(uint32_t addr) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset range");
     u32x2 v;
     asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF) : "memory");
     return v;
@@ -296,57 +300,69 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
     const u32x4* vn = has_new ? reinterpret_cast<const u32x4*>(a.v_new) + (size_t)h * a.n_new * NCH : nullptr;
     const u32x4* zero = reinterpret_cast<const u32x4*>(a.zero_row);
 
-    // Direct-to-LDS staging of block j0 into ring stage st: wave-instruction i of wave w fills
+    // Direct-to-LDS staging of block j0 into ring stage ST: wave-instruction i of wave w fills
     // the 64 consecutive 16-byte slots (i*kWaves + w)*64 .., lane L slot +L; each lane loads the
     // chunk the swizzled layout wants in its slot.  The slot -> (key, chunk) map is per lane and
-    // fixed; rows past kv_len (zero row) and rows this launch appends (k_new/v_new) occur in
-    // few blocks, so other blocks take the plain cache addresses.
+    // fixed, so a block whose 64 rows are consecutive cache rows (every block but those past
+    // kv_len, those holding rows this launch appends and unmapped pages) takes a wave-uniform
+    // base in SGPRs and these fixed per-lane byte offsets (koff, voff): no per-block address
+    // arithmetic.  The other blocks pick each lane's source (zero row, k_new/v_new, cache).
     int sl_key[DMA], sl_ck[DMA], sl_cv[DMA];
+    uint32_t koff[DMA], voff[DMA];
 #pragma unroll
     for (int i = 0; i < DMA; ++i) {
         const int slot = (i * kWaves + wave) * 64 + lane;
         sl_key[i] = slot / NCH;
         sl_ck[i] = (slot % NCH) ^ k_swz<NCH>(sl_key[i]);
         sl_cv[i] = (slot % NCH) ^ v_swz<D>(sl_key[i]);
+        koff[i] = 16u * (uint32_t)(sl_key[i] * NCH + sl_ck[i]);
+        voff[i] = 16u * (uint32_t)(sl_key[i] * NCH + sl_cv[i]);
     }
-    auto issue = [&](int j0, int st) {
+    auto issue = [&](int j0, auto st_c) __attribute__((always_inline)) {
+        constexpr int ST = decltype(st_c)::value;
         const bool special = (j0 + kBN > a.kv_len) ||
                              (has_new && j0 + kBN > a.new_begin && j0 < a.new_begin + a.n_new);
-        // Row j0's first word and the row stride; a paged block (j0 and the page size are
-        // multiples of 64) lies in one page, looked up once (stride 0: unmapped, zero row).
-        const u32x4* kb0 = kg;
-        const u32x4* vb0 = vg;
-        int stride = NCH;
+        // Row j0's first word; a paged block (j0 and the page size are multiples of 64) lies in
+        // one page, looked up once (-1: unmapped, read as zero rows).
+        const u32x4* kb0 = kg + (PAGED ? 0 : (size_t)j0 * NCH);
+        const u32x4* vb0 = vg + (PAGED ? 0 : (size_t)j0 * NCH);
+        bool mapped = true;
         if constexpr (PAGED) {
             const int64_t pr = paged_row_uniform(a.block_table, a.page_shift, a.n_kv_heads, h, j0);
-            if (pr < 0) {
-                kb0 = zero;
-                vb0 = zero;
-                stride = 0;
-            } else {
-                kb0 = kg + (size_t)pr * NCH;
-                vb0 = vg + (size_t)pr * NCH;
+            mapped = pr >= 0;
+            kb0 = kg + (size_t)(mapped ? pr : 0) * NCH;
+            vb0 = vg + (size_t)(mapped ? pr : 0) * NCH;
+        }
+        if (!special && mapped) {
+            const uint64_t kbase = uniform_address(kb0);
+            const uint64_t vbase = uniform_address(vb0);
+#pragma unroll
+            for (int i = 0; i < DMA; ++i) {
+                const int base = (i * kWaves + wave) * 64;
+                dma16_sbase(kbase, koff[i], lds_addr(&lds_k[ST][base]));
+                dma16_sbase(vbase, voff[i], lds_addr(&lds_v[ST][base]));
             }
+            return;
         }
 #pragma unroll
         for (int i = 0; i < DMA; ++i) {
             const int row_idx = j0 + sl_key[i];
-            const size_t roff = PAGED ? (size_t)sl_key[i] * stride : (size_t)row_idx * NCH;
-            const u32x4* sk = kb0 + roff + sl_ck[i];
-            const u32x4* sv = vb0 + roff + sl_cv[i];
-            if (special) {
-                const unsigned r_new = (unsigned)(row_idx - a.new_begin);
-                if (row_idx >= a.kv_len) {
-                    sk = zero + sl_ck[i];
-                    sv = zero + sl_cv[i];
-                } else if (has_new && r_new < (unsigned)a.n_new) {
-                    sk = kn + (size_t)r_new * NCH + sl_ck[i];
-                    sv = vn + (size_t)r_new * NCH + sl_cv[i];
-                }
+            const unsigned r_new = (unsigned)(row_idx - a.new_begin);
+            const u32x4* sk;
+            const u32x4* sv;
+            if (row_idx >= a.kv_len || !mapped) {
+                sk = zero + sl_ck[i];
+                sv = zero + sl_cv[i];
+            } else if (has_new && r_new < (unsigned)a.n_new) {
+                sk = kn + (size_t)r_new * NCH + sl_ck[i];
+                sv = vn + (size_t)r_new * NCH + sl_cv[i];
+            } else {
+                sk = kb0 + (size_t)sl_key[i] * NCH + sl_ck[i];
+                sv = vb0 + (size_t)sl_key[i] * NCH + sl_cv[i];
             }
             const int base = (i * kWaves + wave) * 64;
-            dma16(sk, lds_addr(&lds_k[st][base]));
-            dma16(sv, lds_addr(&lds_v[st][base]));
+            dma16(sk, lds_addr(&lds_k[ST][base]));
+            dma16(sv, lds_addr(&lds_v[ST][base]));
         }
     };
 
@@ -355,8 +371,8 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
     // lane addresses key (lane%16)/4 + 4*half of the step's key base and dims
     // mt*32 + 16*((lane/16)%2) + 4*(lane%4); the step's key base (a multiple of 4) only adds a
     // constant, and the swizzle depends on the key's low two bits alone.
-    // LDS byte addresses in stage 0; a block adds its stage's (uniform) offset once, and the
-    // per-step parts are compile-time constants (instruction offsets).
+    // LDS byte addresses in stage 0; the stage (the loop below runs one copy of its body per
+    // stage) and the per-step parts are compile-time constants: instruction offsets.
     uint32_t kaddr[KSTEPS];
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks)
@@ -385,15 +401,16 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks) qb[ks] = row_ok ? qp[2 * ks + half] : u32x4{0u, 0u, 0u, 0u};
     }
-    if (n_blocks > 0) issue(seg_begin, 0);
-    if (n_blocks > 1) issue(seg_begin + kBN, 1);
+    if (n_blocks > 0) issue(seg_begin, std::integral_constant<int, 0>{});
+    if (n_blocks > 1) issue(seg_begin + kBN, std::integral_constant<int, 1>{});
     if (has_new) append_share();
     // Retire everything now (Q, the append and the first blocks, issued together): with none of
     // its own loads pending, the compiler inserts no wait-for-everything inside the loop, where
     // the stage ring's loads are in flight.
     wait_vmcnt<0>();
-    for (int blk = 0; blk < n_blocks; ++blk) {
-        const int st = blk % kStages;
+    // Block blk of the segment, in ring stage ST = blk % kStages.
+    auto block = [&](int blk, auto st_c) __attribute__((always_inline)) {
+        constexpr int ST = decltype(st_c)::value;
         const int j0 = seg_begin + blk * kBN;
         // This thread's loads of block blk are done once at most the next block's remain
         // (blocks 0 and 1 were retired before the loop).
@@ -401,10 +418,10 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
             if (blk + 1 < n_blocks) wait_vmcnt<LPB>(); else wait_vmcnt<0>();
         }
         stage_barrier();  // every wave's block blk landed; block blk-1's stage is free
-        if (blk + 2 < n_blocks) issue(j0 + 2 * kBN, (blk + 2) % kStages);
-        if (j0 >= wave_hi) continue;  // this wave's rows see no key of the block
+        if (blk + 2 < n_blocks) issue(j0 + 2 * kBN, std::integral_constant<int, (ST + 2) % kStages>{});
+        if (j0 >= wave_hi) return;  // this wave's rows see no key of the block
 
-        const uint32_t stage_off = (uint32_t)st * (uint32_t)(TILE * 16);
+        constexpr int kStageOff = ST * TILE * 16;  // bytes from stage 0 to stage ST
 
         // ---- S^T = K . Q^T (raw scores) ----
         f32x16 sacc[2];
@@ -419,13 +436,13 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // nothing else outstanding on lgkm
         constexpr uint32_t kKt = 32 * NCH * 16;                  // bytes between the two key tiles
         u32x4 kf[KSTEPS][2];
-        kf[0][0] = lds_read128(kaddr[0] + stage_off);
-        kf[0][1] = lds_read128(kaddr[0] + stage_off + kKt);
+        kf[0][0] = lds_read128<kStageOff>(kaddr[0]);
+        kf[0][1] = lds_read128<kStageOff + kKt>(kaddr[0]);
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks) {
             if (ks + 1 < KSTEPS) {
-                kf[ks + 1][0] = lds_read128(kaddr[ks + 1] + stage_off);
-                kf[ks + 1][1] = lds_read128(kaddr[ks + 1] + stage_off + kKt);
+                kf[ks + 1][0] = lds_read128<kStageOff>(kaddr[ks + 1]);
+                kf[ks + 1][1] = lds_read128<kStageOff + kKt>(kaddr[ks + 1]);
                 lgkm_wait<2>(kf[ks][0], kf[ks][1]);
             } else {
                 lgkm_wait<0>(kf[ks][0], kf[ks][1]);
@@ -497,9 +514,8 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
             constexpr int i = decltype(step_c)::value;
             constexpr int st_i = i % 4;
             constexpr int kb = 32 * (st_i >> 1) + 16 * (st_i & 1);  // step's key base (half adds 4)
-            const uint32_t va = vaddr[i / 4] + stage_off;
-            vf[i][0] = lds_read_tr64<kb * (D * 2)>(va);
-            vf[i][1] = lds_read_tr64<(kb + 8) * (D * 2)>(va);
+            vf[i][0] = lds_read_tr64<kStageOff + kb * (D * 2)>(vaddr[i / 4]);
+            vf[i][1] = lds_read_tr64<kStageOff + (kb + 8) * (D * 2)>(vaddr[i / 4]);
         };
         read_v(std::integral_constant<int, 0>{});
         static_for<PV>([&](auto step_c) {
@@ -513,6 +529,12 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
             const u32x4 vw = {vf[i][0].x, vf[i][0].y, vf[i][1].x, vf[i][1].y};
             o[i / 4] = mfma32(vw, pb[i % 4], o[i / 4]);
         });
+    };
+    static_assert(kStages == 3, "one copy of the block body per ring stage");
+    for (int blk = 0; blk < n_blocks; blk += kStages) {
+        block(blk, std::integral_constant<int, 0>{});
+        if (blk + 1 < n_blocks) block(blk + 1, std::integral_constant<int, 1>{});
+        if (blk + 2 < n_blocks) block(blk + 2, std::integral_constant<int, 2>{});
     }
 
     if (!row_ok) return;
@@ -565,9 +587,9 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
 //
 // One work-group per (query head, 32-row block): a 256-row chunk over 32 query heads is 256
 // work-groups, one per CU, with no KV segments across work-groups and so no partials and no merge
-// launch.  The four waves (one per SIMD) take the row block's 32-key blocks in turn (wave w: blocks
-// w, w+4, ...), each streaming its own K and V tiles through a private two-stage LDS ring with
-// direct-to-LDS loads, so no wave waits for another inside the loop.  At the end the waves merge
+// launch.  The NW = 8 waves (two per SIMD) take the row block's 32-key blocks in turn (wave w:
+// blocks w, w+8, ...), each streaming its own K and V tile (one of each, refilled as soon as it has
+// been read) with direct-to-LDS loads, so no wave waits for another inside the loop.  At the end the waves merge
 // their (m, l, O) through LDS and write the bf16 rows.  Grid x is the kv head: work-groups are dealt
 // to the XCDs round robin by linear index, so with 8 kv heads every work-group reading one head's
 // K/V runs on the same XCD and finds them in its L2.  Fragment layouts are prefill_kernel's with one
