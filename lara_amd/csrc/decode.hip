@@ -453,8 +453,7 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
             sv[i] = (key0 + 4 * grp + i < k_end) ? sacc[i] * a.scale_log2 : -INFINITY;
             mx = fmaxf(mx, sv[i]);
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        mx = pair_max32(pair_max16(mx));
         const float m_cand = fmaxf(m_run, mx);
         if (__ballot(m_cand > m_run + kRescaleSlack) != 0) {
             const float corr = (m_cand == -INFINITY) ? 1.f : fast_exp2(m_run - m_cand);
@@ -485,8 +484,7 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
     // ---- merge the waves of this work-group ----
     __syncthreads();  // every wave is done with its K/V tiles, whose space lds_o reuses
     {
-        float l_head = l_lane + __shfl_xor(l_lane, 16);
-        l_head += __shfl_xor(l_head, 32);
+        const float l_head = pair_sum32(pair_sum16(l_lane));
         const int hq = lane & 15, grp = lane >> 4;
         if (hq < G) {
 #pragma unroll

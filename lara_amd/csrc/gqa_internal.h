@@ -9,6 +9,29 @@ namespace lara {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// Cross-lane reductions over lane pairs (l, l ^ 16) and (l, l ^ 32) without an LDS round trip.
+// v_permlane16_swap (v_permlane32_swap) of a register with itself exchanges the odd 16-lane rows
+// (the upper 32-lane half) of its first result with the even rows (lower half) of its second, so
+// of the two results one holds the lane's own value and the other its partner's: their max (sum)
+// is the pair's max (sum), with no select on the lane's position.  (A two-term fp32 sum is the
+// same word in either order.)
+__device__ __forceinline__ float pair_max16(float x) {
+    const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+}
+__device__ __forceinline__ float pair_max32(float x) {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+}
+__device__ __forceinline__ float pair_sum16(float x) {
+    const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+}
+__device__ __forceinline__ float pair_sum32(float x) {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+}
+
 // Where a kernel goes: its stream and, while profiling, a start/stop event pair that the runtime
 // stamps with the launch's own begin and end (hipExtLaunchKernel binds them to the dispatch
 // itself, so no marker command sits between timed launches and they run back to back).

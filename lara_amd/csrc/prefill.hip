@@ -471,7 +471,7 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
                 for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[kt][i]);
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        mx = pair_max32(mx);
         const float bm = mx * c;  // block max in log2 units (-inf if every key is masked)
         const bool grow = bm > m_run + kLazyLog2;
         if (__ballot(grow) != 0) {
@@ -860,7 +860,7 @@ __global__ __launch_bounds__(NW * 64) void prefill_rows_kernel(PrefillArgs a) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[i]);
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        mx = pair_max32(mx);
         const float bm = mx * c;
         const bool grow = bm > m_run + kLazyLog2;
         if (__ballot(grow) != 0) {
