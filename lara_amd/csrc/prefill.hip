@@ -645,7 +645,10 @@ __global__ __launch_bounds__(NW * 64) void prefill_rows_kernel(PrefillArgs a) {
     const int half = lane >> 5;  // which 8 k-values of a step this lane carries
     const int row = rb * kRows + col;
     const bool row_ok = row < a.q_len;
-    const int q_pos = a.q_pos_base + row;
+    // Keys j < key_lim are valid for this lane's row: below kv_len and, causal, at or before the
+    // row's position (kv_pos_base + j <= q_pos_base + row); none for a row past q_len.
+    const int key_lim =
+        row_ok ? min(a.kv_len, a.causal ? a.q_pos_base + row - a.kv_pos_base + 1 : a.kv_len) : 0;
 
     const u32x4* kg = reinterpret_cast<const u32x4*>(a.kc + (PAGED ? 0 : (size_t)h * a.l_cap * D));
     const u32x4* vg = reinterpret_cast<const u32x4*>(a.vc + (PAGED ? 0 : (size_t)h * a.l_cap * D));
@@ -849,11 +852,10 @@ __global__ __launch_bounds__(NW * 64) void prefill_rows_kernel(PrefillArgs a) {
             (j0 + kRowBN > a.kv_len) || (a.causal && a.kv_pos_base + j0 + kRowBN - 1 > a.q_pos_base + rb * kRows);
         float mx = -INFINITY;
         if (need_mask) {
+            const int d = key_lim - (j0 + 4 * half);  // key j0 + 4*half + c is valid iff c < d
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                const int j = j0 + 8 * (i >> 2) + 4 * half + (i & 3);
-                const bool ok = row_ok && j < a.kv_len && (!a.causal || a.kv_pos_base + j <= q_pos);
-                sacc[i] = ok ? sacc[i] : -INFINITY;
+                sacc[i] = 8 * (i >> 2) + (i & 3) < d ? sacc[i] : -INFINITY;
                 mx = fmaxf(mx, sacc[i]);
             }
         } else {
