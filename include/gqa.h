@@ -334,7 +334,7 @@ int gqa_layer_times(gqa_ctx* ctx, float* out_us, int32_t n);
  * No reference counterpart (the board's transaction is driven by CSR writes).  For callers that
  * must capture (a serving loop that replays a whole captured step, harnesses that only accept
  * graphs): on this ROCm a replay costs the host more than the eager launches of the same step,
- * so eager calls are the faster path (B1 x 4097 keys: 25-45 us per replayed step against 9-10 us
+ * so eager calls are the faster path (B1 x 4097 keys: 25-45 us per replayed step against about 9 us
  * eager, back to back).  gqa_graph_capture_decode_append records one
  * gqa_decode_append_device step (k_rows = v_rows = positions = NULL: gqa_decode_device) with
  * these device pointers into a HIP graph; gqa_graph_launch replays it on `stream` (NULL = the
