@@ -20,14 +20,15 @@
 //                                                          V^T from LDS through transposing
 //                                                          reads (A), P^T from VGPRs (B)
 // Computing the transposed products keeps every lane on one query row (column l % 32 of the
-// MFMA result), so the softmax state of a row and its O accumulator live in the same lane
-// and no cross-lane shuffle is needed between the two products.
+// MFMA result; lanes l and l + 32 hold two halves of the row's keys), so the softmax state of
+// a row and its O accumulator live in the same lane pair: between the two products the only
+// cross-lane step is the pair's row max (v_permlane32_swap).
 //
 // Staging.  K and V tiles stream from HBM straight into a three-stage LDS ring with
 // direct-to-LDS loads (no register staging): while block j is computed, blocks j+1 and j+2
-// are in flight.  Each lane picks the global 16-byte chunk that the swizzled LDS layout wants
-// in its slot -- the cache row, the row this launch appends, or a zero row past kv_len (P is 0
-// there, and V must be finite).
+// are in flight.  Each lane loads the global 16-byte chunk that the swizzled LDS layout wants
+// in its slot -- the cache row (from a wave-uniform base and a fixed per-lane offset), the row
+// this launch appends, or a zero row past kv_len (P is 0 there, and V must be finite).
 //
 // MFMA 32x32x16 operand layout used below: lane l supplies row (A) / column (B) l % 32 and
 // the eight k-values 8*(l/32)..8*(l/32)+7 of the step; result register i of lane l holds
