@@ -81,11 +81,17 @@ extern "C" {
  * block, query head) tasks shares each K/V tile over its GQA group; launches smaller than the GPU are
  * cut into KV segments merged by a second launch (GQA_OPT_PREFILL_WGS).  ROWS: a work-group per
  * (query head, 32-row block) whose waves split the keys and merge in LDS (one launch, no segments).
+ * PAIRED: SHARED whose work-groups each own a long and a short causal row block (last and first),
+ * the short one's waves moving to the long one's keys once theirs end, so the work-groups of a causal
+ * launch carry equal work (causal launches of group 4 in one KV segment; others as SHARED).
  * AUTO (default): ROWS when the SHARED grid without segments has fewer work-groups than the GPU has
- * CUs and no segment target is set, else SHARED. */
+ * CUs and no segment target is set; else PAIRED where it applies and the grid is at most one
+ * work-group per CU (a single dispatch round, which longest-first dispatch cannot balance); else
+ * SHARED. */
 #define GQA_PREFILL_KERNEL_AUTO   0
 #define GQA_PREFILL_KERNEL_SHARED 1
 #define GQA_PREFILL_KERNEL_ROWS   2
+#define GQA_PREFILL_KERNEL_PAIRED 3
 
 /* Split merge of the decode (GQA_OPT_DECODE_MERGE).  FUSED: the last split of a (sequence, kv head) to
  * finish merges the others' partials inside the decode launch (agent-scope atomics and a per-unit

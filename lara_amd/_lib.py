@@ -59,6 +59,7 @@ GQA_MAX_LAYERS = 1024
 GQA_PREFILL_KERNEL_AUTO = 0
 GQA_PREFILL_KERNEL_SHARED = 1
 GQA_PREFILL_KERNEL_ROWS = 2
+GQA_PREFILL_KERNEL_PAIRED = 3
 GQA_NUMERICS_EXACT = 0
 GQA_NUMERICS_KV260 = 1
 

@@ -373,6 +373,13 @@ int run_prefill(gqa_ctx* c, int32_t b, const void* q, int32_t q_len, int32_t q_p
         HIP_TRY(launch_prefill_rows(c->cfg.head_dim, a, timed(c, GQA_TIMER_PREFILL, s)));
         return GQA_OK;
     }
+    // Paired causal row blocks: the work of a causal grid grows with the row block, and a grid of one
+    // dispatch round (at most one work-group per CU) cannot be balanced by longest-first dispatch.
+    const bool can_pair = causal && c->group == 4 && plan.n_segs == 1 && q_len > kPrefillRows;
+    a.pair = can_pair && (c->prefill_kernel == GQA_PREFILL_KERNEL_PAIRED ||
+                          (c->prefill_kernel == GQA_PREFILL_KERNEL_AUTO &&
+                           prefill_shared_wgs(q_len, c->group, c->cfg.n_kv_heads) <= c->n_cu))
+                 ? 1 : 0;
     HIP_TRY(launch_prefill(c->cfg.head_dim, c->group, a, timed(c, GQA_TIMER_PREFILL, s)));
     if (plan.n_segs > 1) HIP_TRY(launch_prefill_combine(c->cfg.head_dim, a, timed(c, GQA_TIMER_COMBINE, s)));
     return GQA_OK;
@@ -972,7 +979,7 @@ int gqa_set_option(gqa_ctx* c, int32_t option, int64_t value) {
             return profile_enable(c, value ? 1 : 0);
         case GQA_OPT_PREFILL_KERNEL:
             if (value != GQA_PREFILL_KERNEL_AUTO && value != GQA_PREFILL_KERNEL_SHARED &&
-                value != GQA_PREFILL_KERNEL_ROWS)
+                value != GQA_PREFILL_KERNEL_ROWS && value != GQA_PREFILL_KERNEL_PAIRED)
                 return GQA_ERR_RANGE;
             c->prefill_kernel = (int)value;
             return GQA_OK;

@@ -117,6 +117,7 @@ struct PrefillArgs {
     // contiguous cache of sequence b as above.
     const int32_t* block_table;
     int32_t page_shift;
+    int32_t pair;           // 1: paired causal row blocks (G = 4, one segment; prefill_kernel)
 };
 
 // Row index (in units of D elements) of token row t of (sequence-relative) kv head h in a paged
@@ -146,6 +147,7 @@ struct PrefillPlan {
     int32_t seg_len;
     int32_t n_segs;
 };
+constexpr int kPrefillRows = 32;  // query rows per prefill wave (a row block)
 PrefillPlan plan_prefill(int q_len, int kv_span, int group, int n_kv_heads, int target_wgs, int max_segs);
 // fp32 words of partial-output workspace a plan needs (O and (m, l) per row, per segment).
 size_t prefill_workspace_floats(const PrefillPlan& p, int q_len, int n_q_heads, int head_dim);

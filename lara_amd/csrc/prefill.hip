@@ -50,7 +50,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBN = 64;     // keys per block
-constexpr int kRows = 32;   // query rows per wave
+constexpr int kRows = kPrefillRows;  // query rows per wave
 constexpr int kWaves = 8;   // waves per work-group: (row block, head) tasks, heads fastest
 constexpr int kStages = 3;  // LDS ring depth: two blocks in flight behind the one computed
 constexpr float kLn2 = 0.693147180559945309f;
@@ -155,6 +155,13 @@ __device__ __forceinline__ void lgkm_wait(T& a, T& b) {
     asm volatile("s_waitcnt %2" : "+v"(a), "+v"(b) : "i"(0xF | (0x3 << 14) | (0x7 << 4) | (N << 8)));
 }
 
+// s_waitcnt lgkmcnt(N) that the compiler sees as producing a (one fragment; see lgkm_wait).
+template <int N, typename T>
+__device__ __forceinline__ void lgkm_wait1(T& a) {
+    static_assert(N >= 0 && N < 16, "lgkmcnt range");
+    asm volatile("s_waitcnt %1" : "+v"(a) : "i"(0xF | (0x3 << 14) | (0x7 << 4) | (N << 8)));
+}
+
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // Calls f(std::integral_constant<int, i>) for i = 0 .. N-1 (compile-time indices).
@@ -198,7 +205,7 @@ __device__ __forceinline__ int v_swz(int key) {
 // addresses key (lane%16)/4 of the four, dims d_g + 4*(lane%4) .. +3, and receives one dim of
 // four keys.
 
-template <int D, int G, bool PAGED>
+template <int D, int G, bool PAGED, bool PAIR>
 __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
     constexpr int NCH = D / 8;                   // 16-byte chunks per K/V row
     constexpr int KSTEPS = D / 16;               // QK k-steps
@@ -210,6 +217,10 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
 
     __shared__ __attribute__((aligned(16))) u32x4 lds_k[kStages][TILE];
     __shared__ __attribute__((aligned(16))) u32x4 lds_v[kStages][TILE];
+    // PAIR: row block L's Q^T operand handed from wave g to wave g + 4, then that wave's bf16 output
+    // rows of row block S ([32 rows][D], 16-byte chunks XOR-swizzled by the row).
+    __shared__ __attribute__((aligned(16))) u32x4 lds_q[PAIR ? 4 : 1][PAIR ? KSTEPS : 1][64];
+    static_assert(!PAIR || (G == 4 && kWaves == 8), "paired row blocks: two row blocks of four heads");
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -224,12 +235,20 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
     const int n_tasks = n_rb * G;
     // Causal row blocks grow in work with their index: the largest go to the work-groups the
     // dispatcher starts first (longest first), so a grid larger than the GPU balances.
-    const int wg_x = a.causal ? (int)(gridDim.x - 1 - wx) : wx;
-    const int task = wg_x * kWaves + wave;
+    // PAIR (a causal grid of one dispatch round): work-group p owns row blocks L = n_rb - 1 - p and
+    // S = p, heads 0-3 each.  Waves 0-3 work on L from the first key; waves 4-7 work on S while a block
+    // holds keys of S, then on L: from that block on (split_blk) every block is cut in two halves of
+    // 32 keys, the first for waves 0-3 and the second for waves 4-7, whose partials of L merge in
+    // LDS at the end.  Every work-group then carries about (keys(L) + keys(S)) / 2 key blocks per
+    // wave, instead of keys(L) for the work-groups of the last row blocks.
+    const int wg_x = (a.causal && !PAIR) ? (int)(gridDim.x - 1 - wx) : wx;
+    const int task = PAIR ? (n_rb - 1 - wx) * G + (wave & 3) : wg_x * kWaves + wave;
     const bool active = task < n_tasks;
     const int g = task % G;
-    const int rb = task / G;
+    const int rb = task / G;  // PAIR: row block L (every wave's last)
     const int hq = h * G + g;
+    const bool has_s = PAIR && wx < rb;                 // PAIR: the work-group has a row block S
+    const int rb_first = (has_s && wave >= 4) ? wx : rb;  // the row block the wave starts on
 
     // Keys a row block needs: [0, kv_limit) (causal rows stop at their diagonal).
     auto kv_limit = [&](int row_block) {
@@ -269,8 +288,8 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
         }
     };
     const int last_task = min(n_tasks, (wg_x + 1) * kWaves) - 1;
-    const int wg_hi = kv_limit(last_task / G);  // row blocks grow with the task index
-    const int wave_hi = active ? kv_limit(rb) : 0;
+    const int wg_hi = PAIR ? kv_limit(rb) : kv_limit(last_task / G);  // row blocks grow with the task index
+    int wave_hi = active ? kv_limit(rb_first) : 0;
     const int seg_begin = blockIdx.z * a.seg_len;
     // With several segments, one that no row of this work-group reaches is not read by the
     // merge; a single segment always reaches the epilogue (rows without keys output 0).
@@ -283,9 +302,10 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
 
     const int col = lane & 31;   // query row within the wave's block (MFMA column)
     const int half = lane >> 5;  // which 8 k-values of a step this lane carries
-    const int row = rb * kRows + col;
-    const bool row_ok = active && row < a.q_len;
-    const int q_pos = a.q_pos_base + row;
+    int cur_rb = rb_first;       // the row block the wave works on (PAIR: S, then L)
+    const int row0 = cur_rb * kRows + col;
+    const bool row0_ok = active && row0 < a.q_len;
+    const int q_pos0 = a.q_pos_base + row0;
 
     f32x16 o[MT];
 #pragma unroll
@@ -398,9 +418,9 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
     // K/V loads and the append share's loads are all in flight before the first wait.
     u32x4 qb[KSTEPS];
     {
-        const u32x4* qp = reinterpret_cast<const u32x4*>(a.q + ((size_t)hq * a.q_len + row) * D);
+        const u32x4* qp = reinterpret_cast<const u32x4*>(a.q + ((size_t)hq * a.q_len + row0) * D);
 #pragma unroll
-        for (int ks = 0; ks < KSTEPS; ++ks) qb[ks] = row_ok ? qp[2 * ks + half] : u32x4{0u, 0u, 0u, 0u};
+        for (int ks = 0; ks < KSTEPS; ++ks) qb[ks] = row0_ok ? qp[2 * ks + half] : u32x4{0u, 0u, 0u, 0u};
     }
     if (n_blocks > 0) issue(seg_begin, std::integral_constant<int, 0>{});
     if (n_blocks > 1) issue(seg_begin + kBN, std::integral_constant<int, 1>{});
@@ -409,25 +429,27 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
     // its own loads pending, the compiler inserts no wait-for-everything inside the loop, where
     // the stage ring's loads are in flight.
     wait_vmcnt<0>();
-    // Block blk of the segment, in ring stage ST = blk % kStages.
-    auto block = [&](int blk, auto st_c) __attribute__((always_inline)) {
-        constexpr int ST = decltype(st_c)::value;
-        const int j0 = seg_begin + blk * kBN;
-        // This thread's loads of block blk are done once at most the next block's remain
-        // (blocks 0 and 1 were retired before the loop).
-        if (blk >= 1) {
-            if (blk + 1 < n_blocks) wait_vmcnt<LPB>(); else wait_vmcnt<0>();
+    if constexpr (PAIR) {
+        // Waves 0-3 hand row block L's Q^T operand to waves 4-7 (read once they move to L, after
+        // at least one barrier).
+        if (wave < 4) {
+#pragma unroll
+            for (int ks = 0; ks < KSTEPS; ++ks) lds_q[wave][ks][lane] = qb[ks];
         }
-        stage_barrier();  // every wave's block blk landed; block blk-1's stage is free
-        if (blk + 2 < n_blocks) issue(j0 + 2 * kBN, std::integral_constant<int, (ST + 2) % kStages>{});
-        if (j0 >= wave_hi) return;  // this wave's rows see no key of the block
+    }
+    constexpr uint32_t kKt = 32 * NCH * 16;  // bytes between the two 32-key tiles of a block
 
+    // The block's math for NT 32-key tiles at key jb (NT = 2: the whole block; NT = 1: the half
+    // a PAIR wave takes, its tile offset already in kaddr / vaddr), ring stage ST.
+    auto compute = [&](int jb, auto st_c, auto nt_c) __attribute__((always_inline)) {
+        constexpr int ST = decltype(st_c)::value;
+        constexpr int NT = decltype(nt_c)::value;
         constexpr int kStageOff = ST * TILE * 16;  // bytes from stage 0 to stage ST
 
         // ---- S^T = K . Q^T (raw scores) ----
-        f32x16 sacc[2];
+        f32x16 sacc[NT];
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
+        for (int kt = 0; kt < NT; ++kt)
 #pragma unroll
             for (int i = 0; i < 16; ++i) sacc[kt][i] = 0.f;
         // K fragments are double-buffered: step ks+1's LDS reads are in flight while step ks's
@@ -435,40 +457,45 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
         // Fully unrolled, every fragment is its own value: none is copied while its read is in
         // flight.
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // nothing else outstanding on lgkm
-        constexpr uint32_t kKt = 32 * NCH * 16;                  // bytes between the two key tiles
-        u32x4 kf[KSTEPS][2];
-        kf[0][0] = lds_read128<kStageOff>(kaddr[0]);
-        kf[0][1] = lds_read128<kStageOff + kKt>(kaddr[0]);
+        u32x4 kf[KSTEPS][NT];
+        auto read_k = [&](int ks) __attribute__((always_inline)) {
+            kf[ks][0] = lds_read128<kStageOff>(kaddr[ks]);
+            if constexpr (NT == 2) kf[ks][1] = lds_read128<kStageOff + kKt>(kaddr[ks]);
+        };
+        read_k(0);
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks) {
             if (ks + 1 < KSTEPS) {
-                kf[ks + 1][0] = lds_read128<kStageOff>(kaddr[ks + 1]);
-                kf[ks + 1][1] = lds_read128<kStageOff + kKt>(kaddr[ks + 1]);
-                lgkm_wait<2>(kf[ks][0], kf[ks][1]);
+                read_k(ks + 1);
+                if constexpr (NT == 2) lgkm_wait<2>(kf[ks][0], kf[ks][1]); else lgkm_wait1<1>(kf[ks][0]);
             } else {
-                lgkm_wait<0>(kf[ks][0], kf[ks][1]);
+                if constexpr (NT == 2) lgkm_wait<0>(kf[ks][0], kf[ks][1]); else lgkm_wait1<0>(kf[ks][0]);
             }
-            sacc[0] = mfma32(kf[ks][0], qb[ks], sacc[0]);
-            sacc[1] = mfma32(kf[ks][1], qb[ks], sacc[1]);
+#pragma unroll
+            for (int kt = 0; kt < NT; ++kt) sacc[kt] = mfma32(kf[ks][kt], qb[ks], sacc[kt]);
         }
 
         // ---- online softmax (log2 domain, scale folded into the exponent) ----
-        const bool need_mask =
-            (j0 + kBN > a.kv_len) || (a.causal && a.kv_pos_base + j0 + kBN - 1 > a.q_pos_base + rb * kRows);
+        const int row = PAIR ? cur_rb * kRows + col : row0;
+        const bool row_ok = PAIR ? active && row < a.q_len : row0_ok;
+        const int q_pos = PAIR ? a.q_pos_base + row : q_pos0;
+        const int rb_now = PAIR ? cur_rb : rb;
+        const bool need_mask = (jb + 32 * NT > a.kv_len) ||
+                               (a.causal && a.kv_pos_base + jb + 32 * NT - 1 > a.q_pos_base + rb_now * kRows);
         float mx = -INFINITY;
         if (need_mask) {
 #pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
+            for (int kt = 0; kt < NT; ++kt)
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
-                    const int j = j0 + kt * 32 + 8 * (i >> 2) + 4 * half + (i & 3);
+                    const int j = jb + kt * 32 + 8 * (i >> 2) + 4 * half + (i & 3);
                     const bool ok = row_ok && j < a.kv_len && (!a.causal || a.kv_pos_base + j <= q_pos);
                     sacc[kt][i] = ok ? sacc[kt][i] : -INFINITY;
                     mx = fmaxf(mx, sacc[kt][i]);
                 }
         } else {
 #pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
+            for (int kt = 0; kt < NT; ++kt)
 #pragma unroll
                 for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[kt][i]);
         }
@@ -489,9 +516,9 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
         // as well, and a finite offset keeps 2^(-inf) = 0 without a per-score select.
         const float nm = (m_run == -INFINITY) ? 0.f : -m_run;
         float psum = 0.f;
-        u32x4 pb[4];  // P^T operand of the four PV k-steps (kt, a2)
+        u32x4 pb[2 * NT];  // P^T operand of the PV k-steps (kt, a2)
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
+        for (int kt = 0; kt < NT; ++kt)
 #pragma unroll
             for (int a2 = 0; a2 < 2; ++a2) {
                 float p[8];
@@ -509,14 +536,15 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
         // ---- O^T += V^T . P^T ----
         // Step i = (mt, st_i): the two transposing reads of step i+1 are issued before step i's
         // MFMA, as in the S^T phase.
-        constexpr int PV = MT * 4;
+        constexpr int SPT = 2 * NT;  // k-steps per PV tile
+        constexpr int PV = MT * SPT;
         u32x2 vf[PV][2];
         auto read_v = [&](auto step_c) {
             constexpr int i = decltype(step_c)::value;
-            constexpr int st_i = i % 4;
+            constexpr int st_i = i % SPT;
             constexpr int kb = 32 * (st_i >> 1) + 16 * (st_i & 1);  // step's key base (half adds 4)
-            vf[i][0] = lds_read_tr64<kStageOff + kb * (D * 2)>(vaddr[i / 4]);
-            vf[i][1] = lds_read_tr64<kStageOff + (kb + 8) * (D * 2)>(vaddr[i / 4]);
+            vf[i][0] = lds_read_tr64<kStageOff + kb * (D * 2)>(vaddr[i / SPT]);
+            vf[i][1] = lds_read_tr64<kStageOff + (kb + 8) * (D * 2)>(vaddr[i / SPT]);
         };
         read_v(std::integral_constant<int, 0>{});
         static_for<PV>([&](auto step_c) {
@@ -528,16 +556,165 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
                 lgkm_wait<0>(vf[i][0], vf[i][1]);
             }
             const u32x4 vw = {vf[i][0].x, vf[i][0].y, vf[i][1].x, vf[i][1].y};
-            o[i / 4] = mfma32(vw, pb[i % 4], o[i / 4]);
+            o[i / SPT] = mfma32(vw, pb[i % SPT], o[i / SPT]);
         });
     };
+
+    // PAIR: the move of waves 4-7 from S to L.  S's rows are final: normalised, rounded and kept
+    // in LDS (written to the output after the loop, so no global store is in flight beside the ring's
+    // loads); the wave takes L's Q^T from wave g and starts L with an empty partial.
+    float lse_s = -INFINITY;  // PAIR: S's log-sum-exp (lanes of the first half-wave)
+    auto leave_s = [&]() __attribute__((always_inline)) {
+        const float l_row = l_lane + half_swap(l_lane, half);
+        const float inv = l_row > 0.f ? 1.f / l_row : 0.f;
+        lse_s = l_row > 0.f ? (m_run + log2f(l_row)) * kLn2 : -INFINITY;
+        const int q4 = wave & 3;
+        // L's Q^T first: the stash below takes its place.
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks) qb[ks] = lds_q[q4][ks][lane];
+        uint2* stash = reinterpret_cast<uint2*>(&lds_q[q4][0][0]);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+                uint2 w;
+                w.x = (uint32_t)f32_to_bf16_rne(o[mt][4 * r4 + 0] * inv) | ((uint32_t)f32_to_bf16_rne(o[mt][4 * r4 + 1] * inv) << 16);
+                w.y = (uint32_t)f32_to_bf16_rne(o[mt][4 * r4 + 2] * inv) | ((uint32_t)f32_to_bf16_rne(o[mt][4 * r4 + 3] * inv) << 16);
+                const int chunk = 4 * mt + r4;  // dims 8*chunk .. +7; this lane's four: + 4*half
+                stash[2 * (col * NCH + (chunk ^ (col & (NCH - 1)))) + half] = w;
+            }
+        cur_rb = rb;
+        wave_hi = kv_limit(rb);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[mt][i] = 0.f;
+        m_run = -INFINITY;
+        l_lane = 0.f;
+    };
+    // PAIR: from block split_blk on (the first block past S's keys), waves 0-3 take the first and
+    // waves 4-7 the second 32 keys of every block: their K and V^T read addresses move by 32 keys.
+    const int split_blk = has_s ? (kv_limit(wx) + kBN - 1) / kBN : 0;
+    auto enter_halves = [&]() __attribute__((always_inline)) {
+        if (wave >= 4) {
+#pragma unroll
+            for (int ks = 0; ks < KSTEPS; ++ks) kaddr[ks] += kKt;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) vaddr[mt] += 32 * D * 2;
+            if (cur_rb != rb) leave_s();
+        }
+    };
+
+    // Block blk of the segment, in ring stage ST = blk % kStages: the whole block (NT = 2) or, for
+    // PAIR waves past split_blk, the wave's 32-key half (NT = 1).
+    auto block = [&](int blk, auto st_c, auto nt_c) __attribute__((always_inline)) {
+        constexpr int ST = decltype(st_c)::value;
+        constexpr int NT = decltype(nt_c)::value;
+        const int j0 = seg_begin + blk * kBN;
+        // This thread's loads of block blk are done once at most the next block's remain
+        // (blocks 0 and 1 were retired before the loop).
+        if (blk >= 1) {
+            if (blk + 1 < n_blocks) wait_vmcnt<LPB>(); else wait_vmcnt<0>();
+        }
+        stage_barrier();  // every wave's block blk landed; block blk-1's stage is free
+        if (blk + 2 < n_blocks) issue(j0 + 2 * kBN, std::integral_constant<int, (ST + 2) % kStages>{});
+        const int jb = NT == 2 ? j0 : j0 + 32 * (wave >> 2);
+        if (jb >= wave_hi) return;  // this wave's rows see no key of the block (or half)
+        compute(jb, st_c, nt_c);
+    };
+    // Blocks [b0, b1), one copy of the block body per ring stage.
+    auto run = [&](int b0, int b1, auto nt_c) __attribute__((always_inline)) {
+        int blk = b0;
+        if (blk < b1 && blk % kStages == 1) block(blk++, std::integral_constant<int, 1>{}, nt_c);
+        if (blk < b1 && blk % kStages == 2) block(blk++, std::integral_constant<int, 2>{}, nt_c);
+        for (; blk < b1; blk += kStages) {
+            block(blk, std::integral_constant<int, 0>{}, nt_c);
+            if (blk + 1 < b1) block(blk + 1, std::integral_constant<int, 1>{}, nt_c);
+            if (blk + 2 < b1) block(blk + 2, std::integral_constant<int, 2>{}, nt_c);
+        }
+    };
     static_assert(kStages == 3, "one copy of the block body per ring stage");
-    for (int blk = 0; blk < n_blocks; blk += kStages) {
-        block(blk, std::integral_constant<int, 0>{});
-        if (blk + 1 < n_blocks) block(blk + 1, std::integral_constant<int, 1>{});
-        if (blk + 2 < n_blocks) block(blk + 2, std::integral_constant<int, 2>{});
+    if constexpr (PAIR) {
+        const int split = min(split_blk, n_blocks);
+        stage_barrier();  // the Q hand-off is visible even when no block precedes the move
+        run(0, split, std::integral_constant<int, 2>{});
+        if (split < n_blocks) {
+            enter_halves();
+            run(split, n_blocks, std::integral_constant<int, 1>{});
+        }
+    } else {
+        for (int blk = 0; blk < n_blocks; blk += kStages) {
+            block(blk, std::integral_constant<int, 0>{}, std::integral_constant<int, 2>{});
+            if (blk + 1 < n_blocks) block(blk + 1, std::integral_constant<int, 1>{}, std::integral_constant<int, 2>{});
+            if (blk + 2 < n_blocks) block(blk + 2, std::integral_constant<int, 2>{}, std::integral_constant<int, 2>{});
+        }
     }
 
+    const int row = rb * kRows + col;  // the wave's last row block (PAIR: L)
+    const bool row_ok = active && row < a.q_len;
+    if constexpr (PAIR) {
+        const int q4 = wave & 3;
+        __syncthreads();  // every wave is done with the ring (and waves 0-3 with their Q hand-off)
+        // S's keys all lay before L's last block: waves 4-7 finish S here, with an empty partial of L.
+        if (wave >= 4 && cur_rb != rb) leave_s();
+        // Waves 4-7 publish their partial of L (O^T fragments, running max, l) in the ring's space;
+        // wave g merges it with its own: same lane, same row and dims.
+        float4* part = reinterpret_cast<float4*>(q4 < 2 ? &lds_k[0][0] : &lds_v[0][0]);
+        float2* part_ml = reinterpret_cast<float2*>(part + 2 * MT * 4 * 64) + (q4 & 1) * 64;
+        part += (q4 & 1) * (MT * 4 * 64);
+        const float l_row = l_lane + half_swap(l_lane, half);
+        if (wave >= 4) {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4)
+                    part[(mt * 4 + r4) * 64 + lane] =
+                        make_float4(o[mt][4 * r4], o[mt][4 * r4 + 1], o[mt][4 * r4 + 2], o[mt][4 * r4 + 3]);
+            part_ml[lane] = make_float2(m_run, l_row);
+        }
+        __syncthreads();
+        if (wave < 4) {
+            const float2 mlb = part_ml[lane];
+            const float M = fmaxf(m_run, mlb.x);
+            const float wa = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - M);
+            const float wb = mlb.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mlb.x - M);
+            const float l_sum = fmaf(l_row, wa, mlb.y * wb);
+            if (!row_ok) return;
+            const float inv = l_sum > 0.f ? 1.f / l_sum : 0.f;
+            uint16_t* orow = a.out + ((size_t)hq * a.q_len + row) * D;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4) {
+                    const float4 pb4 = part[(mt * 4 + r4) * 64 + lane];
+                    const float v0 = fmaf(o[mt][4 * r4 + 0], wa, pb4.x * wb) * inv;
+                    const float v1 = fmaf(o[mt][4 * r4 + 1], wa, pb4.y * wb) * inv;
+                    const float v2 = fmaf(o[mt][4 * r4 + 2], wa, pb4.z * wb) * inv;
+                    const float v3 = fmaf(o[mt][4 * r4 + 3], wa, pb4.w * wb) * inv;
+                    uint2 w;
+                    w.x = (uint32_t)f32_to_bf16_rne(v0) | ((uint32_t)f32_to_bf16_rne(v1) << 16);
+                    w.y = (uint32_t)f32_to_bf16_rne(v2) | ((uint32_t)f32_to_bf16_rne(v3) << 16);
+                    *reinterpret_cast<uint2*>(orow + mt * 32 + 8 * r4 + 4 * half) = w;
+                }
+            if (half == 0 && a.lse != nullptr)
+                a.lse[(size_t)hq * a.q_len + row] = l_sum > 0.f ? (M + log2f(l_sum)) * kLn2 : -INFINITY;
+        } else if (has_s) {
+            // S's output rows from the LDS stash, 16 bytes per lane and store.
+            const uint4* stash = reinterpret_cast<const uint4*>(&lds_q[q4][0][0]);
+#pragma unroll
+            for (int it = 0; it < KSTEPS; ++it) {
+                const int qc = it * 64 + lane;  // chunk qc of the [32][D] block: row r, chunk c
+                const int r = qc / NCH, c = qc % NCH;
+                const int srow = wx * kRows + r;
+                if (srow < a.q_len)
+                    *reinterpret_cast<uint4*>(a.out + ((size_t)hq * a.q_len + srow) * D + 8 * c) =
+                        stash[r * NCH + (c ^ (r & (NCH - 1)))];
+            }
+            const int srow = wx * kRows + col;
+            if (half == 0 && a.lse != nullptr && srow < a.q_len) a.lse[(size_t)hq * a.q_len + srow] = lse_s;
+        }
+        return;
+    }
     if (!row_ok) return;
     const float l_row = l_lane + half_swap(l_lane, half);
     if (a.n_segs > 1) {
@@ -597,13 +774,6 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
 // 32-key tile per block (S^T = K . Q^T one 32x32 tile, eight k-steps; O^T += V^T . P^T in two
 // 16-key k-steps per 32-dim tile).
 constexpr int kRowBN = 32;  // keys per block
-
-// s_waitcnt lgkmcnt(N) that the compiler sees as producing a (see lgkm_wait).
-template <int N, typename T>
-__device__ __forceinline__ void lgkm_wait1(T& a) {
-    static_assert(N >= 0 && N < 16, "lgkmcnt range");
-    asm volatile("s_waitcnt %1" : "+v"(a) : "i"(0xF | (0x3 << 14) | (0x7 << 4) | (N << 8)));
-}
 
 // NW waves per work-group take the row block's key blocks in turn.
 template <int D, bool PAGED, int NW>
@@ -1088,8 +1258,17 @@ hipError_t launch_prefill_t(const PrefillArgs& a, const Launch& l) {
     const int n_rb = (a.q_len + kRows - 1) / kRows;
     const int n_tasks = n_rb * G;
     dim3 grid((n_tasks + kWaves - 1) / kWaves, a.n_kv_heads, a.n_segs);
-    if (a.block_table != nullptr) return launch_kernel(prefill_kernel<D, G, true>, grid, dim3(kWaves * 64), l, a);
-    return launch_kernel(prefill_kernel<D, G, false>, grid, dim3(kWaves * 64), l, a);
+    if constexpr (G == 4) {
+        if (a.pair) {
+            // Paired row blocks: causal, one segment (the whole key range in one launch).
+            if (!a.causal || a.n_segs != 1) return hipErrorInvalidValue;
+            if (a.block_table != nullptr)
+                return launch_kernel(prefill_kernel<D, G, true, true>, grid, dim3(kWaves * 64), l, a);
+            return launch_kernel(prefill_kernel<D, G, false, true>, grid, dim3(kWaves * 64), l, a);
+        }
+    }
+    if (a.block_table != nullptr) return launch_kernel(prefill_kernel<D, G, true, false>, grid, dim3(kWaves * 64), l, a);
+    return launch_kernel(prefill_kernel<D, G, false, false>, grid, dim3(kWaves * 64), l, a);
 }
 
 }  // namespace

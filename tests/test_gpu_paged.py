@@ -113,14 +113,15 @@ def test_fused_decode_append_over_a_page_boundary():
             assert np.array_equal(kp, kc) and np.array_equal(vp, vc)
 
 
-@pytest.mark.parametrize("kernel", ["auto", "shared"])
+@pytest.mark.parametrize("kernel", ["auto", "shared", "paired"])
 def test_chunked_prefill_into_pages(kernel):
-    """Chunks of 256 rows take the row-block kernel (auto) or the GQA-shared one (forced): both read
-    the pages' block-table entries through the scalar cache."""
+    """Chunks of 256 rows take the row-block kernel (auto) or the GQA-shared one, unpaired or paired
+    (forced): each reads the pages' block-table entries through the scalar cache."""
     rng = np.random.default_rng(13)
     prompt, chunk = 640, 256
     cont, paged = engines()
-    code = {"auto": _lib.GQA_PREFILL_KERNEL_AUTO, "shared": _lib.GQA_PREFILL_KERNEL_SHARED}[kernel]
+    code = {"auto": _lib.GQA_PREFILL_KERNEL_AUTO, "shared": _lib.GQA_PREFILL_KERNEL_SHARED,
+            "paired": _lib.GQA_PREFILL_KERNEL_PAIRED}[kernel]
     with cont, paged:
         for acc in (cont, paged):
             _lib.check(acc._lib.gqa_set_option(acc._ctx, _lib.GQA_OPT_PREFILL_KERNEL, code), "prefill kernel")

@@ -99,10 +99,11 @@ def test_transaction_protocol_and_busy_start():
 
 
 def set_prefill_kernel(acc, kernel):
-    """Force the prefill decomposition: 'auto', 'shared' (GQA-shared tiles + KV segments) or 'rows'."""
+    """Force the prefill decomposition: 'auto', 'shared' (GQA-shared tiles + KV segments), 'rows' or
+    'paired' (shared tiles, a long and a short causal row block per work-group)."""
     from lara_amd import _lib
     code = {"auto": _lib.GQA_PREFILL_KERNEL_AUTO, "shared": _lib.GQA_PREFILL_KERNEL_SHARED,
-            "rows": _lib.GQA_PREFILL_KERNEL_ROWS}[kernel]
+            "rows": _lib.GQA_PREFILL_KERNEL_ROWS, "paired": _lib.GQA_PREFILL_KERNEL_PAIRED}[kernel]
     _lib.check(acc._lib.gqa_set_option(acc._ctx, _lib.GQA_OPT_PREFILL_KERNEL, code), "prefill kernel")
 
 
@@ -144,6 +145,53 @@ def test_prefill_shapes_ragged(hq, hkv, d, causal, kernel):
         out, lse = acc.prefill_chunk(q, q_pos_base=qb, kv_len=kv_len, kv_pos_base=kb, causal=causal,
                                      return_lse=True)
     ref, ref_lse = oracle_for(q, k, v, causal=causal, q_pos_base=qb, kv_pos_base=kb)
+    check_rows(out, lse, ref, ref_lse)
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (16, 4, 64)])
+@pytest.mark.parametrize("q_len,kv_len,qb,kb", [(33, 33, 0, 0), (64, 64, 0, 0), (96, 96, 0, 0), (333, 333, 0, 0),
+                                                (200, 700, 500, 0), (257, 300, 43, 0), (160, 230, 100, 30),
+                                                (64, 200, 0, 150)])
+def test_prefill_paired_causal(hq, hkv, d, q_len, kv_len, qb, kb):
+    """Paired row blocks (group 4): work-group p owns row blocks n-1-p and p; the short block's waves
+    move to the long block's keys at the first block past their own and the two halves of the long
+    block merge in LDS.  Odd row-block counts (a work-group without a short block), a partial last
+    row block, position bases (rows with no key, chunks after history) and a short block whose keys
+    end in the long block's last block, against the oracle; the short blocks' rows are computed as
+    by the unpaired kernel, word for word."""
+    rng = np.random.default_rng(4000 + q_len + kv_len + qb + kb + d)
+    print(f"[paired] hq={hq} hkv={hkv} d={d} q_len={q_len} kv_len={kv_len} qb={qb} kb={kb}", flush=True)
+    q = bf16_normal(rng, (hq, q_len, d))
+    k = bf16_normal(rng, (hkv, kv_len, d))
+    v = bf16_normal(rng, (hkv, kv_len, d))
+    outs = {}
+    for kernel in ("paired", "shared"):
+        with AttentionAccelerator(n_q_heads=hq, n_kv_heads=hkv, head_dim=d, max_seq_len=kv_len,
+                                  max_q_len=q_len) as acc:
+            set_prefill_kernel(acc, kernel)
+            acc.load_kv(k, v)
+            outs[kernel] = acc.prefill_chunk(q, q_pos_base=qb, kv_len=kv_len, kv_pos_base=kb, causal=True,
+                                             return_lse=True)
+    ref, ref_lse = oracle_for(q, k, v, causal=True, q_pos_base=qb, kv_pos_base=kb)
+    check_rows(*outs["paired"], ref, ref_lse)
+    short = (q_len // 32 + (q_len % 32 > 0)) // 2 * 32  # rows of the short row blocks
+    assert np.array_equal(outs["paired"][0][:, :short], outs["shared"][0][:, :short])
+    assert np.array_equal(outs["paired"][1][:, :short], outs["shared"][1][:, :short])
+
+
+def test_prefill_2048_causal_one_round_pairs_by_default():
+    """The layer's 2048-token causal attention (32q/8kv, D 128: 256 work-groups, one per CU) takes the
+    paired kernel under AUTO; against the oracle, with fused append of the prompt's rows."""
+    rng = np.random.default_rng(4100)
+    P = 2048
+    q = bf16_normal(rng, (32, P, 128))
+    k = bf16_normal(rng, (8, P, 128))
+    v = bf16_normal(rng, (8, P, 128))
+    with AttentionAccelerator(max_seq_len=P, max_q_len=P) as acc:
+        out, lse = acc.prefill_chunk(q, q_pos_base=0, kv_len=P, causal=True, k_rows=k, v_rows=v, return_lse=True)
+        kr, vr = acc.read_kv(0, 0, P)
+    assert np.array_equal(kr, k) and np.array_equal(vr, v)
+    ref, ref_lse = oracle_for(q, k, v, causal=True)
     check_rows(out, lse, ref, ref_lse)
 
 
