@@ -215,8 +215,9 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
     constexpr int LPB = 2 * DMA;                 // per block (K and V)
     static_assert(DMA >= 1 && DMA * kWaves * 64 == TILE, "tile shape");
 
-    __shared__ __attribute__((aligned(16))) u32x4 lds_k[kStages][TILE];
-    __shared__ __attribute__((aligned(16))) u32x4 lds_v[kStages][TILE];
+    constexpr int NST = PAIR ? 4 : kStages;  // ring stages (PAIR: two blocks computed, two in flight)
+    __shared__ __attribute__((aligned(16))) u32x4 lds_k[NST][TILE];
+    __shared__ __attribute__((aligned(16))) u32x4 lds_v[NST][TILE];
     // PAIR: row block L's Q^T operand handed from wave g to wave g + 4, then that wave's bf16 output
     // rows of row block S ([32 rows][D], 16-byte chunks XOR-swizzled by the row).
     __shared__ __attribute__((aligned(16))) u32x4 lds_q[PAIR ? 4 : 1][PAIR ? KSTEPS : 1][64];
@@ -237,10 +238,10 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
     // dispatcher starts first (longest first), so a grid larger than the GPU balances.
     // PAIR (a causal grid of one dispatch round): work-group p owns row blocks L = n_rb - 1 - p and
     // S = p, heads 0-3 each.  Waves 0-3 work on L from the first key; waves 4-7 work on S while a block
-    // holds keys of S, then on L: from that block on (split_blk) every block is cut in two halves of
-    // 32 keys, the first for waves 0-3 and the second for waves 4-7, whose partials of L merge in
-    // LDS at the end.  Every work-group then carries about (keys(L) + keys(S)) / 2 key blocks per
-    // wave, instead of keys(L) for the work-groups of the last row blocks.
+    // holds keys of S, then on L: from there on two blocks are in LDS at a time, the even one for
+    // waves 0-3 and the odd one for waves 4-7, whose partials of L merge in LDS at the end.  A
+    // work-group then carries about (keys(L) + keys(S)) / 2 keys per wave, instead of keys(L) for
+    // the work-groups of the last row blocks.
     const int wg_x = (a.causal && !PAIR) ? (int)(gridDim.x - 1 - wx) : wx;
     const int task = PAIR ? (n_rb - 1 - wx) * G + (wave & 3) : wg_x * kWaves + wave;
     const bool active = task < n_tasks;
@@ -439,11 +440,11 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
     }
     constexpr uint32_t kKt = 32 * NCH * 16;  // bytes between the two 32-key tiles of a block
 
-    // The block's math for NT 32-key tiles at key jb (NT = 2: the whole block; NT = 1: the half
-    // a PAIR wave takes, its tile offset already in kaddr / vaddr), ring stage ST.
-    auto compute = [&](int jb, auto st_c, auto nt_c) __attribute__((always_inline)) {
+    // The math of the 64-key block at key jb in ring stage ST (PAIR waves 4-7 past S: the stage
+    // after ST, through their read addresses).
+    auto compute = [&](int jb, auto st_c) __attribute__((always_inline)) {
         constexpr int ST = decltype(st_c)::value;
-        constexpr int NT = decltype(nt_c)::value;
+        constexpr int NT = 2;  // 32-key tiles per block
         constexpr int kStageOff = ST * TILE * 16;  // bytes from stage 0 to stage ST
 
         // ---- S^T = K . Q^T (raw scores) ----
@@ -460,16 +461,16 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
         u32x4 kf[KSTEPS][NT];
         auto read_k = [&](int ks) __attribute__((always_inline)) {
             kf[ks][0] = lds_read128<kStageOff>(kaddr[ks]);
-            if constexpr (NT == 2) kf[ks][1] = lds_read128<kStageOff + kKt>(kaddr[ks]);
+            kf[ks][1] = lds_read128<kStageOff + kKt>(kaddr[ks]);
         };
         read_k(0);
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks) {
             if (ks + 1 < KSTEPS) {
                 read_k(ks + 1);
-                if constexpr (NT == 2) lgkm_wait<2>(kf[ks][0], kf[ks][1]); else lgkm_wait1<1>(kf[ks][0]);
+                lgkm_wait<2>(kf[ks][0], kf[ks][1]);
             } else {
-                if constexpr (NT == 2) lgkm_wait<0>(kf[ks][0], kf[ks][1]); else lgkm_wait1<0>(kf[ks][0]);
+                lgkm_wait<0>(kf[ks][0], kf[ks][1]);
             }
 #pragma unroll
             for (int kt = 0; kt < NT; ++kt) sacc[kt] = mfma32(kf[ks][kt], qb[ks], sacc[kt]);
@@ -592,24 +593,36 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
         m_run = -INFINITY;
         l_lane = 0.f;
     };
-    // PAIR: from block split_blk on (the first block past S's keys), waves 0-3 take the first and
-    // waves 4-7 the second 32 keys of every block: their K and V^T read addresses move by 32 keys.
+    // PAIR: from the first even block at or past S's keys on, blocks go in pairs: waves 4-7 read the
+    // ring stage after the one waves 0-3 read.  (Waves 0-3's LDS Q hand-off precedes a barrier
+    // before any wave reads it.)
     const int split_blk = has_s ? (kv_limit(wx) + kBN - 1) / kBN : 0;
-    auto enter_halves = [&]() __attribute__((always_inline)) {
+    auto enter_pairs = [&]() __attribute__((always_inline)) {
         if (wave >= 4) {
 #pragma unroll
-            for (int ks = 0; ks < KSTEPS; ++ks) kaddr[ks] += kKt;
+            for (int ks = 0; ks < KSTEPS; ++ks) kaddr[ks] += TILE * 16;
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt) vaddr[mt] += 32 * D * 2;
+            for (int mt = 0; mt < MT; ++mt) vaddr[mt] += TILE * 16;
             if (cur_rb != rb) leave_s();
         }
     };
-
-    // Block blk of the segment, in ring stage ST = blk % kStages: the whole block (NT = 2) or, for
-    // PAIR waves past split_blk, the wave's 32-key half (NT = 1).
-    auto block = [&](int blk, auto st_c, auto nt_c) __attribute__((always_inline)) {
+    // PAIR, past S's keys: blocks j (waves 0-3) and j + 1 (waves 4-7, whose read addresses point one
+    // stage on), j even and in ring stages ST and ST + 1; blocks j + 2 and j + 3 go into the two stages
+    // the previous pair (or the last two single blocks) freed.
+    auto block_pair = [&](int j, auto st_c) __attribute__((always_inline)) {
         constexpr int ST = decltype(st_c)::value;
-        constexpr int NT = decltype(nt_c)::value;
+        const int j0 = seg_begin + j * kBN;
+        wait_vmcnt<0>();  // blocks j and j + 1 are all that is in flight
+        stage_barrier();
+        if (j + 2 < n_blocks) issue(j0 + 2 * kBN, std::integral_constant<int, (ST + 2) % NST>{});
+        if (j + 3 < n_blocks) issue(j0 + 3 * kBN, std::integral_constant<int, (ST + 3) % NST>{});
+        const int jb = j0 + kBN * (wave >> 2);
+        if (jb < wave_hi) compute(jb, st_c);
+    };
+
+    // Block blk of the segment, in ring stage ST = blk % NST.
+    auto block = [&](int blk, auto st_c) __attribute__((always_inline)) {
+        constexpr int ST = decltype(st_c)::value;
         const int j0 = seg_begin + blk * kBN;
         // This thread's loads of block blk are done once at most the next block's remain
         // (blocks 0 and 1 were retired before the loop).
@@ -617,36 +630,42 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
             if (blk + 1 < n_blocks) wait_vmcnt<LPB>(); else wait_vmcnt<0>();
         }
         stage_barrier();  // every wave's block blk landed; block blk-1's stage is free
-        if (blk + 2 < n_blocks) issue(j0 + 2 * kBN, std::integral_constant<int, (ST + 2) % kStages>{});
-        const int jb = NT == 2 ? j0 : j0 + 32 * (wave >> 2);
-        if (jb >= wave_hi) return;  // this wave's rows see no key of the block (or half)
-        compute(jb, st_c, nt_c);
-    };
-    // Blocks [b0, b1), one copy of the block body per ring stage.
-    auto run = [&](int b0, int b1, auto nt_c) __attribute__((always_inline)) {
-        int blk = b0;
-        if (blk < b1 && blk % kStages == 1) block(blk++, std::integral_constant<int, 1>{}, nt_c);
-        if (blk < b1 && blk % kStages == 2) block(blk++, std::integral_constant<int, 2>{}, nt_c);
-        for (; blk < b1; blk += kStages) {
-            block(blk, std::integral_constant<int, 0>{}, nt_c);
-            if (blk + 1 < b1) block(blk + 1, std::integral_constant<int, 1>{}, nt_c);
-            if (blk + 2 < b1) block(blk + 2, std::integral_constant<int, 2>{}, nt_c);
-        }
+        if (blk + 2 < n_blocks) issue(j0 + 2 * kBN, std::integral_constant<int, (ST + 2) % NST>{});
+        if (j0 >= wave_hi) return;  // this wave's rows see no key of the block
+        compute(j0, st_c);
     };
     static_assert(kStages == 3, "one copy of the block body per ring stage");
     if constexpr (PAIR) {
-        const int split = min(split_blk, n_blocks);
+        // Single blocks up to the first even block past S's keys, then pairs of blocks.
+        const int p0 = min(n_blocks, split_blk + (split_blk & 1));
         stage_barrier();  // the Q hand-off is visible even when no block precedes the move
-        run(0, split, std::integral_constant<int, 2>{});
-        if (split < n_blocks) {
-            enter_halves();
-            run(split, n_blocks, std::integral_constant<int, 1>{});
+        int blk = 0;
+        for (; blk + NST <= p0; blk += NST) {
+            block(blk, std::integral_constant<int, 0>{});
+            block(blk + 1, std::integral_constant<int, 1>{});
+            block(blk + 2, std::integral_constant<int, 2>{});
+            block(blk + 3, std::integral_constant<int, 3>{});
+        }
+        if (blk < p0) block(blk++, std::integral_constant<int, 0>{});
+        if (blk < p0) block(blk++, std::integral_constant<int, 1>{});
+        if (blk < p0) block(blk++, std::integral_constant<int, 2>{});
+        if (p0 < n_blocks) {
+            enter_pairs();
+            int j = p0;
+            if (j % NST == 2) {
+                block_pair(j, std::integral_constant<int, 2>{});
+                j += 2;
+            }
+            for (; j < n_blocks; j += NST) {
+                block_pair(j, std::integral_constant<int, 0>{});
+                if (j + 2 < n_blocks) block_pair(j + 2, std::integral_constant<int, 2>{});
+            }
         }
     } else {
         for (int blk = 0; blk < n_blocks; blk += kStages) {
-            block(blk, std::integral_constant<int, 0>{}, std::integral_constant<int, 2>{});
-            if (blk + 1 < n_blocks) block(blk + 1, std::integral_constant<int, 1>{}, std::integral_constant<int, 2>{});
-            if (blk + 2 < n_blocks) block(blk + 2, std::integral_constant<int, 2>{}, std::integral_constant<int, 2>{});
+            block(blk, std::integral_constant<int, 0>{});
+            if (blk + 1 < n_blocks) block(blk + 1, std::integral_constant<int, 1>{});
+            if (blk + 2 < n_blocks) block(blk + 2, std::integral_constant<int, 2>{});
         }
     }
 
