@@ -84,10 +84,10 @@ extern "C" {
  * PAIRED: SHARED whose work-groups each own a long and a short causal row block (last and first),
  * the short one's waves moving to the long one's keys once theirs end, so the work-groups of a causal
  * launch carry equal work (causal launches of group 4 in one KV segment; others as SHARED).
- * AUTO (default): ROWS when the SHARED grid without segments has fewer work-groups than the GPU has
- * CUs and no segment target is set; else PAIRED where it applies and the grid is at most one
- * work-group per CU (a single dispatch round, which longest-first dispatch cannot balance); else
- * SHARED. */
+ * AUTO (default, no segment target set): PAIRED (one segment) for a causal prompt whose rows see no
+ * keys before its own and whose SHARED grid holds half to one work-group per CU (a single dispatch
+ * round, which longest-first dispatch cannot balance); else ROWS when the SHARED grid without
+ * segments has fewer work-groups than the GPU has CUs; else SHARED. */
 #define GQA_PREFILL_KERNEL_AUTO   0
 #define GQA_PREFILL_KERNEL_SHARED 1
 #define GQA_PREFILL_KERNEL_ROWS   2

@@ -331,14 +331,25 @@ int run_prefill(gqa_ctx* c, int32_t b, const void* q, int32_t q_len, int32_t q_p
         return GQA_OK;
     }
     if (!prefill_supported(c->cfg.head_dim, c->group)) return GQA_ERR_UNSUPPORTED;
+    int kv_span = kv_len;
+    if (causal) kv_span = std::min(kv_len, std::max(0, q_pos_base + q_len - kv_pos_base));
+    // Paired causal row blocks (shared kernel, one segment) for a causal prompt without earlier keys
+    // (its rows see at most the prompt's own keys) whose shared grid is between half and one
+    // work-group per CU: one dispatch round, whose row blocks range from one key block to all of
+    // them.  (Measured, one causal launch, 32q/8kv, D 128: 1024 tokens 28.0 us paired vs 30.5 row
+    // blocks, 1536: 37.6 vs 52.6, 2048: 48.8 vs 79.6 (64.4 unpaired); 768 tokens, 96 work-groups:
+    // 23.5 vs 21.4.)  Earlier keys are read by both row blocks of a pair in step, unpaired, so
+    // chunks after a history keep the row-block kernel.
+    const int shared_wgs = prefill_shared_wgs(q_len, c->group, c->cfg.n_kv_heads);
+    const bool pairable = causal && c->group == 4 && q_len > kPrefillRows;
+    const bool pair_auto = c->prefill_kernel == GQA_PREFILL_KERNEL_AUTO && c->prefill_wgs_opt == 0 && pairable &&
+                           kv_span <= q_len && 2 * shared_wgs >= c->n_cu && shared_wgs <= c->n_cu;
     // Launches whose shared-tile grid would not fill the GPU without KV segments take the row-block
     // kernel (no segments, no merge launch), unless a segment target is set.
     const bool rows = c->prefill_kernel == GQA_PREFILL_KERNEL_ROWS ||
                       (c->prefill_kernel == GQA_PREFILL_KERNEL_AUTO && c->prefill_wgs_opt == 0 &&
-                       prefill_shared_wgs(q_len, c->group, c->cfg.n_kv_heads) < c->n_cu);
-    int kv_span = kv_len;
-    if (causal) kv_span = std::min(kv_len, std::max(0, q_pos_base + q_len - kv_pos_base));
-    const int target = c->prefill_wgs_opt > 0 ? c->prefill_wgs_opt : c->n_cu;
+                       shared_wgs < c->n_cu && !pair_auto);
+    const int target = pair_auto ? 1 : c->prefill_wgs_opt > 0 ? c->prefill_wgs_opt : c->n_cu;
     PrefillPlan plan = plan_prefill(q_len, kv_span, c->group, c->cfg.n_kv_heads, target, kMaxPrefillSegs);
     if (prefill_workspace_floats(plan, q_len, c->cfg.n_q_heads, c->cfg.head_dim) > c->pre_ws_floats)
         plan = plan_prefill(q_len, kv_span, c->group, c->cfg.n_kv_heads, 1, 1);  // one segment
@@ -375,10 +386,9 @@ int run_prefill(gqa_ctx* c, int32_t b, const void* q, int32_t q_len, int32_t q_p
     }
     // Paired causal row blocks: the work of a causal grid grows with the row block, and a grid of one
     // dispatch round (at most one work-group per CU) cannot be balanced by longest-first dispatch.
-    const bool can_pair = causal && c->group == 4 && plan.n_segs == 1 && q_len > kPrefillRows;
-    a.pair = can_pair && (c->prefill_kernel == GQA_PREFILL_KERNEL_PAIRED ||
-                          (c->prefill_kernel == GQA_PREFILL_KERNEL_AUTO &&
-                           prefill_shared_wgs(q_len, c->group, c->cfg.n_kv_heads) <= c->n_cu))
+    a.pair = pairable && plan.n_segs == 1 &&
+                     (c->prefill_kernel == GQA_PREFILL_KERNEL_PAIRED || pair_auto ||
+                      (c->prefill_kernel == GQA_PREFILL_KERNEL_AUTO && shared_wgs == c->n_cu))
                  ? 1 : 0;
     HIP_TRY(launch_prefill(c->cfg.head_dim, c->group, a, timed(c, GQA_TIMER_PREFILL, s)));
     if (plan.n_segs > 1) HIP_TRY(launch_prefill_combine(c->cfg.head_dim, a, timed(c, GQA_TIMER_COMBINE, s)));

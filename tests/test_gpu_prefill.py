@@ -179,11 +179,11 @@ def test_prefill_paired_causal(hq, hkv, d, q_len, kv_len, qb, kb):
     assert np.array_equal(outs["paired"][1][:, :short], outs["shared"][1][:, :short])
 
 
-def test_prefill_2048_causal_one_round_pairs_by_default():
-    """The layer's 2048-token causal attention (32q/8kv, D 128: 256 work-groups, one per CU) takes the
-    paired kernel under AUTO; against the oracle, with fused append of the prompt's rows."""
-    rng = np.random.default_rng(4100)
-    P = 2048
+@pytest.mark.parametrize("P", [1024, 1536, 2048])
+def test_prefill_whole_causal_prompt_pairs_by_default(P):
+    """A whole causal prompt of 1024-2048 tokens (32q/8kv, D 128: 128-256 work-groups, one dispatch
+    round) takes the paired kernel under AUTO; against the oracle, with fused append of its rows."""
+    rng = np.random.default_rng(4100 + P)
     q = bf16_normal(rng, (32, P, 128))
     k = bf16_normal(rng, (8, P, 128))
     v = bf16_normal(rng, (8, P, 128))
