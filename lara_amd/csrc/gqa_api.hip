@@ -275,6 +275,7 @@ int run_decode(gqa_ctx* c, const void* q, const int32_t* lens, const void* k_new
     a.max_pages = c->max_pages;
     a.zero_row = c->zero_row;
     a.longest_first = c->cfg.batch > 1;
+    a.cached = decode_cached_loads((int64_t)c->cfg.batch * c->cfg.n_kv_heads, max_len, c->cfg.head_dim) ? 1 : 0;
     a.arrivals = fuse_merge(c->decode_merge, c->cfg.batch * c->cfg.n_kv_heads, max_splits, c->n_cu) ? c->arrivals
                                                                                                       : nullptr;
     HIP_TRY(launch_decode(c->cfg.head_dim, c->group, a, timed(c, GQA_TIMER_DECODE, s)));
@@ -1364,6 +1365,7 @@ int gqa_decode_append_noalloc(const gqa_config* cfg, void* k_cache, void* v_cach
     a.lse = lse;
     a.zero_row = dev->zero;
     a.longest_first = k.batch > 1;
+    a.cached = decode_cached_loads((int64_t)k.batch * k.n_kv_heads, k.max_seq_len, k.head_dim) ? 1 : 0;
     // The same merge as the context entry point's default (GQA_DECODE_MERGE_AUTO), when the counters
     // cover the units.
     const int units = k.batch * k.n_kv_heads;

@@ -84,7 +84,17 @@ struct DecodeArgs {
     // [B*H_kv] split arrival counters, zero between launches: the last split of a (sequence, kv
     // head) to finish merges the partials itself (no merge launch); nullptr = decode_combine_kernel.
     int32_t* arrivals;
+    // Nonzero: K/V rows are read with plain (L2-allocating) loads instead of nontemporal ones
+    // (decode_cached_loads).
+    int32_t cached;
 };
+// Whether a decode launch over `units` (sequence, kv head) units of at most max_len keys reads
+// its K/V with plain loads: when they fit the L2s of the XCDs (4 MiB each) several times over, a
+// step finds them where the last one left them.
+constexpr int64_t kDecodeCachedBytes = 24ll << 20;
+inline bool decode_cached_loads(int64_t units, int max_len, int head_dim) {
+    return units * (int64_t)max_len * head_dim * 2 * 2 <= kDecodeCachedBytes;
+}
 
 // Chunked prefill / full-transaction launch description (one sequence b).
 struct PrefillArgs {
