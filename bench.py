@@ -3,7 +3,8 @@
 
 Default workload: Llama-3-8B-shape GQA decode, batch 64, 32 query / 8 KV heads,
 head_dim 128, bf16, 8192 attended keys per sequence.  One step appends one K/V row per
-sequence (bit-exact row copy into the HBM cache) and then attends every cached row, in one
+sequence (bit-exact row copy into the HBM cache, at a position that advances every step: a
+ring over the sequence's rows) and then attends every cached row, in one
 split-KV decode launch (plus a log-sum-exp merge launch when a sequence spans several
 splits).  Inputs are synthetic N(0, 1) bf16 generated on the GPU and resident in HBM before
 the timed region; the cache (2 GiB) is far larger than the 256 MB Infinity Cache, so the
@@ -172,6 +173,14 @@ def step_stats(step_us) -> dict:
             "min": float(a.min()), "max": float(a.max()), "n": int(a.size)}
 
 
+def rolling_positions(lens, n_steps: int) -> np.ndarray:
+    """[n_steps][B] int32: the cache row step i appends to in sequence b, (L_b - 1 + i) mod L_b --
+    the last row first, then a ring over the sequence's L_b rows (L_b >= 1)."""
+    lens64 = np.asarray(lens, dtype=np.int64)[None, :]
+    steps = np.arange(n_steps, dtype=np.int64)[:, None]
+    return ((lens64 - 1 + steps) % lens64).astype(np.int32)
+
+
 class DecodeBench:
     """Owns one libgqa context and HBM-resident inputs for a decode workload."""
 
@@ -224,20 +233,38 @@ class DecodeBench:
                                                    ctypes.c_void_p(v.data_ptr()), sptr), "load_kv_device")
             torch.cuda.synchronize(dev)
             del k, v
-        self.q = (torch.randn((w.batch, w.n_q_heads, w.head_dim), generator=g, device=dev) * amp).to(torch.bfloat16)
-        self.k_new = (torch.randn((w.batch, w.n_kv_heads, w.head_dim), generator=g, device=dev) * amp).to(
+        # Rolling append: step i of sequence b writes its new K/V row at cache row
+        # (L_b - 1 + i) mod L_b -- a ring over the sequence's L_b rows, the oldest row giving way --
+        # and attends all L_b rows, so every step attends the configured context while the append
+        # position advances as in a decode loop.  Each step takes its Q and new rows from one of
+        # INPUT_SETS seeded sets in turn; the position table covers POSITION_STEPS steps, then
+        # starts over.
+        S = self.INPUT_SETS
+        self.q_sets = (torch.randn((S, w.batch, w.n_q_heads, w.head_dim), generator=g, device=dev) * amp).to(
             torch.bfloat16)
-        self.v_new = (torch.randn((w.batch, w.n_kv_heads, w.head_dim), generator=g, device=dev) * amp).to(
+        self.k_sets = (torch.randn((S, w.batch, w.n_kv_heads, w.head_dim), generator=g, device=dev) * amp).to(
             torch.bfloat16)
-        self.pos = torch.from_numpy((self.lens - 1).astype(np.int32)).to(dev)
+        self.v_sets = (torch.randn((S, w.batch, w.n_kv_heads, w.head_dim), generator=g, device=dev) * amp).to(
+            torch.bfloat16)
+        self.pos_table = torch.from_numpy(rolling_positions(self.lens, self.POSITION_STEPS)).to(dev)
         self.lens_dev = torch.from_numpy(self.lens.astype(np.int32)).to(dev)
         self.o = torch.empty((w.batch, w.n_q_heads, w.head_dim), dtype=torch.bfloat16, device=dev)
+        self.n_steps = 0
+        # the fixed-pointer form (set 0, first position) for the captured graph
+        self.q, self.k_new, self.v_new, self.pos = self.q_sets[0], self.k_sets[0], self.v_sets[0], self.pos_table[0]
         torch.cuda.synchronize(dev)
+
+    INPUT_SETS = 16
+    POSITION_STEPS = 1024
 
     def step(self) -> None:
         c = ctypes.c_void_p
-        rc = self.lib.gqa_decode_append_device(self.ctx, c(self.q.data_ptr()), c(self.k_new.data_ptr()),
-                                               c(self.v_new.data_ptr()), c(self.pos.data_ptr()),
+        i = self.n_steps
+        self.n_steps += 1
+        s = i % self.INPUT_SETS
+        rc = self.lib.gqa_decode_append_device(self.ctx, c(self.q_sets[s].data_ptr()), c(self.k_sets[s].data_ptr()),
+                                               c(self.v_sets[s].data_ptr()),
+                                               c(self.pos_table[i % self.POSITION_STEPS].data_ptr()),
                                                c(self.lens_dev.data_ptr()), c(self.o.data_ptr()), None, self.sptr)
         if rc:
             self._lib.check(rc, "decode_append")
@@ -629,7 +656,7 @@ def measure_layer(name: str, steps: int, warmup: int, target_wgs: int = 0) -> di
 
 
 ONESHOT_PREFILL = {"prefill-8192": 8192}  # one causal prefill launch of this many tokens (32 q / 8 kv heads, D 128)
-DEFAULT_OTHERS = ("decode-b1-ctx4097", "decode-b64-ragged", "decode-b4-ctx131072", "prefill-chunked-2048",
+DEFAULT_OTHERS = ("decode-b1-d64-ctx256", "decode-b1-ctx4097", "decode-b64-ragged", "decode-b4-ctx131072", "prefill-chunked-2048",
                   "prefill-8192", "layer-2048", "decode-b64-ctx8192" + PAGED_SUFFIX,
                   "prefill-chunked-2048" + PAGED_SUFFIX)
 
@@ -677,6 +704,69 @@ def measure_prefill_oneshot(name: str, steps: int, warmup: int) -> dict:
     log(f"{name}: {out['us_per_prompt']:.1f} us/prompt, kernels {kern_us:.1f} us = "
         f"{out['kernel_tflops'] or 0:.0f} TFLOP/s")
     return out
+
+
+CONFIG_LABEL = {"decode-b1-d64-ctx256": "C1", "decode-b1-ctx4097": "C2", "decode-b64-ragged": "C3",
+                "decode-b4-ctx131072": "C4", "prefill-chunked-2048": "C5", "decode-b64-ctx8192": "NS",
+                "prefill-8192": "p8k", "layer-2048": "layer"}
+
+
+def _fmt_us(us) -> str:
+    if us is None:
+        return "-"
+    return f"{us / 1e3:.1f}ms" if us >= 1e4 else f"{us:.1f}us"
+
+
+def _cpu_text(cpu) -> str:
+    """'cpu1 <time> <rate> cpuN <time> <rate>' of a cpu_baseline entry (decode: per step; prefill: per prompt)."""
+    if not cpu:
+        return "cpu -"
+    parts = []
+    for c in (cpu, cpu.get("all_cores")):
+        if not c:
+            continue
+        t = c.get("us_per_step", c.get("us_per_prompt"))
+        rate = f"{c['value']:.1f}GB/s" if c["unit"] == "GB/s" else f"{c['value']:.2f}TF/s"
+        parts.append(f"cpu{c['cores']} {_fmt_us(t)} {rate}")
+    return " ".join(parts)
+
+
+def summary_lines(main_name: str, main_r: dict, cpu, others: dict) -> list:
+    """One short line per workload (GPU time per step, kernel time and rate, CPU baseline): the last
+    lines the bench prints, so that a short tail of its output still holds every configuration."""
+    from lara_amd.benchmark import BF16_DENSE_TFLOPS, HBM_PEAK_GBPS
+
+    def label(name):
+        base = name.removesuffix(PAGED_SUFFIX)
+        tag = CONFIG_LABEL.get(base, "")
+        return (tag + "-paged" if name != base and tag else tag) + " " + name
+
+    def decode_line(name, r, c):
+        gbps = r.get("kernels_gbps") or 0.0
+        cache = " (in cache: latency-bound)" if r.get("cache_resident") else ""
+        merge = f"+merge {r['combine_us']:.1f}" if r.get("merges_per_step") else ""
+        return (f"{label(name)} {r['us_per_step']:.1f}us/step med {r['step_us']['median']:.1f} "
+                f"p95 {r['step_us']['p95']:.1f} | kern {r['decode_us']:.1f}{merge}us {gbps / 1e3:.2f}TB/s "
+                f"{gbps / HBM_PEAK_GBPS:.1%}{cache} | {_cpu_text(c)}")
+
+    lines = [decode_line(main_name, main_r, cpu)]
+    for name, r in others.items():
+        if "us_per_step" in r:
+            lines.append(decode_line(name, r, r.get("cpu_baseline")))
+        elif "prefill_kernel_us_per_prompt" in r:
+            tf = r.get("kernel_tflops") or 0.0
+            lines.append(f"{label(name)} {r['us_per_prompt']:.1f}us/prompt | kern {r['prefill_kernel_us_per_prompt']:.1f}"
+                         f"us {tf:.0f}TF/s {tf / BF16_DENSE_TFLOPS:.1%} | {_cpu_text(r.get('cpu_baseline'))}")
+        elif "kernel_us" in r:
+            tf = r.get("kernel_tflops") or 0.0
+            lines.append(f"{label(name)} {r['us_per_prompt']:.1f}us/prompt | kern {r['kernel_us']:.1f}us {tf:.0f}TF/s "
+                         f"{tf / BF16_DENSE_TFLOPS:.1%}")
+        elif "us_per_layer" in r:
+            tf = r.get("attention_tflops") or 0.0
+            lines.append(f"{label(name)} {r['us_per_layer']:.1f}us/layer | attn {r['attention_us']:.1f}us {tf:.0f}TF/s "
+                         f"{tf / BF16_DENSE_TFLOPS:.1%} norm {r['rms_norm_us']:.1f} gemm {r['qkv_projection_us']:.1f} "
+                         f"rope {r['rope_scatter_us']:.1f}")
+    return lines
 
 
 def read_traffic():
@@ -1263,7 +1353,9 @@ def main() -> int:
             "head_dim": w.head_dim,
             "attended_keys": int(w.lengths().max()),
             "step": "append 1 K/V row per sequence fused into the split-KV decode launch (a second LSE-merge "
-                    "launch only when a sequence spans several splits; none at this shape)",
+                    "launch only when a sequence spans several splits; none at this shape); rolling append: step i "
+                    "writes row (L - 1 + i) mod L of each sequence (a ring over its L rows) and attends all L rows; "
+                    f"Q and the new rows cycle over {DecodeBench.INPUT_SETS} seeded sets",
             "accumulate": "fp32",
             "working_set_bytes": main_r["working_set_bytes"],
             "residency": main_r["residency"],
@@ -1276,7 +1368,10 @@ def main() -> int:
         "environment": collect_environment(),
         "other_workloads": others,
     }
+    line["summary"] = summary_lines(args.workload, main_r, cpu, others)
     print(json.dumps(line), flush=True)
+    for text in line["summary"]:
+        print(f"[summary] {text}", file=sys.stderr, flush=True)
     return 0
 
 

@@ -83,11 +83,14 @@ extern "C" {
  * (query head, 32-row block) whose waves split the keys and merge in LDS (one launch, no segments).
  * PAIRED: SHARED whose work-groups each own a long and a short causal row block (last and first),
  * the short one's waves moving to the long one's keys once theirs end, so the work-groups of a causal
- * launch carry equal work (causal launches of group 4 in one KV segment; others as SHARED).
+ * launch carry equal work (causal launches of group 4 with more than one row block, always planned in
+ * one KV segment; others as SHARED).
  * AUTO (default, no segment target set): PAIRED (one segment) for a causal prompt whose rows see no
  * keys before its own and whose SHARED grid holds half to one work-group per CU (a single dispatch
  * round, which longest-first dispatch cannot balance); else ROWS when the SHARED grid without
- * segments has fewer work-groups than the GPU has CUs; else SHARED. */
+ * segments has fewer work-groups than the GPU has CUs; else SHARED -- paired when that grid is exactly
+ * one work-group per CU (for instance a causal 2048-row chunk after earlier keys at 32q/8kv on 256
+ * CUs), unpaired when larger.  gqa_last_prefill_plan reports the decomposition a launch took. */
 #define GQA_PREFILL_KERNEL_AUTO   0
 #define GQA_PREFILL_KERNEL_SHARED 1
 #define GQA_PREFILL_KERNEL_ROWS   2
@@ -105,7 +108,12 @@ extern "C" {
 #define GQA_DECODE_MERGE_FUSED  2
 
 /* Numerics of the attention kernels (GQA_OPT_NUMERICS).
- * EXACT: fp32 accumulation, exact exp, exact divide -- within 2 bf16 ulp of exact attention.
+ * EXACT: fp32 scores, softmax, sums and accumulation, exact divide; the P.V product takes each
+ *        softmax weight rounded to bf16 (RNE; the board truncates it, attn_top.sv:653-658) while
+ *        l sums the fp32 weights.  Each output element is within 2 bf16 ulp of its row's largest
+ *        |output| of exact attention plus 2^-8 of exact attention over |V| at that element
+ *        (sum_k p_k |v_k[d]| / l); the second term matters only where V rows cancel -- otherwise
+ *        it lies within the first.
  * KV260: the deployed KV260 datapath bit for bit -- sequential fp32 sums of exact bf16 products,
  *        the 1024-entry interpolated exp table (softmax_engine.sv:570-706), P truncated to bf16
  *        for PV (attn_top.sv:653-658), reciprocal-table normalisation (output_buffer.sv:192-286),
@@ -382,6 +390,12 @@ int gqa_kernel_launch_counts(gqa_ctx* ctx, int32_t* out_counts, int32_t n);
  * *n_out = the number recorded. */
 int gqa_kernel_durations(gqa_ctx* ctx, int32_t slot, float* out_us, int32_t n, int32_t* n_out);
 int gqa_synchronize(gqa_ctx* ctx);
+/* gqa_last_prefill_plan: the decomposition (GQA_PREFILL_KERNEL_ROWS, _SHARED or _PAIRED) and the KV
+ * segment count of the context's last prefill launch (gqa_prefill*, a transaction, run_layer's
+ * attention); 0, 0 before any and after a KV260-numerics launch.  A diagnostic beside read_perf
+ * (attn_driver.py:466-467): the board's tiling is fixed (attn_core.sv:107-154), the engine's is
+ * chosen per launch, and tests use this to check which decomposition a launch took. */
+int gqa_last_prefill_plan(gqa_ctx* ctx, int32_t* kernel, int32_t* n_segs);
 
 #ifdef __cplusplus
 }

@@ -146,6 +146,7 @@ _SIGNATURES = {
     "gqa_kernel_launch_counts": [_CTX, _P32, c_int32],
     "gqa_kernel_durations": [_CTX, c_int32, _PF, c_int32, _P32],
     "gqa_synchronize": [_CTX],
+    "gqa_last_prefill_plan": [_CTX, _P32, _P32],
 }
 
 EXPORTED = tuple(_SIGNATURES) + ("gqa_status_string",)

@@ -587,6 +587,15 @@ class AttentionAccelerator:
         self._call("gqa_paged_layers", ctypes.byref(n), ctypes.byref(cur))
         return int(cur.value)
 
+    def last_prefill_plan(self) -> tuple[str, int]:
+        """Decomposition ("rows", "shared", "paired"; "" before any prefill and after a kv260-numerics
+        launch) and KV segment count of the engine's last prefill launch."""
+        kernel, segs = ctypes.c_int32(0), ctypes.c_int32(0)
+        self._call("gqa_last_prefill_plan", ctypes.byref(kernel), ctypes.byref(segs))
+        names = {_lib.GQA_PREFILL_KERNEL_ROWS: "rows", _lib.GQA_PREFILL_KERNEL_SHARED: "shared",
+                 _lib.GQA_PREFILL_KERNEL_PAIRED: "paired"}
+        return names.get(int(kernel.value), ""), int(segs.value)
+
     def page_info(self) -> dict[str, int]:
         """Page size, pool size, free pages and block-table width of a paged engine."""
         vals = [ctypes.c_int32(0) for _ in range(4)]

@@ -118,6 +118,8 @@ struct gqa_ctx {
     int32_t* table_dev = nullptr;
     PageTable pages;
     int capturing = 0;  // a HIP graph capture is recording this context's launches (no timer events)
+    int last_prefill_kernel = 0;  // decomposition and KV segments of the last prefill launch (gqa_last_prefill_plan)
+    int last_prefill_segs = 0;
 };
 
 // A captured decode step (gqa_graph_capture_decode_append) and the context it reads.
@@ -329,6 +331,8 @@ int run_prefill(gqa_ctx* c, int32_t b, const void* q, int32_t q_len, int32_t q_p
         r.out = (uint16_t*)o;
         r.lse = lse;
         HIP_TRY(launch_rtl_transaction(c->cfg.head_dim, r, timed(c, GQA_TIMER_PREFILL, s)));
+        c->last_prefill_kernel = 0;
+        c->last_prefill_segs = 0;
         return GQA_OK;
     }
     if (!prefill_supported(c->cfg.head_dim, c->group)) return GQA_ERR_UNSUPPORTED;
@@ -350,7 +354,10 @@ int run_prefill(gqa_ctx* c, int32_t b, const void* q, int32_t q_len, int32_t q_p
     const bool rows = c->prefill_kernel == GQA_PREFILL_KERNEL_ROWS ||
                       (c->prefill_kernel == GQA_PREFILL_KERNEL_AUTO && c->prefill_wgs_opt == 0 &&
                        shared_wgs < c->n_cu && !pair_auto);
-    const int target = pair_auto ? 1 : c->prefill_wgs_opt > 0 ? c->prefill_wgs_opt : c->n_cu;
+    // A forced PAIRED decomposition plans one KV segment (pairs exist only in one-segment launches);
+    // launches it cannot pair (not causal, group != 4, one row block) plan as SHARED.
+    const bool pair_forced = c->prefill_kernel == GQA_PREFILL_KERNEL_PAIRED && pairable;
+    const int target = (pair_auto || pair_forced) ? 1 : c->prefill_wgs_opt > 0 ? c->prefill_wgs_opt : c->n_cu;
     PrefillPlan plan = plan_prefill(q_len, kv_span, c->group, c->cfg.n_kv_heads, target, kMaxPrefillSegs);
     if (prefill_workspace_floats(plan, q_len, c->cfg.n_q_heads, c->cfg.head_dim) > c->pre_ws_floats)
         plan = plan_prefill(q_len, kv_span, c->group, c->cfg.n_kv_heads, 1, 1);  // one segment
@@ -383,6 +390,8 @@ int run_prefill(gqa_ctx* c, int32_t b, const void* q, int32_t q_len, int32_t q_p
     a.part_ml = c->pre_ws + (size_t)plan.n_segs * c->cfg.n_q_heads * q_len * (c->cfg.head_dim / 2);
     if (rows) {
         HIP_TRY(launch_prefill_rows(c->cfg.head_dim, a, timed(c, GQA_TIMER_PREFILL, s)));
+        c->last_prefill_kernel = GQA_PREFILL_KERNEL_ROWS;
+        c->last_prefill_segs = 1;
         return GQA_OK;
     }
     // Paired causal row blocks: the work of a causal grid grows with the row block, and a grid of one
@@ -393,6 +402,8 @@ int run_prefill(gqa_ctx* c, int32_t b, const void* q, int32_t q_len, int32_t q_p
                  ? 1 : 0;
     HIP_TRY(launch_prefill(c->cfg.head_dim, c->group, a, timed(c, GQA_TIMER_PREFILL, s)));
     if (plan.n_segs > 1) HIP_TRY(launch_prefill_combine(c->cfg.head_dim, a, timed(c, GQA_TIMER_COMBINE, s)));
+    c->last_prefill_kernel = a.pair ? GQA_PREFILL_KERNEL_PAIRED : GQA_PREFILL_KERNEL_SHARED;
+    c->last_prefill_segs = plan.n_segs;
     return GQA_OK;
 }
 
@@ -764,11 +775,11 @@ int create_ctx(const gqa_config* cfg, int32_t page_size, int32_t n_pages, int32_
         for (int i = 0; i < 4 && ok; ++i) ok = hipEventCreate(&c->ev_t[i]) == hipSuccess;
         if (!ok) rc = GQA_ERR_HIP;
     }
-    // Zero the caches once so rows beyond every sequence's length hold finite words.
+    // Zero the caches (every layer's pool) once so rows beyond every sequence's length hold finite words.
     if (rc == GQA_OK && (hipMemsetAsync(c->zero_row, 0, D * 2, c->stream) != hipSuccess ||
                          hipMemsetAsync(c->arrivals, 0, units * sizeof(int32_t), c->stream) != hipSuccess ||
-                         hipMemsetAsync(c->k_cache, 0, kv_words(c) * 2, c->stream) != hipSuccess ||
-                         hipMemsetAsync(c->v_cache, 0, kv_words(c) * 2, c->stream) != hipSuccess ||
+                         hipMemsetAsync(c->k_pool, 0, kv_words(c) * 2 * (size_t)n_layers, c->stream) != hipSuccess ||
+                         hipMemsetAsync(c->v_pool, 0, kv_words(c) * 2 * (size_t)n_layers, c->stream) != hipSuccess ||
                          (c->paged && hipMemsetAsync(c->table_dev, 0xFF, (size_t)k.batch * c->max_pages * 4,
                                                      c->stream) != hipSuccess) ||  // every entry -1: unmapped
                          hipStreamSynchronize(c->stream) != hipSuccess))
@@ -1771,6 +1782,13 @@ int gqa_kernel_durations(gqa_ctx* c, int32_t slot, float* out_us, int32_t n, int
 int gqa_kernel_launch_counts(gqa_ctx* c, int32_t* out_counts, int32_t n) {
     if (!c || !out_counts) return GQA_ERR_NULL;
     for (int i = 0; i < n; ++i) out_counts[i] = (i < GQA_TIMER_COUNT && c->profile) ? c->ev_count[i] : 0;
+    return GQA_OK;
+}
+
+int gqa_last_prefill_plan(gqa_ctx* c, int32_t* kernel, int32_t* n_segs) {
+    if (!c || !kernel || !n_segs) return GQA_ERR_NULL;
+    *kernel = c->last_prefill_kernel;
+    *n_segs = c->last_prefill_segs;
     return GQA_OK;
 }
 

@@ -44,6 +44,7 @@ __all__ = [
     "cpu_attention_numpy_fp32",
     "decode_fp32_baseline",
     "row_ulp_error",
+    "weight_rounding_error",
 ]
 
 
@@ -218,6 +219,24 @@ def decode_fp32_baseline(q_words, k_words, v_words, *, scale=None):
 # ---------------------------------------------------------------------------------------
 # parity metric
 # ---------------------------------------------------------------------------------------
+
+def weight_rounding_error(out_words, ref, ref_abs_v) -> np.ndarray:
+    """Per output element: |out - ref| / (2 bf16 ulp(max |ref| of the row) + 2^-8 * ref_abs_v).
+
+    ``ref_abs_v`` is attention over |V| (sum_k p_k |v_k[d]| / l, e.g. ``attention(q, k, abs(v))``):
+    a kernel that rounds each softmax weight to bf16 (relative error <= 2^-8) for the P.V product
+    -- as the board does, by truncation, ``attn_top.sv:653-658`` -- is off by at most 2^-8 of it.
+    Where the rows of V do not cancel that term is within the output's own magnitude, and the bound
+    is the 2-ulp parity measure of ``row_ulp_error``; where they cancel it is what limits any bf16-P
+    product.  An element passes when the returned value is <= 1.
+    """
+    out = bf16_u16_to_fp32(out_words).astype(np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    mag = np.max(np.abs(ref), axis=-1, keepdims=True)
+    allowed = 2.0 * np.where(mag > 0, bf16_ulp(mag), 0.0) + 2.0 ** -8 * np.asarray(ref_abs_v, dtype=np.float64)
+    err = np.abs(out - ref)
+    return np.where(allowed > 0, err / np.where(allowed > 0, allowed, 1.0), np.where(err == 0, 0.0, np.inf))
+
 
 def row_ulp_error(out_words, ref) -> np.ndarray:
     """Per output row (last axis = D): max |out - ref| in units of bf16 ulp(max |ref| of the row).

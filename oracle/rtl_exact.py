@@ -23,8 +23,10 @@ PLANT_FLAT_ACCUMULATE = 4   # O accumulated key by key instead of one delta per 
 PLANT_TILE_RESCALE = 8      # running max per 64-key tile instead of per 16-key sub-block
 PLANT_EXACT_DIVIDE = 16     # O / l (IEEE) instead of O x R(l)
 PLANT_QK_REVERSED = 32      # Q.K summed from the last dimension down
+PLANT_FRAC_RNE = 64         # the exp table's interpolation fraction rounded to nearest instead of truncated
 PLANTS = {"p_rne": PLANT_P_RNE, "sum_reversed": PLANT_SUM_REVERSED, "flat_accumulate": PLANT_FLAT_ACCUMULATE,
-          "tile_rescale": PLANT_TILE_RESCALE, "exact_divide": PLANT_EXACT_DIVIDE, "qk_reversed": PLANT_QK_REVERSED}
+          "tile_rescale": PLANT_TILE_RESCALE, "exact_divide": PLANT_EXACT_DIVIDE, "qk_reversed": PLANT_QK_REVERSED,
+          "frac_rne": PLANT_FRAC_RNE}
 
 _U32 = ctypes.POINTER(ctypes.c_uint32)
 _U16 = ctypes.POINTER(ctypes.c_uint16)

@@ -19,3 +19,14 @@ def kv_with_outliers(rng, shape, amplitude=1.0, fraction=0.0, factor=1.0):
         idx = rng.choice(rows.shape[0], size=n, replace=False)
         rows[idx] *= np.float32(factor)
     return fp32_to_bf16_u16(x)
+
+
+def cancelling_kv(rng, hkv, n, d):
+    """K/V words [hkv, n, d] in row pairs: row 2j+1 repeats row 2j's K but for dim 0 and negates its
+    V, so the pair's softmax weights are close and their V contributions almost cancel (n even)."""
+    k = fp32_to_bf16_u16(rng.standard_normal((hkv, n, d), dtype=np.float32))
+    v = fp32_to_bf16_u16(rng.standard_normal((hkv, n, d), dtype=np.float32))
+    k[:, 1::2] = k[:, 0::2]
+    k[:, 1::2, 0] = fp32_to_bf16_u16(rng.standard_normal((hkv, n // 2), dtype=np.float32) * np.float32(0.05))
+    v[:, 1::2] = v[:, 0::2] ^ np.uint16(0x8000)
+    return k, v

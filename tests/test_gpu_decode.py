@@ -288,3 +288,31 @@ def test_decode_fused_merge_matches_merge_launch(hq, hkv, d):
             assert np.array_equal(out_f, out_l), f"step {step}"
             assert np.array_equal(lse_f.view(np.uint32), lse_l.view(np.uint32))
             check_decode(out_f, lse_f, q, kc, vc, lens, None)
+
+
+def test_decode_cancelling_v_rows_within_the_weight_rounding_bound():
+    """V rows in cancelling pairs with near-equal weights: the products take P rounded to bf16 (as the
+    board takes it truncated), so each element is within 2 bf16 ulp of its row's largest |output|
+    plus 2^-8 of attention over |V| at that element (oracle.weight_rounding_error), the stated bound
+    of the EXACT mode; the softmax sum stays within rtol 1e-2."""
+    from tests._gen import cancelling_kv
+
+    rng = np.random.default_rng(160)
+    B, hq, hkv, d = 2, 32, 8, 128
+    lens = np.array([64, 300], np.int32)
+    with make_engine(B, hq, hkv, d, 300) as eng:
+        kc = np.zeros((B, hkv, 300, d), np.uint16)
+        vc = np.zeros((B, hkv, 300, d), np.uint16)
+        for b in range(B):
+            kc[b, :, :lens[b]], vc[b, :, :lens[b]] = cancelling_kv(rng, hkv, int(lens[b]), d)
+            eng.load_kv(kc[b, :, :lens[b]], vc[b, :, :lens[b]], b=b)
+        q = bf16_normal(rng, (B, hq, d))
+        out, lse = eng.decode_step(q, lens, return_lse=True)
+    ref, ref_lse = orc.decode(q, kc, vc, lens)
+    ref_abs, _ = orc.decode(q, kc, vc & np.uint16(0x7FFF), lens)
+    err = orc.weight_rounding_error(out, ref, ref_abs)
+    print(f"[cancel] decode: bound use {err.max():.3f}, 2-ulp measure {orc.row_ulp_error(out, ref).max():.2f}",
+          flush=True)
+    assert float(err.max()) <= 1.0
+    rel = np.abs(np.expm1(lse.astype(np.float64) - ref_lse))
+    assert float(rel.max()) <= L_RTOL

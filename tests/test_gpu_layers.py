@@ -177,3 +177,21 @@ def test_layer_option_and_creation_limits():
     with AttentionAccelerator(max_seq_len=256) as contiguous:
         assert lib.gqa_paged_layers(contiguous._ctx, None, None) == _lib.GQA_ERR_UNSUPPORTED
         assert lib.gqa_set_option(contiguous._ctx, _lib.GQA_OPT_LAYER, 0) == _lib.GQA_OK
+
+
+def test_reserved_rows_never_written_read_as_zero_on_every_layer():
+    """Creation clears every layer's pool, not only layer 0's: a reserved row that no call has
+    written reads as zero words on each layer (first dirtying device memory that the engine's
+    allocation may reuse)."""
+    import torch
+
+    junk = torch.full((64 << 20,), -1, dtype=torch.int32, device="cuda")  # 256 MiB of 0xFFFFFFFF words
+    torch.cuda.synchronize()
+    del junk
+    torch.cuda.empty_cache()
+    with layered() as acc:
+        acc.reserve(0, 2 * P)
+        for layer in range(N_LAYERS):
+            acc.select_layer(layer)
+            k, v = acc.read_kv(0, 0, 2 * P)
+            assert not k.any() and not v.any(), layer

@@ -137,6 +137,10 @@ def test_chunked_prefill_into_pages(kernel):
             o_c, l_c = cont.prefill_chunk(q, **kw)
             o_p, l_p = paged.prefill_chunk(q, **kw)
             assert np.array_equal(o_p, o_c) and np.array_equal(l_p, l_c), start
+            if kernel != "auto":  # the forced decomposition ran, paired in one KV segment
+                for acc in (cont, paged):
+                    assert acc.last_prefill_plan()[0] == kernel
+                    assert kernel != "paired" or acc.last_prefill_plan()[1] == 1
         kc, vc = cont.read_kv(2, 0, prompt)
         kp, vp = paged.read_kv(2, 0, prompt)
     assert np.array_equal(kp, kc) and np.array_equal(vp, vc)

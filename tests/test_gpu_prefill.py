@@ -172,6 +172,10 @@ def test_prefill_paired_causal(hq, hkv, d, q_len, kv_len, qb, kb):
             acc.load_kv(k, v)
             outs[kernel] = acc.prefill_chunk(q, q_pos_base=qb, kv_len=kv_len, kv_pos_base=kb, causal=True,
                                              return_lse=True)
+            # a forced decomposition must be the one that ran (one KV segment when paired)
+            assert acc.last_prefill_plan()[0] == kernel
+            if kernel == "paired":
+                assert acc.last_prefill_plan()[1] == 1
     ref, ref_lse = oracle_for(q, k, v, causal=True, q_pos_base=qb, kv_pos_base=kb)
     check_rows(*outs["paired"], ref, ref_lse)
     short = (q_len // 32 + (q_len % 32 > 0)) // 2 * 32  # rows of the short row blocks
@@ -189,10 +193,43 @@ def test_prefill_whole_causal_prompt_pairs_by_default(P):
     v = bf16_normal(rng, (8, P, 128))
     with AttentionAccelerator(max_seq_len=P, max_q_len=P) as acc:
         out, lse = acc.prefill_chunk(q, q_pos_base=0, kv_len=P, causal=True, k_rows=k, v_rows=v, return_lse=True)
+        assert acc.last_prefill_plan() == ("paired", 1)
         kr, vr = acc.read_kv(0, 0, P)
     assert np.array_equal(kr, k) and np.array_equal(vr, v)
     ref, ref_lse = oracle_for(q, k, v, causal=True)
     check_rows(out, lse, ref, ref_lse)
+
+
+@pytest.mark.parametrize("paged", [False, True])
+def test_prefill_chunk_after_history_pairs_when_the_grid_fills_the_gpu(paged):
+    """A causal 2048-row chunk after 192 cached rows (32q/8kv, D 128): its shared grid is one
+    work-group per CU, so AUTO takes the paired kernel in one segment although earlier keys exist;
+    against the oracle, and on a paged cache (scattered pages) word for word equal to the contiguous
+    engine."""
+    rng = np.random.default_rng(4200)
+    H, C = 192, 2048
+    q = bf16_normal(rng, (32, C, 128))
+    k = bf16_normal(rng, (8, H + C, 128))
+    v = bf16_normal(rng, (8, H + C, 128))
+    outs = []
+    for use_pages in ([False, True] if paged else [False]):
+        kw = dict(page_size=64, n_pages=2 * (H + C) // 64 + 2, batch=2) if use_pages else {}
+        with AttentionAccelerator(max_seq_len=H + C, max_q_len=C, **kw) as acc:
+            b = 1 if use_pages else 0
+            if use_pages:  # sequence 1's pages alternate with sequence 0's
+                for n in range(64, H + C + 1, 64):
+                    acc.reserve(0, n)
+                    acc.reserve(1, n)
+            acc.load_kv(k[:, :H], v[:, :H], b=b)
+            print(f"[paired-after-history] paged={use_pages}", flush=True)
+            outs.append(acc.prefill_chunk(q, b=b, q_pos_base=H, kv_len=H + C, causal=True, k_rows=k[:, H:],
+                                          v_rows=v[:, H:], return_lse=True))
+            assert acc.last_prefill_plan() == ("paired", 1)
+    if paged:
+        assert np.array_equal(outs[1][0], outs[0][0]) and np.array_equal(outs[1][1], outs[0][1])
+    else:
+        ref, ref_lse = oracle_for(q, k, v, causal=True, q_pos_base=H)
+        check_rows(*outs[0], ref, ref_lse)
 
 
 def test_prefill_rows_without_keys_are_zero():
@@ -329,3 +366,28 @@ def test_segment_partials_at_extreme_magnitudes(v_scale):
     ref, ref_lse = oracle_for(q, k, v, causal=True, q_pos_base=kv_len - q_len)
     check_rows(out, lse, ref, ref_lse)
     check_rows(outs[1][0], outs[1][1], ref, ref_lse)
+
+
+@pytest.mark.parametrize("kernel", ["rows", "shared"])
+def test_prefill_cancelling_v_rows_within_the_weight_rounding_bound(kernel):
+    """Causal prefill over V rows in cancelling pairs: within 2 ulp of the row's largest |output| plus
+    2^-8 of attention over |V| per element (P rounded to bf16 for the PV product), the stated bound
+    of the EXACT mode; l within rtol 1e-2."""
+    from tests._gen import cancelling_kv
+
+    rng = np.random.default_rng(4300)
+    q_len, kv_len = 64, 256
+    q = bf16_normal(rng, (32, q_len, 128))
+    k, v = cancelling_kv(rng, 8, kv_len, 128)
+    with AttentionAccelerator(max_seq_len=kv_len, max_q_len=q_len) as acc:
+        set_prefill_kernel(acc, kernel)
+        acc.load_kv(k, v)
+        out, lse = acc.prefill_chunk(q, q_pos_base=kv_len - q_len, kv_len=kv_len, causal=True, return_lse=True)
+    ref, ref_lse = oracle_for(q, k, v, causal=True, q_pos_base=kv_len - q_len)
+    ref_abs, _ = oracle_for(q, k, v & np.uint16(0x7FFF), causal=True, q_pos_base=kv_len - q_len)
+    err = orc.weight_rounding_error(out, ref, ref_abs)
+    print(f"[cancel] prefill {kernel}: bound use {err.max():.3f}, 2-ulp measure "
+          f"{orc.row_ulp_error(out, ref).max():.2f}", flush=True)
+    assert float(err.max()) <= 1.0
+    rel = np.abs(np.expm1(lse.astype(np.float64) - ref_lse))
+    assert float(rel.max()) <= L_RTOL

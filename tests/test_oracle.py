@@ -12,6 +12,7 @@ import pytest
 import torch
 
 from oracle import gqa_oracle as orc
+from tests._gen import cancelling_kv
 
 
 def words_to_f32(words):
@@ -90,6 +91,48 @@ def test_row_ulp_error_detects_planted_error():
     bumped[1, 3] += 3  # three bf16 ulps at that element (same binade)
     err = orc.row_ulp_error(bumped, ref)
     assert err[1] > 2.0 and np.all(err[[0, 2, 3]] <= 0.5 + 1e-9)
+
+
+def _bf16_p_attention(q, k, v, scale):
+    """Attention whose P.V product takes each weight rounded to bf16 (RNE) while l sums the exact
+    weights: the product of a bf16-P matrix-core kernel, emulated in float64."""
+    s = q @ k.T * scale
+    p = np.exp(s - s.max(axis=-1, keepdims=True))
+    pb = orc.bf16_u16_to_fp32(orc.bf16_rne(p.astype(np.float32))).astype(np.float64)
+    return (pb @ v) / p.sum(axis=-1, keepdims=True)
+
+
+def test_weight_rounding_error_bounds_a_bf16_p_product():
+    """A bf16-P product stays within 2 ulp + 2^-8 * attention(|V|) on inputs whose V rows cancel,
+    although the 2-ulp measure alone rejects it there; on ordinary inputs both measures pass it; an
+    element off by twice the allowed error is rejected."""
+    rng = np.random.default_rng(3)
+    d, n = 128, 64
+    q = orc.bf16_u16_to_fp32(orc.bf16_rne(rng.standard_normal((8, d)).astype(np.float32))).astype(np.float64)
+    kw, vw = cancelling_kv(rng, 1, n, d)
+    k = orc.bf16_u16_to_fp32(kw[0]).astype(np.float64)
+    v = orc.bf16_u16_to_fp32(vw[0]).astype(np.float64)
+    scale = 1 / math.sqrt(d)
+    ref, _ = orc.attention(q[:, None], k[None], v[None], scale=scale)
+    ref_abs, _ = orc.attention(q[:, None], k[None], np.abs(v)[None], scale=scale)
+    ref, ref_abs = ref[:, 0], ref_abs[:, 0]
+    out = orc.bf16_rne(_bf16_p_attention(q, k, v, scale).astype(np.float32))
+    assert float(orc.weight_rounding_error(out, ref, ref_abs).max()) <= 1.0
+    assert float(orc.row_ulp_error(out, ref).max()) > 2.0  # the cancellation defeats the 2-ulp measure
+    # ordinary inputs: V without cancelling pairs
+    v2 = orc.bf16_u16_to_fp32(orc.bf16_rne(rng.standard_normal((n, d)).astype(np.float32))).astype(np.float64)
+    ref2, _ = orc.attention(q[:, None], k[None], v2[None], scale=scale)
+    abs2, _ = orc.attention(q[:, None], k[None], np.abs(v2)[None], scale=scale)
+    out2 = orc.bf16_rne(_bf16_p_attention(q, k, v2, scale).astype(np.float32))
+    assert float(orc.row_ulp_error(out2, ref2[:, 0]).max()) <= 2.0
+    assert float(orc.weight_rounding_error(out2, ref2[:, 0], abs2[:, 0]).max()) <= 1.0
+    # a planted error of twice the allowed amount at one element
+    mag = np.max(np.abs(ref), axis=-1)
+    allowed = 2 * orc.bf16_ulp(mag[2]) + 2.0 ** -8 * ref_abs[2, 5]
+    planted = out.copy()
+    planted[2, 5] = orc.bf16_rne(np.float32(ref[2, 5] + 2.2 * allowed))
+    err = orc.weight_rounding_error(planted, ref, ref_abs)
+    assert err[2, 5] > 1.0 and float(np.delete(err.ravel(), 2 * d + 5).max()) <= 1.0
 
 
 # ---------------------------------------------------------------------------------------

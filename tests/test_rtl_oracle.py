@@ -217,3 +217,24 @@ def test_board_format_cases_regenerate_from_the_oracle():
             out, _, _ = rtl.attention(d["q_heads"], d["k_heads"], d["v_heads"], causal=bool(d["causal"]),
                                       q_pos_base=int(d["q_pos_base"]), kv_pos_base=int(d["kv_pos_base"]))
             assert np.array_equal(out, d["expected_o"])
+
+
+def test_exp_lookup_fraction_is_truncated_word_for_word():
+    """Inputs whose interpolation fraction r / 2^26 has r >= 2^24 (more than 24 significant bits):
+    the RTL's q26_to_fp32 (softmax_engine.sv:547-566) truncates r's significand, and the exp lookup
+    of the restatement gives the words derived by hand that way, each differing from the word a
+    rounded fraction would give (tests/_kv260_cases.exp_by_hand, float32 scalar steps)."""
+    from tests import _kv260_cases as kc
+
+    words = {  # x: (E with the truncated fraction, E with a rounded one)
+        0xBF0023C6: (0x3F1B2FE9, 0x3F1B2FEA),
+        0xBF0AB2BF: (0x3F14EAED, 0x3F14EAEE),
+        0xBF244AAD: (0x3F06BFC8, 0x3F06BFC9),
+        0xBF3147D6: (0x3F001562, 0x3F001563),
+        0xBFDC6A2F: (0x3E36FFFF, 0x3E370000),  # the upper halves differ too: the PV operand moves
+    }
+    for x, (trunc, rounded) in words.items():
+        assert kc.bits(kc.exp_by_hand(kc.from_bits(x))) == trunc, hex(x)
+        assert kc.bits(kc.exp_by_hand(kc.from_bits(x), round_fraction=True)) == rounded, hex(x)
+    got = rtl.exp_lookup(np.array(list(words), np.uint32))
+    assert [int(g) for g in got] == [t for t, _ in words.values()]
