@@ -250,6 +250,13 @@ class DecodeBench:
         self.lens_dev = torch.from_numpy(self.lens.astype(np.int32)).to(dev)
         self.o = torch.empty((w.batch, w.n_q_heads, w.head_dim), dtype=torch.bfloat16, device=dev)
         self.n_steps = 0
+        # device addresses of every set and position row, so a step costs the host no tensor indexing
+        c = ctypes.c_void_p
+        self.set_ptrs = [(c(self.q_sets[s].data_ptr()), c(self.k_sets[s].data_ptr()), c(self.v_sets[s].data_ptr()))
+                         for s in range(S)]
+        self.pos_ptrs = [c(self.pos_table[i].data_ptr()) for i in range(self.POSITION_STEPS)]
+        self.lens_ptr = c(self.lens_dev.data_ptr())
+        self.o_ptr = c(self.o.data_ptr())
         # the fixed-pointer form (set 0, first position) for the captured graph
         self.q, self.k_new, self.v_new, self.pos = self.q_sets[0], self.k_sets[0], self.v_sets[0], self.pos_table[0]
         torch.cuda.synchronize(dev)
@@ -258,14 +265,11 @@ class DecodeBench:
     POSITION_STEPS = 1024
 
     def step(self) -> None:
-        c = ctypes.c_void_p
         i = self.n_steps
         self.n_steps += 1
-        s = i % self.INPUT_SETS
-        rc = self.lib.gqa_decode_append_device(self.ctx, c(self.q_sets[s].data_ptr()), c(self.k_sets[s].data_ptr()),
-                                               c(self.v_sets[s].data_ptr()),
-                                               c(self.pos_table[i % self.POSITION_STEPS].data_ptr()),
-                                               c(self.lens_dev.data_ptr()), c(self.o.data_ptr()), None, self.sptr)
+        q, k, v = self.set_ptrs[i % self.INPUT_SETS]
+        rc = self.lib.gqa_decode_append_device(self.ctx, q, k, v, self.pos_ptrs[i % self.POSITION_STEPS],
+                                               self.lens_ptr, self.o_ptr, None, self.sptr)
         if rc:
             self._lib.check(rc, "decode_append")
 

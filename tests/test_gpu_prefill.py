@@ -169,13 +169,13 @@ def test_prefill_paired_causal(hq, hkv, d, q_len, kv_len, qb, kb):
         with AttentionAccelerator(n_q_heads=hq, n_kv_heads=hkv, head_dim=d, max_seq_len=kv_len,
                                   max_q_len=q_len) as acc:
             set_prefill_kernel(acc, kernel)
+            if kernel == "shared":  # the unpaired kernel in one KV segment, as the paired one runs
+                drv._lib.check(acc._lib.gqa_set_option(acc._ctx, drv._lib.GQA_OPT_PREFILL_WGS, 1), "wgs")
             acc.load_kv(k, v)
             outs[kernel] = acc.prefill_chunk(q, q_pos_base=qb, kv_len=kv_len, kv_pos_base=kb, causal=True,
                                              return_lse=True)
-            # a forced decomposition must be the one that ran (one KV segment when paired)
-            assert acc.last_prefill_plan()[0] == kernel
-            if kernel == "paired":
-                assert acc.last_prefill_plan()[1] == 1
+            # the forced decomposition is the one that ran, in one KV segment
+            assert acc.last_prefill_plan() == (kernel, 1)
     ref, ref_lse = oracle_for(q, k, v, causal=True, q_pos_base=qb, kv_pos_base=kb)
     check_rows(*outs["paired"], ref, ref_lse)
     short = (q_len // 32 + (q_len % 32 > 0)) // 2 * 32  # rows of the short row blocks
