@@ -344,18 +344,20 @@ int gqa_layer_qkv_device(gqa_ctx* ctx, int32_t b, const void* x, int32_t n_token
                          int32_t rope, void* q_out, void* stream);
 int gqa_layer_times(gqa_ctx* ctx, float* out_us, int32_t n);
 
-/* ---- HIP graphs -------------------------------------------------------------------
- * No reference counterpart (the board's transaction is driven by CSR writes).  For callers that
- * must capture (a serving loop that replays a whole captured step, harnesses that only accept
- * graphs): on this ROCm a replay costs the host more than the eager launches of the same step,
- * so eager calls are the faster path (B1 x 4097 keys: 25-45 us per replayed step against about 9 us
- * eager, back to back).  gqa_graph_capture_decode_append records one
- * gqa_decode_append_device step (k_rows = v_rows = positions = NULL: gqa_decode_device) with
- * these device pointers into a HIP graph; gqa_graph_launch replays it on `stream` (NULL = the
- * context stream), reading q, rows, positions and ctx_lens and writing o, lse and the cache at
- * the captured addresses, so the caller updates those buffers in place between replays.  The
- * split plan is fixed at capture (sized for max_seq_len).  A graph must be destroyed before
- * its context; profiling timers do not record replays. */
+/* ---- prepared decode steps ---------------------------------------------------------
+ * No reference counterpart (the board's transaction is driven by CSR writes).  For serving loops
+ * that replay one step shape over fixed device buffers.  gqa_graph_capture_decode_append plans one
+ * gqa_decode_append_device step (k_rows = v_rows = positions = NULL: gqa_decode_device) over these
+ * device pointers -- split plan sized for max_seq_len, kernel arguments bound -- and launches
+ * nothing; gqa_graph_launch launches that step on `stream` (NULL = the context stream), reading q,
+ * rows, positions and ctx_lens and writing o, lse and the cache at the bound addresses, so the
+ * caller updates those buffers in place between launches.  A launch is the eager step's kernels
+ * without the planning: no slower than gqa_decode_append_device.  (A HIP graph of the same step,
+ * replayed back to back on this ROCm, cost 4.6 us more GPU time per replay and about 15 us of host
+ * time per launch: B1 x 4097 keys 12.9 us against 8.3 eager.)  Callers that need a real HIP graph
+ * capture gqa_decode_append_device or gqa_decode_append_noalloc in their own stream capture:
+ * those calls enqueue only kernel launches (no allocation, synchronisation or memset).  A prepared
+ * step must be destroyed before its context; profiling timers do not record its launches. */
 typedef struct gqa_graph gqa_graph;
 int gqa_graph_capture_decode_append(gqa_ctx* ctx, const void* q, const void* k_rows, const void* v_rows,
                                     const int32_t* positions, const int32_t* ctx_lens, void* o,

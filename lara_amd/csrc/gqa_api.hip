@@ -117,16 +117,16 @@ struct gqa_ctx {
     int page_size = 0, page_shift = 0, n_pages = 0, max_pages = 0;
     int32_t* table_dev = nullptr;
     PageTable pages;
-    int capturing = 0;  // a HIP graph capture is recording this context's launches (no timer events)
     int last_prefill_kernel = 0;  // decomposition and KV segments of the last prefill launch (gqa_last_prefill_plan)
     int last_prefill_segs = 0;
 };
 
-// A captured decode step (gqa_graph_capture_decode_append) and the context it reads.
+// A prepared decode step (gqa_graph_capture_decode_append): the launch description planned once,
+// replayed by direct launches, and the context it reads.
 struct gqa_graph {
     gqa_ctx* ctx = nullptr;
-    hipGraph_t graph = nullptr;
-    hipGraphExec_t exec = nullptr;
+    lara::DecodeArgs args{};
+    bool combine = false;
 };
 
 namespace {
@@ -216,12 +216,19 @@ int choose_chunk(const gqa_ctx* c, int max_len) {
 
 constexpr int kProfileLaunches = 512;  // event pairs kept per timer slot
 
-// A launch on stream s; while profiling (outside a graph capture), with the next event pair of
+// Whether work enqueued on s is being recorded into a caller's HIP graph (stream capture): such
+// launches take no timer events and the layer stage does not tune on them.
+bool stream_capturing(hipStream_t s) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+}
+
+// A launch on stream s; while profiling (outside a stream capture), with the next event pair of
 // the timer slot bound to the launch itself (no marker commands between launches).
 Launch timed(gqa_ctx* c, int slot, hipStream_t s) {
     Launch l;
     l.stream = s;
-    if (c->profile && !c->capturing && c->ev_count[slot] < kProfileLaunches) {
+    if (c->profile && c->ev_count[slot] < kProfileLaunches && !stream_capturing(s)) {
         l.start = c->ev_pool[slot][2 * c->ev_count[slot]];
         l.stop = c->ev_pool[slot][2 * c->ev_count[slot] + 1];
         c->ev_count[slot] += 1;
@@ -247,13 +254,16 @@ int profile_enable(gqa_ctx* c, int on) {
     return GQA_OK;
 }
 
-int run_decode(gqa_ctx* c, const void* q, const int32_t* lens, const void* k_new, const void* v_new,
-               const int32_t* positions, void* o, float* lse, hipStream_t s, int max_len) {
+// The launch description of one decode step (split kernel, plus the merge launch when *combine);
+// run_decode launches it, a prepared step (gqa_graph) keeps it for its replays.
+int plan_decode(gqa_ctx* c, const void* q, const int32_t* lens, const void* k_new, const void* v_new,
+                const int32_t* positions, void* o, float* lse, int max_len, DecodeArgs* out, bool* combine) {
     if (!decode_supported(c->cfg.head_dim, c->group) || c->numerics != GQA_NUMERICS_EXACT) return GQA_ERR_UNSUPPORTED;
     const int chunk = choose_chunk(c, max_len);
     const int max_splits = decode_split_count(max_len, chunk);
     if (max_splits > c->max_splits_cap) return GQA_ERR_RANGE;
-    DecodeArgs a{};
+    DecodeArgs& a = *out;
+    a = DecodeArgs{};
     a.q = (const uint16_t*)q;
     a.kc = c->k_cache;
     a.vc = c->v_cache;
@@ -280,9 +290,18 @@ int run_decode(gqa_ctx* c, const void* q, const int32_t* lens, const void* k_new
     a.cached = decode_cached_loads((int64_t)c->cfg.batch * c->cfg.n_kv_heads, max_len, c->cfg.head_dim) ? 1 : 0;
     a.arrivals = fuse_merge(c->decode_merge, c->cfg.batch * c->cfg.n_kv_heads, max_splits, c->n_cu) ? c->arrivals
                                                                                                       : nullptr;
+    *combine = max_splits > 1 && a.arrivals == nullptr;
+    return GQA_OK;
+}
+
+int run_decode(gqa_ctx* c, const void* q, const int32_t* lens, const void* k_new, const void* v_new,
+               const int32_t* positions, void* o, float* lse, hipStream_t s, int max_len) {
+    DecodeArgs a;
+    bool combine = false;
+    const int rc = plan_decode(c, q, lens, k_new, v_new, positions, o, lse, max_len, &a, &combine);
+    if (rc != GQA_OK) return rc;
     HIP_TRY(launch_decode(c->cfg.head_dim, c->group, a, timed(c, GQA_TIMER_DECODE, s)));
-    if (max_splits > 1 && a.arrivals == nullptr)
-        HIP_TRY(launch_combine(c->cfg.head_dim, c->group, a, timed(c, GQA_TIMER_COMBINE, s)));
+    if (combine) HIP_TRY(launch_combine(c->cfg.head_dim, c->group, a, timed(c, GQA_TIMER_COMBINE, s)));
     return GQA_OK;
 }
 
@@ -627,8 +646,9 @@ int run_layer_qkv(gqa_ctx* c, int32_t b, const void* x, int32_t n_tokens, int32_
         ProjectionPlan* p = nullptr;
         rc = projection_plan(c, rows[i], n_tokens, hidden, ld, &p);
         if (rc != GQA_OK) return rc;
+        const bool tune = !p->tuned && !stream_capturing(s);
         size_t ws_need = p->cand[p->pick].workspaceSize;
-        if (!p->tuned && !c->capturing)
+        if (tune)
             for (int k = 0; k < p->n_cand; ++k) ws_need = std::max(ws_need, p->cand[k].workspaceSize);
         rc = ensure_buffer(&c->lt_ws, &c->lt_ws_bytes, std::max<size_t>(ws_need, 256));
         if (rc != GQA_OK) return rc;
@@ -636,7 +656,7 @@ int run_layer_qkv(gqa_ctx* c, int32_t b, const void* x, int32_t n_tokens, int32_
             return hipblasLtMatmul(c->lt, p->desc, &one, ws[i], p->w, src, p->x, &zero, qkv + off[i], p->d,
                                    qkv + off[i], p->d, &p->cand[k].algo, c->lt_ws, p->cand[k].workspaceSize, s);
         };
-        if (!p->tuned && !c->capturing) {
+        if (tune) {
             rc = tune_projection(c, p, gemm, s);
             if (rc != GQA_OK) return rc;
         }
@@ -1577,35 +1597,12 @@ int gqa_graph_capture_decode_append(gqa_ctx* c, const void* q, const void* k_row
     if (!aligned16(q) || !aligned16(k_rows) || !aligned16(v_rows)) return GQA_ERR_RANGE;
     int rc = txn_idle(c);
     if (rc != GQA_OK) return rc;
-    HIP_TRY(hipSetDevice(c->cfg.device));
-    hipStream_t cap = nullptr;
-    HIP_TRY(hipStreamCreateWithFlags(&cap, hipStreamNonBlocking));
     gqa_graph* g = new gqa_graph();
     g->ctx = c;
-    hipError_t e = hipStreamBeginCapture(cap, hipStreamCaptureModeThreadLocal);
-    if (e == hipSuccess) {
-        c->capturing = 1;
-        rc = run_decode(c, q, ctx_lens, k_rows, v_rows, positions, o, lse, cap, c->cfg.max_seq_len);
-        c->capturing = 0;
-        const hipError_t e2 = hipStreamEndCapture(cap, &g->graph);
-        if (rc == GQA_OK && e2 != hipSuccess) {
-            last_hip_error(e2, "hipStreamEndCapture");
-            rc = GQA_ERR_HIP;
-        }
-    } else {
-        last_hip_error(e, "hipStreamBeginCapture");
-        rc = GQA_ERR_HIP;
-    }
-    if (rc == GQA_OK) {
-        e = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
-        if (e != hipSuccess) {
-            last_hip_error(e, "hipGraphInstantiate");
-            rc = GQA_ERR_HIP;
-        }
-    }
-    (void)hipStreamDestroy(cap);
+    // The plan of gqa_decode_append_device for device-resident lengths (sized for max_seq_len).
+    rc = plan_decode(c, q, ctx_lens, k_rows, v_rows, positions, o, lse, c->cfg.max_seq_len, &g->args, &g->combine);
     if (rc != GQA_OK) {
-        gqa_graph_destroy(g);
+        delete g;
         return rc;
     }
     *out = g;
@@ -1613,16 +1610,18 @@ int gqa_graph_capture_decode_append(gqa_ctx* c, const void* q, const void* k_row
 }
 
 int gqa_graph_launch(gqa_graph* g, void* stream) {
-    if (!g || !g->exec) return GQA_ERR_NULL;
-    HIP_TRY(hipSetDevice(g->ctx->cfg.device));
-    HIP_TRY(hipGraphLaunch(g->exec, pick_stream(g->ctx, stream)));
+    if (!g || !g->ctx) return GQA_ERR_NULL;
+    gqa_ctx* c = g->ctx;
+    HIP_TRY(hipSetDevice(c->cfg.device));
+    Launch l;
+    l.stream = pick_stream(c, stream);
+    HIP_TRY(launch_decode(c->cfg.head_dim, c->group, g->args, l));
+    if (g->combine) HIP_TRY(launch_combine(c->cfg.head_dim, c->group, g->args, l));
     return GQA_OK;
 }
 
 int gqa_graph_destroy(gqa_graph* g) {
     if (!g) return GQA_ERR_NULL;
-    if (g->exec) (void)hipGraphExecDestroy(g->exec);
-    if (g->graph) (void)hipGraphDestroy(g->graph);
     delete g;
     return GQA_OK;
 }
