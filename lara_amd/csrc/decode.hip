@@ -571,10 +571,6 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
 // matrix-core rounds, so two waves per SIMD), which gives one (sequence, kv head) twice the loads in
 // flight of a 4-wave work-group: ragged batches finish their long sequences sooner, and a long
 // context is cut into half as many splits.
-template <int G>
-constexpr int decode_waves_t() {
-    return 8;
-}
 
 template <int D, int G, int NW>
 __global__ __launch_bounds__(NW * 64) void decode_combine_kernel(DecodeArgs a) {
@@ -590,9 +586,8 @@ __global__ __launch_bounds__(NW * 64) void decode_combine_kernel(DecodeArgs a) {
     merge_splits_parallel<D, G, NW>(a, unit, b, h, n_splits, lds_o, lds_m, lds_l);
 }
 
-template <int D, int G>
-hipError_t launch_decode_t(const DecodeArgs& a, const Launch& l) {
-    constexpr int NW = decode_waves_t<G>();
+template <int D, int G, int NW>
+hipError_t launch_decode_nw(const DecodeArgs& a, const Launch& l) {
     dim3 grid(a.max_splits, a.batch * a.n_kv_heads);
     if (a.cached) {
         if (a.block_table != nullptr)
@@ -605,18 +600,25 @@ hipError_t launch_decode_t(const DecodeArgs& a, const Launch& l) {
 }
 
 template <int D, int G>
+hipError_t launch_decode_t(const DecodeArgs& a, const Launch& l) {
+    if (a.waves == kDecodeWavesSmall) return launch_decode_nw<D, G, kDecodeWavesSmall>(a, l);
+    if (a.waves == kDecodeWaves) return launch_decode_nw<D, G, kDecodeWaves>(a, l);
+    return hipErrorInvalidValue;
+}
+
+template <int D, int G>
 hipError_t launch_combine_t(const DecodeArgs& a, const Launch& l) {
-    constexpr int NW = decode_waves_t<G>();
-    return launch_kernel(decode_combine_kernel<D, G, NW>, dim3(a.batch * a.n_kv_heads), dim3(NW * 64), l, a);
+    const dim3 grid(a.batch * a.n_kv_heads);
+    if (a.waves == kDecodeWavesSmall)
+        return launch_kernel(decode_combine_kernel<D, G, kDecodeWavesSmall>, grid, dim3(kDecodeWavesSmall * 64), l, a);
+    if (a.waves == kDecodeWaves)
+        return launch_kernel(decode_combine_kernel<D, G, kDecodeWaves>, grid, dim3(kDecodeWaves * 64), l, a);
+    return hipErrorInvalidValue;
 }
 
 }  // namespace
 
 int decode_round_keys(int) { return 16; }  // RK of decode_split_kernel, every group size
-
-int decode_waves(int group) {
-    return group <= 4 ? decode_waves_t<4>() : group <= 8 ? decode_waves_t<8>() : decode_waves_t<16>();
-}
 
 bool decode_supported(int head_dim, int group) {
     return (head_dim == 64 || head_dim == 128) && (group == 2 || group == 4 || group == 8 || group == 16);

@@ -171,21 +171,21 @@ hipStream_t pick_stream(gqa_ctx* c, void* s) { return s ? (hipStream_t)s : c->st
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 // Splits per (sequence, kv head) the automatic plan aims for: about kDecodeWavesPerCu waves per CU
-// over the batch's units.
-int plan_splits(int batch, int n_kv_heads, int group, int n_cu) {
+// over the batch's units, with `waves` waves per work-group.
+int plan_splits(int batch, int n_kv_heads, int n_cu, int waves) {
     const int units = batch * n_kv_heads;
-    const int target_wgs = kDecodeWavesPerCu * n_cu / decode_waves(group);
+    const int target_wgs = kDecodeWavesPerCu * n_cu / waves;
     const int splits = (target_wgs + units - 1) / units;
     return splits < 1 ? 1 : splits;
 }
 
 // Keys per split for max_len attended keys: max_len over plan_splits, in whole rounds of every wave
-// of a work-group (128 keys at D 128, group 4) so the waves of a split share its keys evenly --
-// rounded down when that still gives at most plan_splits splits (a short tail joins the last split),
-// else up.  decode_split_count(max_len, chunk) <= plan_splits either way.
-int plan_chunk(int batch, int n_kv_heads, int group, int n_cu, int max_len) {
-    const int quantum = decode_waves(group) * decode_round_keys(group);
-    const int splits = plan_splits(batch, n_kv_heads, group, n_cu);
+// of a work-group (128 keys with 8 waves) so the waves of a split share its keys evenly -- rounded
+// down when that still gives at most plan_splits splits (a short tail joins the last split), else
+// up.  decode_split_count(max_len, chunk) <= plan_splits either way.
+int plan_chunk(int batch, int n_kv_heads, int group, int n_cu, int max_len, int waves) {
+    const int quantum = waves * decode_round_keys(group);
+    const int splits = plan_splits(batch, n_kv_heads, n_cu, waves);
     const int even = (max_len + splits - 1) / splits;
     const int down = std::max(quantum, even / quantum * quantum);
     if (decode_split_count(max_len, down) <= splits) return down;
@@ -209,9 +209,29 @@ bool fuse_merge(int option, int units, int max_splits, int n_cu) {
            (2 * (int64_t)units * max_splits <= n_cu && max_splits <= kFusedMergeSplits);
 }
 
-int choose_chunk(const gqa_ctx* c, int max_len) {
-    if (c->chunk_opt > 0) return c->chunk_opt;
-    return plan_chunk(c->cfg.batch, c->cfg.n_kv_heads, c->group, c->n_cu, max_len);
+// A decode launch's shape: keys per split, splits and waves per work-group.  Work-groups have
+// kDecodeWaves waves, except in launches of at most kSmallDecodeGrid work-groups at that size (a
+// step that is a short latency chain, such as one sequence of a few hundred keys): those are
+// planned with kDecodeWavesSmall waves per work-group, which start and merge sooner (measured,
+// 8 q / 2 kv heads, D 64, 256 keys: 4.87 vs 5.04 us of kernel; at 256 work-groups and more the
+// 8-wave shape streams faster).  chunk_opt > 0 forces the keys per split.
+constexpr int64_t kSmallDecodeGrid = 8;
+
+struct DecodeShape {
+    int chunk;
+    int max_splits;
+    int waves;
+};
+
+DecodeShape plan_decode_shape(int batch, int n_kv_heads, int group, int n_cu, int max_len, int chunk_opt) {
+    const int64_t units = (int64_t)batch * n_kv_heads;
+    auto shape = [&](int waves) {
+        const int chunk = chunk_opt > 0 ? chunk_opt : plan_chunk(batch, n_kv_heads, group, n_cu, max_len, waves);
+        return DecodeShape{chunk, decode_split_count(max_len, chunk), waves};
+    };
+    const DecodeShape big = shape(kDecodeWaves);
+    if (units * big.max_splits > kSmallDecodeGrid) return big;
+    return shape(kDecodeWavesSmall);
 }
 
 constexpr int kProfileLaunches = 512;  // event pairs kept per timer slot
@@ -259,8 +279,9 @@ int profile_enable(gqa_ctx* c, int on) {
 int plan_decode(gqa_ctx* c, const void* q, const int32_t* lens, const void* k_new, const void* v_new,
                 const int32_t* positions, void* o, float* lse, int max_len, DecodeArgs* out, bool* combine) {
     if (!decode_supported(c->cfg.head_dim, c->group) || c->numerics != GQA_NUMERICS_EXACT) return GQA_ERR_UNSUPPORTED;
-    const int chunk = choose_chunk(c, max_len);
-    const int max_splits = decode_split_count(max_len, chunk);
+    const DecodeShape shape = plan_decode_shape(c->cfg.batch, c->cfg.n_kv_heads, c->group, c->n_cu, max_len, c->chunk_opt);
+    const int chunk = shape.chunk;
+    const int max_splits = shape.max_splits;
     if (max_splits > c->max_splits_cap) return GQA_ERR_RANGE;
     DecodeArgs& a = *out;
     a = DecodeArgs{};
@@ -288,6 +309,7 @@ int plan_decode(gqa_ctx* c, const void* q, const int32_t* lens, const void* k_ne
     a.zero_row = c->zero_row;
     a.longest_first = c->cfg.batch > 1;
     a.cached = decode_cached_loads((int64_t)c->cfg.batch * c->cfg.n_kv_heads, max_len, c->cfg.head_dim) ? 1 : 0;
+    a.waves = shape.waves;
     a.arrivals = fuse_merge(c->decode_merge, c->cfg.batch * c->cfg.n_kv_heads, max_splits, c->n_cu) ? c->arrivals
                                                                                                       : nullptr;
     *combine = max_splits > 1 && a.arrivals == nullptr;
@@ -739,9 +761,12 @@ int create_ctx(const gqa_config* cfg, int32_t page_size, int32_t n_pages, int32_
     c->cfg = k;
     c->group = group;
     c->l_cap = ((k.max_seq_len + 63) / 64) * 64;
+    // Enough partial slots for any plan: the automatic one at either work-group shape, or forced
+    // chunks down to kMinSplitCap keys.
     c->max_splits_cap = std::max((c->l_cap + kMinSplitCap - 1) / kMinSplitCap,
-                                 plan_splits(k.batch, k.n_kv_heads, group, prop.multiProcessorCount > 0
-                                                                             ? prop.multiProcessorCount : 256));
+                                 plan_splits(k.batch, k.n_kv_heads,
+                                             prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256,
+                                             kDecodeWavesSmall));
     c->scale = k.scale > 0.f ? k.scale : (float)(1.0 / sqrt((double)k.head_dim));
     c->cfg.scale = c->scale;
     c->clock_mhz = prop.clockRate / 1000.0;
@@ -1368,8 +1393,9 @@ int gqa_decode_append_noalloc(const gqa_config* cfg, void* k_cache, void* v_cach
     if (rc != GQA_OK) return rc;
     // The plan gqa_decode_append_device makes for the same configuration (keys per split from the
     // CU count and max_seq_len), so both entry points give the same words.
-    const int chunk = plan_chunk(k.batch, k.n_kv_heads, group, dev->n_cu, k.max_seq_len);
-    const int max_splits = decode_split_count(k.max_seq_len, chunk);
+    const DecodeShape shape = plan_decode_shape(k.batch, k.n_kv_heads, group, dev->n_cu, k.max_seq_len, 0);
+    const int chunk = shape.chunk;
+    const int max_splits = shape.max_splits;
     const size_t rows = (size_t)k.batch * k.n_kv_heads * max_splits * group;  // partial rows of the plan
     const size_t o_bytes = max_splits > 1 ? (rows * k.head_dim * sizeof(float) + 255) / 256 * 256 : 0;
     const size_t ml_bytes = max_splits > 1 ? rows * 2 * sizeof(float) : 0;
@@ -1397,6 +1423,7 @@ int gqa_decode_append_noalloc(const gqa_config* cfg, void* k_cache, void* v_cach
     a.zero_row = dev->zero;
     a.longest_first = k.batch > 1;
     a.cached = decode_cached_loads((int64_t)k.batch * k.n_kv_heads, k.max_seq_len, k.head_dim) ? 1 : 0;
+    a.waves = shape.waves;
     // The same merge as the context entry point's default (GQA_DECODE_MERGE_AUTO), when the counters
     // cover the units.
     const int units = k.batch * k.n_kv_heads;

@@ -87,7 +87,13 @@ struct DecodeArgs {
     // Nonzero: K/V rows are read with plain (L2-allocating) loads instead of nontemporal ones
     // (decode_cached_loads).
     int32_t cached;
+    // Waves per work-group of the split and merge kernels: kDecodeWaves, or kDecodeWavesSmall for
+    // launches that are a short latency chain (plan_decode_shape).  Both kernels of a plan use the
+    // same count, so the in-launch merge and the merge launch fold in the same order.
+    int32_t waves;
 };
+constexpr int kDecodeWaves = 8;
+constexpr int kDecodeWavesSmall = 4;
 // Whether a decode launch over `units` (sequence, kv head) units of at most max_len keys reads
 // its K/V with plain loads: when they fit the L2s of the XCDs (4 MiB each) several times over, a
 // step finds them where the last one left them.
@@ -195,7 +201,7 @@ bool decode_supported(int head_dim, int group);
 // Keys a wave of the decode kernel takes per round (a divisor of 64) for a group size.
 int decode_round_keys(int group);
 // Waves per split work-group of the decode kernel for a group size.
-int decode_waves(int group);
+
 // Split-KV attention with an optional fused row append; sequences longer than one split
 // leave fp32 partials that launch_combine merges.
 hipError_t launch_decode(int head_dim, int group, const DecodeArgs& a, const Launch& l);
