@@ -1356,15 +1356,20 @@ def main() -> int:
             "n_kv_heads": w.n_kv_heads,
             "head_dim": w.head_dim,
             "attended_keys": int(w.lengths().max()),
-            "step": "append 1 K/V row per sequence fused into the split-KV decode launch (a second LSE-merge "
-                    "launch only when a sequence spans several splits; none at this shape); rolling append: step i "
-                    "writes row (L - 1 + i) mod L of each sequence (a ring over its L rows) and attends all L rows; "
+            "step": "append 1 K/V row per sequence fused into the split-KV decode launch ("
+                    + ("plus an LSE-merge launch: the sequences span several splits"
+                       if main_r["merges_per_step"] > 0 else
+                       "no merge launch: one split per sequence, or the splits merged inside the launch")
+                    + "); rolling append: step i writes row (L - 1 + i) mod L of each sequence (a ring over its L "
+                    "rows) and attends all L rows; "
                     f"Q and the new rows cycle over {DecodeBench.INPUT_SETS} seeded sets",
             "accumulate": "fp32",
             "working_set_bytes": main_r["working_set_bytes"],
             "residency": main_r["residency"],
         },
-        "kernels_us": {"decode_step": main_r["decode_us"]},
+        "kernels_us": {"decode_step": main_r["decode_us"],
+                       "merge": main_r["combine_us"] if main_r["merges_per_step"] > 0 else None,
+                       "per_step": main_r["kernels_us_per_step"]},
         "roofline": roofline,
         "read_ceiling": ceiling,
         "launch_floor": floor,
