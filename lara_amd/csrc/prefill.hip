@@ -413,6 +413,9 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
     // The running reference max only moves when a block's max exceeds it by more than
     // kLazyLog2 (p <= 2^kLazyLog2 meanwhile), so most blocks skip the O rescale.
     constexpr float kLazyLog2 = 8.0f;
+    // Weights up to this sum per lane are taken against a stale reference max (see the block's
+    // weights below): 2^16, so O = sum p v stays finite for |v| up to about 10^31 over 1024 keys.
+    constexpr float kFreeSum = 65536.0f;
     const float c = a.scale_log2;
 
     // Q^T operand: row `row`, dims 16*ks + 8*half .. +7.  The Q loads, the first two blocks'
@@ -483,7 +486,6 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
         const int rb_now = PAIR ? cur_rb : rb;
         const bool need_mask = (jb + 32 * NT > a.kv_len) ||
                                (a.causal && a.kv_pos_base + jb + 32 * NT - 1 > a.q_pos_base + rb_now * kRows);
-        float mx = -INFINITY;
         if (need_mask) {
 #pragma unroll
             for (int kt = 0; kt < NT; ++kt)
@@ -492,46 +494,60 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
                     const int j = jb + kt * 32 + 8 * (i >> 2) + 4 * half + (i & 3);
                     const bool ok = row_ok && j < a.kv_len && (!a.causal || a.kv_pos_base + j <= q_pos);
                     sacc[kt][i] = ok ? sacc[kt][i] : -INFINITY;
-                    mx = fmaxf(mx, sacc[kt][i]);
                 }
-        } else {
+        }
+        // p = 2^(s*c - m_run); with no valid key yet (m_run = -inf) every s of the block is -inf
+        // as well, and a finite offset keeps 2^(-inf) = 0 without a per-score select.
+        float psum = 0.f;
+        u32x4 pb[2 * NT];  // P^T operand of the PV k-steps (kt, a2)
+        auto weights = [&]() __attribute__((always_inline)) {
+            const float nm = (m_run == -INFINITY) ? 0.f : -m_run;
+            psum = 0.f;
+#pragma unroll
+            for (int kt = 0; kt < NT; ++kt)
+#pragma unroll
+                for (int a2 = 0; a2 < 2; ++a2) {
+                    float p[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const float sv = sacc[kt][8 * a2 + j];
+                        p[j] = __builtin_amdgcn_exp2f(fmaf(sv, c, nm));
+                        psum += p[j];
+                    }
+                    pb[2 * kt + a2] = u32x4{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
+                                            pack_bf16x2(p[6], p[7])};
+                }
+        };
+        // Once every row of the wave has a reference max, the weights are taken against it directly
+        // and the block's own max is needed only where a lane's weights sum past kFreeSum (or
+        // overflow): weights up to that size keep their relative precision in the bf16 P operand and
+        // in the fp32 sums, so the reference max stays until a block passes it by about 11 (log2).
+        bool need_max = __ballot(m_run == -INFINITY) != 0;
+        if (!need_max) {
+            weights();
+            need_max = __ballot(!(psum <= kFreeSum)) != 0;  // also true for inf and NaN
+        }
+        if (need_max) {
+            float mx = -INFINITY;
 #pragma unroll
             for (int kt = 0; kt < NT; ++kt)
 #pragma unroll
                 for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[kt][i]);
-        }
-        mx = pair_max32(mx);
-        const float bm = mx * c;  // block max in log2 units (-inf if every key is masked)
-        const bool grow = bm > m_run + kLazyLog2;
-        if (__ballot(grow) != 0) {
-            const float m_new = grow ? bm : m_run;
-            const float corr = (m_run == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
-            m_run = m_new;
-            l_lane *= corr;
+            mx = pair_max32(mx);
+            const float bm = mx * c;  // block max in log2 units (-inf if every key is masked)
+            const bool grow = bm > m_run + kLazyLog2;
+            if (__ballot(grow) != 0) {
+                const float m_new = grow ? bm : m_run;
+                const float corr = (m_run == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
+                m_run = m_new;
+                l_lane *= corr;
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
+                for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-                for (int i = 0; i < 16; ++i) o[mt][i] *= corr;
-        }
-        // p = 2^(s*c - m_run); with no valid key yet (m_run = -inf) every s of the block is -inf
-        // as well, and a finite offset keeps 2^(-inf) = 0 without a per-score select.
-        const float nm = (m_run == -INFINITY) ? 0.f : -m_run;
-        float psum = 0.f;
-        u32x4 pb[2 * NT];  // P^T operand of the PV k-steps (kt, a2)
-#pragma unroll
-        for (int kt = 0; kt < NT; ++kt)
-#pragma unroll
-            for (int a2 = 0; a2 < 2; ++a2) {
-                float p[8];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const float sv = sacc[kt][8 * a2 + j];
-                    p[j] = __builtin_amdgcn_exp2f(fmaf(sv, c, nm));
-                    psum += p[j];
-                }
-                pb[2 * kt + a2] = u32x4{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
-                                        pack_bf16x2(p[6], p[7])};
+                    for (int i = 0; i < 16; ++i) o[mt][i] *= corr;
             }
+            weights();
+        }
         l_lane += psum;
 
         // ---- O^T += V^T . P^T ----
@@ -937,6 +953,7 @@ __global__ __launch_bounds__(NW * 64) void prefill_rows_kernel(PrefillArgs a) {
     float m_run = -INFINITY;  // running max (log2 units) of this lane's row
     float l_lane = 0.f;       // this lane's half of the running sum
     constexpr float kLazyLog2 = 8.0f;  // the reference max moves only when passed by more than this
+    constexpr float kFreeSum = 65536.0f;  // 2^16, as in prefill_kernel
     const float c = a.scale_log2;
 
     // Appended rows of kv head h go to the cache in equal shares over the kv head's work-groups;
@@ -1040,44 +1057,53 @@ __global__ __launch_bounds__(NW * 64) void prefill_rows_kernel(PrefillArgs a) {
         // ---- online softmax (log2 domain, scale folded into the exponent) ----
         const bool need_mask =
             (j0 + kRowBN > a.kv_len) || (a.causal && a.kv_pos_base + j0 + kRowBN - 1 > a.q_pos_base + rb * kRows);
-        float mx = -INFINITY;
         if (need_mask) {
             const int d = key_lim - (j0 + 4 * half);  // key j0 + 4*half + c is valid iff c < d
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                sacc[i] = 8 * (i >> 2) + (i & 3) < d ? sacc[i] : -INFINITY;
-                mx = fmaxf(mx, sacc[i]);
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[i]);
+            for (int i = 0; i < 16; ++i) sacc[i] = 8 * (i >> 2) + (i & 3) < d ? sacc[i] : -INFINITY;
         }
-        mx = pair_max32(mx);
-        const float bm = mx * c;
-        const bool grow = bm > m_run + kLazyLog2;
-        if (__ballot(grow) != 0) {
-            const float m_new = grow ? bm : m_run;
-            const float corr = (m_run == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
-            m_run = m_new;
-            l_lane *= corr;
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) o[mt][i] *= corr;
-        }
-        const float nm = (m_run == -INFINITY) ? 0.f : -m_run;
         float psum = 0.f;
         u32x4 pb[2];  // P^T operand of the two PV k-steps (keys 0-15, 16-31 of the block)
+        auto weights = [&]() __attribute__((always_inline)) {
+            const float nm = (m_run == -INFINITY) ? 0.f : -m_run;
+            psum = 0.f;
 #pragma unroll
-        for (int a2 = 0; a2 < 2; ++a2) {
-            float p[8];
+            for (int a2 = 0; a2 < 2; ++a2) {
+                float p[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                p[j] = __builtin_amdgcn_exp2f(fmaf(sacc[8 * a2 + j], c, nm));
-                psum += p[j];
+                for (int j = 0; j < 8; ++j) {
+                    p[j] = __builtin_amdgcn_exp2f(fmaf(sacc[8 * a2 + j], c, nm));
+                    psum += p[j];
+                }
+                pb[a2] = u32x4{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
+                               pack_bf16x2(p[6], p[7])};
             }
-            pb[a2] = u32x4{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
-                           pack_bf16x2(p[6], p[7])};
+        };
+        // As in prefill_kernel: against the reference max directly once every row has one; the
+        // block's own max only where a lane's weights sum past kFreeSum or overflow.
+        bool need_max = __ballot(m_run == -INFINITY) != 0;
+        if (!need_max) {
+            weights();
+            need_max = __ballot(!(psum <= kFreeSum)) != 0;  // also true for inf and NaN
+        }
+        if (need_max) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[i]);
+            mx = pair_max32(mx);
+            const float bm = mx * c;
+            const bool grow = bm > m_run + kLazyLog2;
+            if (__ballot(grow) != 0) {
+                const float m_new = grow ? bm : m_run;
+                const float corr = (m_run == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
+                m_run = m_new;
+                l_lane *= corr;
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) o[mt][i] *= corr;
+            }
+            weights();
         }
         l_lane += psum;
 

@@ -368,6 +368,30 @@ def test_segment_partials_at_extreme_magnitudes(v_scale):
     check_rows(outs[1][0], outs[1][1], ref, ref_lse)
 
 
+@pytest.mark.parametrize("kernel", ["rows", "shared", "paired"])
+def test_prefill_scores_climbing_past_the_reference_max(kernel):
+    """Scores that climb block after block far past the first block's max (positive Q, K rows
+    scaled by a ramp: about 140 log2 units over the prompt) with V of magnitude 1e20.  The kernels
+    take a block's weights against the row's reference max while a lane's weights sum to at most
+    2^16 and otherwise move the max and rescale; both paths run here, and every output row is within
+    the 2-ulp bound and finite."""
+    rng = np.random.default_rng(777)
+    hq, hkv, d, L = 32, 8, 128, 512
+    print(f"[climb] kernel={kernel} L={L}", flush=True)
+    q = orc.fp32_to_bf16_u16(np.abs(rng.standard_normal((hq, L, d), dtype=np.float32)) + np.float32(1.0))
+    ramp = np.linspace(0.0, 6.0, L, dtype=np.float32)[None, :, None]
+    k = orc.fp32_to_bf16_u16(np.abs(rng.standard_normal((hkv, L, d), dtype=np.float32)) * ramp)
+    v = bf16_normal(rng, (hkv, L, d), 1e20)
+    with AttentionAccelerator(max_seq_len=L, max_q_len=L) as acc:
+        set_prefill_kernel(acc, kernel)
+        acc.load_kv(k, v)
+        out, lse = acc.prefill_chunk(q, q_pos_base=0, kv_len=L, causal=True, return_lse=True)
+        assert acc.last_prefill_plan()[0] == kernel
+    assert np.all(np.isfinite(drv.bf16_u16_to_fp32(out)))
+    ref, ref_lse = oracle_for(q, k, v, causal=True)
+    check_rows(out, lse, ref, ref_lse)
+
+
 @pytest.mark.parametrize("kernel", ["rows", "shared"])
 def test_prefill_cancelling_v_rows_within_the_weight_rounding_bound(kernel):
     """Causal prefill over V rows in cancelling pairs: within 2 ulp of the row's largest |output| plus
