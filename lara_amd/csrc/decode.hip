@@ -182,19 +182,22 @@ __device__ int rank_to_sequence(const DecodeArgs& a, int rank) {
     return rank;
 }
 
-// Log-sum-exp merge of the split partials of one (sequence, kv head), split-parallel: wave w
-// folds splits w, w + NW, ... with lane e (and e + 64, ...) owning 8 consecutive dims of one
-// head (16-byte loads of the partial O, one 8-byte load of (m, l)), kMergeBatch splits per
-// memory round trip; then the waves' (M, O, l) fold through LDS and thread (g, d) writes the
-// output.  The split kernel's fused merge (the last split to arrive, after its acquire of the
-// other splits' partials, reusing the LDS of its own wave merge) and decode_combine_kernel run
-// this same code with the same NW, so both fold in the same order and give the same words.
+// Log-sum-exp merge of the split partials of one (sequence, kv head), split-parallel, for its
+// GH heads g0 .. g0 + GH - 1: wave w folds splits w, w + NW, ... with lane e (and e + 64, ...)
+// owning 8 consecutive dims of one head (16-byte loads of the partial O, one 8-byte load of
+// (m, l)), kMergeBatch splits per memory round trip; then the waves' (M, O, l) fold through LDS
+// and thread (g, d) writes the output.  Every (head, 8 dims) entry folds the same splits in the
+// same order whichever lane holds it and however many heads a work-group takes, so the split
+// kernel's fused merge (the last split to arrive merges all G heads, after its acquire of the
+// other splits' partials, reusing the LDS of its own wave merge) and decode_combine_kernel (one
+// work-group per head) give the same words.
 constexpr int kMergeBatch = 4;
 
-template <int D, int G, int NW>
+template <int D, int G, int NW, int GH>
 __device__ __forceinline__ void merge_splits_parallel(const DecodeArgs& a, int unit, int b, int h, int n_splits,
-                                                      float (*lds_o)[G][D], float (*lds_m)[G], float (*lds_l)[G]) {
-    constexpr int E = G * D / 8;               // 8-dim entries of the group's output
+                                                      int g0, float (*lds_o)[GH][D], float (*lds_m)[GH],
+                                                      float (*lds_l)[GH]) {
+    constexpr int E = GH * D / 8;              // 8-dim entries of the heads' output
     constexpr int EPL = (E + 63) / 64;         // entries per lane
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const float4* po = reinterpret_cast<const float4*>(a.part_o);
@@ -213,7 +216,8 @@ __device__ __forceinline__ void merge_splits_parallel(const DecodeArgs& a, int u
         for (int k = 0; k < EPL; ++k) {
             const int e = lane + 64 * k;
             if (e >= E) break;
-            const int g = e / (D / 8), c = e - g * (D / 8);
+            const int gl = e / (D / 8), c = e - gl * (D / 8);
+            const int g = g0 + gl;
             float2 ml[kMergeBatch];
             float4 lo[kMergeBatch], hi[kMergeBatch];
 #pragma unroll
@@ -257,31 +261,31 @@ __device__ __forceinline__ void merge_splits_parallel(const DecodeArgs& a, int u
     for (int k = 0; k < EPL; ++k) {
         const int e = lane + 64 * k;
         if (e >= E) break;
-        const int g = e / (D / 8), c = e - g * (D / 8);
+        const int gl = e / (D / 8), c = e - gl * (D / 8);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) lds_o[wave][g][8 * c + i] = O[k][i];
+        for (int i = 0; i < 8; ++i) lds_o[wave][gl][8 * c + i] = O[k][i];
         if (c == 0) {
-            lds_m[wave][g] = M[k];
-            lds_l[wave][g] = L[k];
+            lds_m[wave][gl] = M[k];
+            lds_l[wave][gl] = L[k];
         }
     }
     __syncthreads();
     const int H_q = a.n_kv_heads * G;
-    for (int idx = threadIdx.x; idx < G * D; idx += NW * 64) {
-        const int g = idx / D, d = idx - g * D;
+    for (int idx = threadIdx.x; idx < GH * D; idx += NW * 64) {
+        const int gl = idx / D, d = idx - gl * D;
         float Mx = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < NW; ++w) Mx = fmaxf(Mx, lds_m[w][g]);
+        for (int w = 0; w < NW; ++w) Mx = fmaxf(Mx, lds_m[w][gl]);
         float Ov = 0.f, Ls = 0.f;
         if (Mx != -INFINITY) {
 #pragma unroll
             for (int w = 0; w < NW; ++w) {
-                const float sc = fast_exp2(lds_m[w][g] - Mx);  // 0 for a wave without splits
-                Ov = fmaf(sc, lds_o[w][g][d], Ov);
-                Ls = fmaf(sc, lds_l[w][g], Ls);
+                const float sc = fast_exp2(lds_m[w][gl] - Mx);  // 0 for a wave without splits
+                Ov = fmaf(sc, lds_o[w][gl][d], Ov);
+                Ls = fmaf(sc, lds_l[w][gl], Ls);
             }
         }
-        const size_t row = (size_t)b * H_q + h * G + g;
+        const size_t row = (size_t)b * H_q + h * G + g0 + gl;
         a.out[row * D + d] = f32_to_bf16_rne(Ls > 0.f ? Ov / Ls : 0.f);
         if (d == 0 && a.lse != nullptr) a.lse[row] = Ls > 0.f ? (Mx + log2f(Ls)) * kLn2 : -INFINITY;
     }
@@ -564,7 +568,7 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
     }
     __syncthreads();
     if (!is_last) return;
-    merge_splits_parallel<D, G, NW>(a, unit, b, h, n_splits, lds_o, lds_m, lds_l);
+    merge_splits_parallel<D, G, NW, G>(a, unit, b, h, n_splits, 0, lds_o, lds_m, lds_l);
 }
 
 // Waves per split work-group: 8 for every group size (at most 150 registers per lane with the
@@ -572,18 +576,22 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
 // flight of a 4-wave work-group: ragged batches finish their long sequences sooner, and a long
 // context is cut into half as many splits.
 
+// The merge launch: one work-group per (sequence, kv head, query head of the group), each reading
+// one head's share of the partials (G times the work-groups of a per-(sequence, kv head) grid, each
+// with 1/G of the loads and LDS).
 template <int D, int G, int NW>
 __global__ __launch_bounds__(NW * 64) void decode_combine_kernel(DecodeArgs a) {
-    const int unit = blockIdx.x;
+    const int unit = blockIdx.x / G;
+    const int g = blockIdx.x - unit * G;
     const int b = unit / a.n_kv_heads;
     const int h = unit - b * a.n_kv_heads;
     const int L = clamp_len(a.lens[b], a.l_max);
     const int n_splits = decode_split_count(L, a.chunk);
     if (n_splits <= 1) return;  // written directly by the split kernel
-    __shared__ float lds_o[NW][G][D];
-    __shared__ float lds_m[NW][G];
-    __shared__ float lds_l[NW][G];
-    merge_splits_parallel<D, G, NW>(a, unit, b, h, n_splits, lds_o, lds_m, lds_l);
+    __shared__ float lds_o[NW][1][D];
+    __shared__ float lds_m[NW][1];
+    __shared__ float lds_l[NW][1];
+    merge_splits_parallel<D, G, NW, 1>(a, unit, b, h, n_splits, g, lds_o, lds_m, lds_l);
 }
 
 template <int D, int G, int NW>
@@ -608,7 +616,7 @@ hipError_t launch_decode_t(const DecodeArgs& a, const Launch& l) {
 
 template <int D, int G>
 hipError_t launch_combine_t(const DecodeArgs& a, const Launch& l) {
-    const dim3 grid(a.batch * a.n_kv_heads);
+    const dim3 grid(a.batch * a.n_kv_heads * G);
     if (a.waves == kDecodeWavesSmall)
         return launch_kernel(decode_combine_kernel<D, G, kDecodeWavesSmall>, grid, dim3(kDecodeWavesSmall * 64), l, a);
     if (a.waves == kDecodeWaves)
