@@ -66,8 +66,9 @@ extern "C" {
 #define GQA_OPT_DECODE_CHUNK 1 /* keys per split-KV work-group (a multiple of 64 giving at most max(l_cap / 256,
                                   the automatic plan's) splits; a last split of <= chunk/4 keys joins the one
                                   before it; 0 = auto: about 8 waves per CU, whole 16-key rounds per wave).
-                                  Work-groups have 8 waves, or 4 when the 8-wave plan has at most 8
-                                  work-groups (the automatic chunk is then planned for 4 waves) */
+                                  The automatic plan does not split a (sequence, kv head) whose K/V take
+                                  at most 128 KiB.  Work-groups have 8 waves, or 4 when the 8-wave plan
+                                  has at most 8 work-groups (the automatic chunk is then planned for 4) */
 #define GQA_OPT_PROFILE      2 /* 1 = time every kernel launch with a HIP event pair bound to the launch
                                   (hipExtLaunchKernel; restarts the record).  Binding adds no GPU work
                                   between launches, but each timed launch costs the host several us,

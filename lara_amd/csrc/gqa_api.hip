@@ -183,8 +183,15 @@ int plan_splits(int batch, int n_kv_heads, int n_cu, int waves) {
 // of a work-group (128 keys with 8 waves) so the waves of a split share its keys evenly -- rounded
 // down when that still gives at most plan_splits splits (a short tail joins the last split), else
 // up.  decode_split_count(max_len, chunk) <= plan_splits either way.
-int plan_chunk(int batch, int n_kv_heads, int group, int n_cu, int max_len, int waves) {
+// A (sequence, kv head) whose K/V take at most this many bytes is not split: one work-group streams
+// it in about a microsecond, less than merging splits costs (8 q / 2 kv heads, D 64, 256 keys = 64 KiB
+// per unit: 4.2 us of kernel in one split per unit against 4.8 us in four splits merged in-launch).
+constexpr int64_t kDecodeSplitMinBytes = 128 << 10;
+
+int plan_chunk(int batch, int n_kv_heads, int group, int n_cu, int max_len, int waves, int head_dim) {
     const int quantum = waves * decode_round_keys(group);
+    if ((int64_t)max_len * head_dim * 2 * 2 <= kDecodeSplitMinBytes)
+        return std::max(quantum, (max_len + quantum - 1) / quantum * quantum);
     const int splits = plan_splits(batch, n_kv_heads, n_cu, waves);
     const int even = (max_len + splits - 1) / splits;
     const int down = std::max(quantum, even / quantum * quantum);
@@ -223,10 +230,12 @@ struct DecodeShape {
     int waves;
 };
 
-DecodeShape plan_decode_shape(int batch, int n_kv_heads, int group, int n_cu, int max_len, int chunk_opt) {
+DecodeShape plan_decode_shape(int batch, int n_kv_heads, int group, int head_dim, int n_cu, int max_len,
+                              int chunk_opt) {
     const int64_t units = (int64_t)batch * n_kv_heads;
     auto shape = [&](int waves) {
-        const int chunk = chunk_opt > 0 ? chunk_opt : plan_chunk(batch, n_kv_heads, group, n_cu, max_len, waves);
+        const int chunk =
+            chunk_opt > 0 ? chunk_opt : plan_chunk(batch, n_kv_heads, group, n_cu, max_len, waves, head_dim);
         return DecodeShape{chunk, decode_split_count(max_len, chunk), waves};
     };
     const DecodeShape big = shape(kDecodeWaves);
@@ -279,7 +288,8 @@ int profile_enable(gqa_ctx* c, int on) {
 int plan_decode(gqa_ctx* c, const void* q, const int32_t* lens, const void* k_new, const void* v_new,
                 const int32_t* positions, void* o, float* lse, int max_len, DecodeArgs* out, bool* combine) {
     if (!decode_supported(c->cfg.head_dim, c->group) || c->numerics != GQA_NUMERICS_EXACT) return GQA_ERR_UNSUPPORTED;
-    const DecodeShape shape = plan_decode_shape(c->cfg.batch, c->cfg.n_kv_heads, c->group, c->n_cu, max_len, c->chunk_opt);
+    const DecodeShape shape = plan_decode_shape(c->cfg.batch, c->cfg.n_kv_heads, c->group, c->cfg.head_dim, c->n_cu,
+                                                max_len, c->chunk_opt);
     const int chunk = shape.chunk;
     const int max_splits = shape.max_splits;
     if (max_splits > c->max_splits_cap) return GQA_ERR_RANGE;
@@ -1393,7 +1403,7 @@ int gqa_decode_append_noalloc(const gqa_config* cfg, void* k_cache, void* v_cach
     if (rc != GQA_OK) return rc;
     // The plan gqa_decode_append_device makes for the same configuration (keys per split from the
     // CU count and max_seq_len), so both entry points give the same words.
-    const DecodeShape shape = plan_decode_shape(k.batch, k.n_kv_heads, group, dev->n_cu, k.max_seq_len, 0);
+    const DecodeShape shape = plan_decode_shape(k.batch, k.n_kv_heads, group, k.head_dim, dev->n_cu, k.max_seq_len, 0);
     const int chunk = shape.chunk;
     const int max_splits = shape.max_splits;
     const size_t rows = (size_t)k.batch * k.n_kv_heads * max_splits * group;  // partial rows of the plan
