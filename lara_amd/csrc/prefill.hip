@@ -211,9 +211,15 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
     constexpr int KSTEPS = D / 16;               // QK k-steps
     constexpr int MT = D / 32;                   // PV result tiles (32 dims each)
     constexpr int TILE = kBN * NCH;              // 16-byte chunks per K (or V) tile
-    constexpr int DMA = TILE / (kWaves * 64);    // direct-to-LDS loads per thread per tile
+    // Waves 4-7 alone issue the ring's K/V loads.  The issue of a block's 32 KiB stalls its waves
+    // for about 500 cycles (the load path's address rate), in which waves 0-3, on the same SIMDs,
+    // compute their scores; waves 4-7 then start theirs after, so the two waves of a SIMD are out
+    // of phase (MFMA beside softmax) instead of in lockstep.
+    constexpr int kLoaders = 4;                  // waves 4 .. 4 + kLoaders - 1
+    constexpr int DMA = TILE / (kLoaders * 64);  // direct-to-LDS loads per loading thread per tile
     constexpr int LPB = 2 * DMA;                 // per block (K and V)
-    static_assert(DMA >= 1 && DMA * kWaves * 64 == TILE, "tile shape");
+    static_assert(DMA >= 1 && DMA * kLoaders * 64 == TILE, "tile shape");
+    static_assert(kWaves == 8, "waves 4-7 load the ring");
 
     constexpr int NST = PAIR ? 4 : kStages;  // ring stages (PAIR: two blocks computed, two in flight)
     __shared__ __attribute__((aligned(16))) u32x4 lds_k[NST][TILE];
@@ -322,18 +328,19 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
     const u32x4* vn = has_new ? reinterpret_cast<const u32x4*>(a.v_new) + (size_t)h * a.n_new * NCH : nullptr;
     const u32x4* zero = reinterpret_cast<const u32x4*>(a.zero_row);
 
-    // Direct-to-LDS staging of block j0 into ring stage ST: wave-instruction i of wave w fills
-    // the 64 consecutive 16-byte slots (i*kWaves + w)*64 .., lane L slot +L; each lane loads the
-    // chunk the swizzled layout wants in its slot.  The slot -> (key, chunk) map is per lane and
+    // Direct-to-LDS staging of block j0 into ring stage ST: wave-instruction i of loading wave w
+    // (ld = w - 4) fills the 64 consecutive 16-byte slots (i*kLoaders + ld)*64 .., lane L slot +L;
+    // each lane loads the chunk the swizzled layout wants in its slot.  Waves 0-3 issue nothing.  The slot -> (key, chunk) map is per lane and
     // fixed, so a block whose 64 rows are consecutive cache rows (every block but those past
     // kv_len, those holding rows this launch appends and unmapped pages) takes a wave-uniform
     // base in SGPRs and these fixed per-lane byte offsets (koff, voff): no per-block address
     // arithmetic.  The other blocks pick each lane's source (zero row, k_new/v_new, cache).
+    const int ld = wave & 3;  // loading wave index (waves 4-7)
     int sl_key[DMA], sl_ck[DMA], sl_cv[DMA];
     uint32_t koff[DMA], voff[DMA];
 #pragma unroll
     for (int i = 0; i < DMA; ++i) {
-        const int slot = (i * kWaves + wave) * 64 + lane;
+        const int slot = (i * kLoaders + ld) * 64 + lane;
         sl_key[i] = slot / NCH;
         sl_ck[i] = (slot % NCH) ^ k_swz<NCH>(sl_key[i]);
         sl_cv[i] = (slot % NCH) ^ v_swz<D>(sl_key[i]);
@@ -342,6 +349,7 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
     }
     auto issue = [&](int j0, auto st_c) __attribute__((always_inline)) {
         constexpr int ST = decltype(st_c)::value;
+        if (wave < 4) return;
         const bool special = (j0 + kBN > a.kv_len) ||
                              (has_new && j0 + kBN > a.new_begin && j0 < a.new_begin + a.n_new);
         // Row j0's first word; a paged block (j0 and the page size are multiples of 64) lies in
@@ -360,7 +368,7 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
             const uint64_t vbase = uniform_address(vb0);
 #pragma unroll
             for (int i = 0; i < DMA; ++i) {
-                const int base = (i * kWaves + wave) * 64;
+                const int base = (i * kLoaders + ld) * 64;
                 dma16_sbase(kbase, koff[i], lds_addr(&lds_k[ST][base]));
                 dma16_sbase(vbase, voff[i], lds_addr(&lds_v[ST][base]));
             }
@@ -382,7 +390,7 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
                 sk = kb0 + (size_t)sl_key[i] * NCH + sl_ck[i];
                 sv = vb0 + (size_t)sl_key[i] * NCH + sl_cv[i];
             }
-            const int base = (i * kWaves + wave) * 64;
+            const int base = (i * kLoaders + ld) * 64;
             dma16(sk, lds_addr(&lds_k[ST][base]));
             dma16(sv, lds_addr(&lds_v[ST][base]));
         }
