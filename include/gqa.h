@@ -103,9 +103,11 @@ extern "C" {
  * finish merges the others' partials inside the decode launch (agent-scope atomics and a per-unit
  * arrival counter; one launch per step).  LAUNCH: a second, log-sum-exp merge launch.  AUTO (default):
  * FUSED while the split grid (sequences x kv heads x splits) is at most half the GPU's CU count and a
- * sequence has at most 8 splits -- every split ends with an L2 write-back of its XCD and an increment
+ * sequence has at most 16 splits -- every split ends with an L2 write-back of its XCD and an increment
  * of its sequence's counter, which saves the launch for short steps but slows the streaming of larger
- * grids more than a launch costs -- else LAUNCH.  Both fold the splits in the same order (the same output words). */
+ * grids more than a launch costs -- else LAUNCH.  An automatic plan of the shortest splits (one round
+ * of every wave) that would need the merge launch takes splits twice as long where that lets AUTO fuse.
+ * Both fold the splits in the same order (the same output words). */
 #define GQA_DECODE_MERGE_AUTO   0
 #define GQA_DECODE_MERGE_LAUNCH 1
 #define GQA_DECODE_MERGE_FUSED  2

@@ -205,10 +205,11 @@ int plan_chunk(int batch, int n_kv_heads, int group, int n_cu, int max_len, int 
 // merge launch where the step is a short latency chain, but the L2 maintenance of many work-groups
 // slows the streaming of the others.  AUTO fuses up to kFusedMergeSplits splits per sequence while
 // the split grid fills at most half the CUs (measured, kernel time per step, fused vs launch: 4
-// work-groups (2 splits of 128 keys) 5.1 vs 8.1 us, 64 work-groups (8 splits of 512) 9.4 vs 11.7 us;
+// work-groups (2 splits of 128 keys) 5.1 vs 8.1 us, 64 work-groups (8 splits of 512) 9.4 vs 11.7 us,
+// 32 q / 8 kv heads, one sequence of 2049 keys: 128 work-groups (16 splits of 128) 7.5 vs 8.6 us;
 // 256 work-groups: 8 splits of 16384 keys 314.1 vs 311.5 us, 4 of 8192 161 vs 160 us, 2 of 4096
-// 83-86 vs 81-82 us, 2 of 512 16.7 vs 16.1 us; 32 splits of 128 keys 10.3 vs 9.3 us).
-constexpr int kFusedMergeSplits = 8;
+// 83-86 vs 81-82 us, 2 of 512 16.7 vs 16.1 us; 32 splits of 128 keys 9.4 vs 8.8 us).
+constexpr int kFusedMergeSplits = 16;
 
 bool fuse_merge(int option, int units, int max_splits, int n_cu) {
     if (max_splits <= 1 || option == GQA_DECODE_MERGE_LAUNCH) return false;
@@ -222,6 +223,11 @@ bool fuse_merge(int option, int units, int max_splits, int n_cu) {
 // planned with kDecodeWavesSmall waves per work-group, which start and merge sooner (measured,
 // 8 q / 2 kv heads, D 64, 256 keys: 4.87 vs 5.04 us of kernel; at 256 work-groups and more the
 // 8-wave shape streams faster).  chunk_opt > 0 forces the keys per split.
+// Under GQA_DECODE_MERGE_AUTO, a plan of the shortest splits (one round of every wave) whose merge
+// would be a launch takes splits twice as long when that lets the merge fuse: the step loses a
+// launch's latency for a round per split (measured, 32 q / 8 kv heads: one sequence of 4097 keys,
+// 16 fused splits of 256 keys 8.27 us of kernel against 32 of 128 merged by a launch 8.66-8.80; two
+// of 2049 keys, 8 fused splits of 256 8.50 against 16 of 128 and a launch 9.00).
 constexpr int64_t kSmallDecodeGrid = 8;
 
 struct DecodeShape {
@@ -231,7 +237,7 @@ struct DecodeShape {
 };
 
 DecodeShape plan_decode_shape(int batch, int n_kv_heads, int group, int head_dim, int n_cu, int max_len,
-                              int chunk_opt) {
+                              int chunk_opt, int merge_option) {
     const int64_t units = (int64_t)batch * n_kv_heads;
     auto shape = [&](int waves) {
         const int chunk =
@@ -239,8 +245,15 @@ DecodeShape plan_decode_shape(int batch, int n_kv_heads, int group, int head_dim
         return DecodeShape{chunk, decode_split_count(max_len, chunk), waves};
     };
     const DecodeShape big = shape(kDecodeWaves);
-    if (units * big.max_splits > kSmallDecodeGrid) return big;
-    return shape(kDecodeWavesSmall);
+    if (units * big.max_splits <= kSmallDecodeGrid) return shape(kDecodeWavesSmall);
+    if (chunk_opt <= 0 && merge_option == GQA_DECODE_MERGE_AUTO && big.max_splits > 1 &&
+        big.chunk == kDecodeWaves * decode_round_keys(group) &&
+        !fuse_merge(merge_option, (int)units, big.max_splits, n_cu)) {
+        const int chunk = 2 * big.chunk;
+        const DecodeShape twice{chunk, decode_split_count(max_len, chunk), kDecodeWaves};
+        if (fuse_merge(merge_option, (int)units, twice.max_splits, n_cu)) return twice;
+    }
+    return big;
 }
 
 constexpr int kProfileLaunches = 512;  // event pairs kept per timer slot
@@ -289,7 +302,7 @@ int plan_decode(gqa_ctx* c, const void* q, const int32_t* lens, const void* k_ne
                 const int32_t* positions, void* o, float* lse, int max_len, DecodeArgs* out, bool* combine) {
     if (!decode_supported(c->cfg.head_dim, c->group) || c->numerics != GQA_NUMERICS_EXACT) return GQA_ERR_UNSUPPORTED;
     const DecodeShape shape = plan_decode_shape(c->cfg.batch, c->cfg.n_kv_heads, c->group, c->cfg.head_dim, c->n_cu,
-                                                max_len, c->chunk_opt);
+                                                max_len, c->chunk_opt, c->decode_merge);
     const int chunk = shape.chunk;
     const int max_splits = shape.max_splits;
     if (max_splits > c->max_splits_cap) return GQA_ERR_RANGE;
@@ -1403,7 +1416,8 @@ int gqa_decode_append_noalloc(const gqa_config* cfg, void* k_cache, void* v_cach
     if (rc != GQA_OK) return rc;
     // The plan gqa_decode_append_device makes for the same configuration (keys per split from the
     // CU count and max_seq_len), so both entry points give the same words.
-    const DecodeShape shape = plan_decode_shape(k.batch, k.n_kv_heads, group, k.head_dim, dev->n_cu, k.max_seq_len, 0);
+    const DecodeShape shape =
+        plan_decode_shape(k.batch, k.n_kv_heads, group, k.head_dim, dev->n_cu, k.max_seq_len, 0, GQA_DECODE_MERGE_AUTO);
     const int chunk = shape.chunk;
     const int max_splits = shape.max_splits;
     const size_t rows = (size_t)k.batch * k.n_kv_heads * max_splits * group;  // partial rows of the plan

@@ -200,7 +200,6 @@ __host__ __device__ inline int decode_split_count(int L, int chunk) {
 bool decode_supported(int head_dim, int group);
 // Keys a wave of the decode kernel takes per round (a divisor of 64) for a group size.
 int decode_round_keys(int group);
-// Waves per split work-group of the decode kernel for a group size.
 
 // Split-KV attention with an optional fused row append; sequences longer than one split
 // leave fp32 partials that launch_combine merges.
