@@ -5,6 +5,8 @@ sequence) the max abs error against the float64 oracle is <= 2 bf16 ulp of the r
 largest |output| ("2 bf16 ulp of output magnitude"); the softmax sum l, recovered from
 the returned log-sum-exp, is within rtol 1e-2; K/V append and read-back are bit-exact.
 """
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -316,3 +318,43 @@ def test_decode_cancelling_v_rows_within_the_weight_rounding_bound():
     assert float(err.max()) <= 1.0
     rel = np.abs(np.expm1(lse.astype(np.float64) - ref_lse))
     assert float(rel.max()) <= L_RTOL
+
+
+def _merge_launches(eng):
+    counts = (ctypes.c_int32 * _lib.GQA_TIMER_COUNT)()
+    _lib.check(eng._lib.gqa_kernel_launch_counts(eng._ctx, counts, _lib.GQA_TIMER_COUNT), "counts")
+    return int(counts[_lib.GQA_TIMER_COMBINE]), int(counts[_lib.GQA_TIMER_DECODE])
+
+
+@pytest.mark.parametrize("B,hq,hkv,d,L,twice", [(1, 32, 8, 128, 4097, True), (2, 32, 8, 128, 2049, True),
+                                                (4, 32, 8, 128, 1025, True), (8, 32, 8, 128, 513, True),
+                                                (1, 32, 8, 128, 2049, False), (1, 8, 2, 64, 2049, False)])
+def test_decode_auto_plan_merges_small_grids_in_launch(B, hq, hkv, d, L, twice):
+    """Small split grids under GQA_DECODE_MERGE_AUTO on 256 CUs: up to 16 splits within half the CUs
+    merge inside the decode launch, and a plan of the shortest splits (128 keys) that would need the
+    merge launch takes 256-key splits instead ("twice"), equal word for word to those splits merged by
+    the merge launch.  Every step is checked against the oracle."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(700 + B * 10 + d + L)
+    lens = np.full(B, L, np.int32)
+    lens[-1] = L - 37 if B > 1 else L  # one shorter sequence: its split count differs
+    n_cu = torch.cuda.get_device_properties(0).multi_processor_count
+    with make_engine(B, hq, hkv, d, L) as auto, make_engine(B, hq, hkv, d, L) as ref:
+        kc, vc = fill_cache(auto, rng, B, hkv, d, lens, lcap=L)
+        for b in range(B):
+            ref.load_kv(kc[b, :, :lens[b]], vc[b, :, :lens[b]], b=b)
+        _lib.check(ref._lib.gqa_set_option(ref._ctx, _lib.GQA_OPT_DECODE_MERGE, _lib.GQA_DECODE_MERGE_LAUNCH), "m")
+        _lib.check(ref._lib.gqa_set_option(ref._ctx, _lib.GQA_OPT_DECODE_CHUNK, 256), "chunk")
+        _lib.check(auto._lib.gqa_set_option(auto._ctx, _lib.GQA_OPT_PROFILE, 1), "profile")
+        for step in range(2):
+            q = bf16_normal(rng, (B, hq, d))
+            out_a, lse_a = auto.decode_step(q, lens, return_lse=True)
+            check_decode(out_a, lse_a, q, kc, vc, lens, None)
+            if twice and n_cu == 256:
+                out_r, lse_r = ref.decode_step(q, lens, return_lse=True)
+                assert np.array_equal(out_a, out_r), f"step {step}"
+                assert np.array_equal(lse_a.view(np.uint32), lse_r.view(np.uint32))
+        merges, decodes = _merge_launches(auto)
+        assert decodes == 2
+        if n_cu == 256:
+            assert merges == 0, "the automatic plan took the merge launch"
