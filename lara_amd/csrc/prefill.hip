@@ -330,7 +330,8 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
 
     // Direct-to-LDS staging of block j0 into ring stage ST: wave-instruction i of loading wave w
     // (ld = w - 4) fills the 64 consecutive 16-byte slots (i*kLoaders + ld)*64 .., lane L slot +L;
-    // each lane loads the chunk the swizzled layout wants in its slot.  Waves 0-3 issue nothing.  The slot -> (key, chunk) map is per lane and
+    // each lane loads the chunk the swizzled layout wants in its slot.  Waves 0-3 issue nothing.
+    // The slot -> (key, chunk) map is per lane and
     // fixed, so a block whose 64 rows are consecutive cache rows (every block but those past
     // kv_len, those holding rows this launch appends and unmapped pages) takes a wave-uniform
     // base in SGPRs and these fixed per-lane byte offsets (koff, voff): no per-block address
@@ -648,12 +649,12 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
     auto block = [&](int blk, auto st_c) __attribute__((always_inline)) {
         constexpr int ST = decltype(st_c)::value;
         const int j0 = seg_begin + blk * kBN;
-        // This thread's loads of block blk are done once at most the next block's remain
-        // (blocks 0 and 1 were retired before the loop).
+        // A loading wave's loads of block blk are done once at most the next block's remain (blocks 0
+        // and 1 were retired before the loop; waves 0-3 have none in flight).
         if (blk >= 1) {
             if (blk + 1 < n_blocks) wait_vmcnt<LPB>(); else wait_vmcnt<0>();
         }
-        stage_barrier();  // every wave's block blk landed; block blk-1's stage is free
+        stage_barrier();  // block blk landed in every slot; block blk-1's stage is free
         if (blk + 2 < n_blocks) issue(j0 + 2 * kBN, std::integral_constant<int, (ST + 2) % NST>{});
         if (j0 >= wave_hi) return;  // this wave's rows see no key of the block
         compute(j0, st_c);
