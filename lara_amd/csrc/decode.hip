@@ -131,6 +131,18 @@ __device__ __forceinline__ int length_bucket(const DecodeArgs& a, int s) {
     return (int)(((int64_t)L * kBuckets) / ((int64_t)a.l_max + 1));
 }
 
+// Whether the batch's attended lengths differ (every lane of the wave gets the same answer).
+__device__ bool batch_is_ragged(const DecodeArgs& a) {
+    const int lane = threadIdx.x & 63;
+    int lo = INT_MAX, hi = -1;
+    for (int s = lane; s < a.batch; s += 64) {
+        const int L = clamp_len(a.lens[s], a.l_max);
+        lo = L < lo ? L : lo;
+        hi = L > hi ? L : hi;
+    }
+    return __reduce_min_sync(~0ull, lo) != __reduce_max_sync(~0ull, hi);
+}
+
 __device__ int rank_to_sequence(const DecodeArgs& a, int rank) {
     const int lane = threadIdx.x & 63;
     if (a.batch <= 64) {
@@ -300,9 +312,29 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
     static_assert(NLD >= 1 && G <= 16, "16-key rounds, up to 16 heads per group");
 
     const int split = blockIdx.x;
-    const int h = blockIdx.y % a.n_kv_heads;
-    int b = blockIdx.y / a.n_kv_heads;
-    if (a.longest_first) b = rank_to_sequence(a, b);
+    int row = blockIdx.y;  // (rank of the sequence) * H_kv + kv head
+    // Equal lengths keep index order (rank_to_sequence would return the rank): then no ticket and no
+    // ranking.  Every wave of every work-group reaches the same answer from the same lengths.
+    const bool ranked = a.longest_first && batch_is_ragged(a);
+    if (a.ticket != nullptr && ranked) {
+        // One split per row: the work-group takes the next row in longest-first order as it starts,
+        // and the one that takes the last row resets the counter for the next launch (every
+        // work-group takes exactly one ticket, so no increment follows).  Rows are tickets modulo
+        // the row count: any run of that many tickets names every row once, so a row is in range
+        // whatever the counter held.
+        __shared__ int s_row;
+        if (threadIdx.x == 0) {
+            const unsigned rows = gridDim.y;
+            const unsigned t = (unsigned)__hip_atomic_fetch_add(a.ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (t % rows == rows - 1) __hip_atomic_store(a.ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s_row = (int)(t % rows);
+        }
+        __syncthreads();
+        row = s_row;
+    }
+    const int h = row % a.n_kv_heads;
+    int b = row / a.n_kv_heads;
+    if (ranked) b = rank_to_sequence(a, b);
     const int unit = b * a.n_kv_heads + h;
     const int H_q = a.n_kv_heads * G;
     const int L = clamp_len(a.lens[b], a.l_max);

@@ -66,7 +66,8 @@ struct gqa_ctx {
     int n_layers = 1, layer = 0;
     float* part_o = nullptr;
     float* part_ml = nullptr;
-    int32_t* arrivals = nullptr;  // [B*H_kv] split arrival counters of the fused merge (zero between launches)
+    int32_t* arrivals = nullptr;  // [B*H_kv] split arrival counters of the fused merge, then the row ticket
+                                  // of one-split launches (all zero between launches)
     int decode_merge = GQA_DECODE_MERGE_AUTO;
     int prefill_kernel = GQA_PREFILL_KERNEL_AUTO;
     float* pre_ws = nullptr;     // prefill KV-segment partials (O, then (m, l))
@@ -336,6 +337,7 @@ int plan_decode(gqa_ctx* c, const void* q, const int32_t* lens, const void* k_ne
     a.arrivals = fuse_merge(c->decode_merge, c->cfg.batch * c->cfg.n_kv_heads, max_splits, c->n_cu) ? c->arrivals
                                                                                                       : nullptr;
     *combine = max_splits > 1 && a.arrivals == nullptr;
+    a.ticket = (c->cfg.batch > 1 && max_splits == 1) ? c->arrivals + (size_t)c->cfg.batch * c->cfg.n_kv_heads : nullptr;
     return GQA_OK;
 }
 
@@ -819,7 +821,7 @@ int create_ctx(const gqa_config* cfg, int32_t page_size, int32_t n_pages, int32_
     c->v_cache = c->v_pool;
     alloc((void**)&c->part_o, units * c->max_splits_cap * group * D * sizeof(float));
     alloc((void**)&c->part_ml, units * c->max_splits_cap * group * 2 * sizeof(float));
-    alloc((void**)&c->arrivals, units * sizeof(int32_t));
+    alloc((void**)&c->arrivals, (units + 1) * sizeof(int32_t));
     if (prefill_supported(k.head_dim, group)) {
         c->pre_ws_floats = prefill_workspace_need(c, c->n_cu);
         if (c->pre_ws_floats > 0) alloc((void**)&c->pre_ws, c->pre_ws_floats * sizeof(float));
@@ -845,7 +847,7 @@ int create_ctx(const gqa_config* cfg, int32_t page_size, int32_t n_pages, int32_
     }
     // Zero the caches (every layer's pool) once so rows beyond every sequence's length hold finite words.
     if (rc == GQA_OK && (hipMemsetAsync(c->zero_row, 0, D * 2, c->stream) != hipSuccess ||
-                         hipMemsetAsync(c->arrivals, 0, units * sizeof(int32_t), c->stream) != hipSuccess ||
+                         hipMemsetAsync(c->arrivals, 0, (units + 1) * sizeof(int32_t), c->stream) != hipSuccess ||
                          hipMemsetAsync(c->k_pool, 0, kv_words(c) * 2 * (size_t)n_layers, c->stream) != hipSuccess ||
                          hipMemsetAsync(c->v_pool, 0, kv_words(c) * 2 * (size_t)n_layers, c->stream) != hipSuccess ||
                          (c->paged && hipMemsetAsync(c->table_dev, 0xFF, (size_t)k.batch * c->max_pages * 4,

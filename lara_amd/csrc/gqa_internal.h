@@ -84,6 +84,11 @@ struct DecodeArgs {
     // [B*H_kv] split arrival counters, zero between launches: the last split of a (sequence, kv
     // head) to finish merges the partials itself (no merge launch); nullptr = decode_combine_kernel.
     int32_t* arrivals;
+    // One split per (sequence, kv head) and several sequences: a counter, zero between launches,
+    // from which each work-group takes its grid row as it starts (rows in longest-first order), so
+    // the rows left for the second dispatch round go to the work-groups that start first, on
+    // whichever XCDs stream fastest; nullptr = row blockIdx.y.
+    int32_t* ticket;
     // Nonzero: K/V rows are read with plain (L2-allocating) loads instead of nontemporal ones
     // (decode_cached_loads).
     int32_t cached;
