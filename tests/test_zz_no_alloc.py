@@ -104,6 +104,20 @@ def test_noalloc_decode_matches_context_entry_point_twice():
     _case(lib, torch, rng, 2, 64, 8, 128, 700, np.array([700, 129], np.int32))
 
 
+def test_noalloc_matches_context_on_a_ragged_one_split_batch():
+    """32 sequences x 8 kv heads fill the GPU with one split each: the context entry point then takes
+    its grid rows from a ticket counter (ragged lengths), the no-alloc entry point in index order; the
+    words must not depend on which work-group ran which (sequence, kv head)."""
+    torch = pytest.importorskip("torch")
+    if not torch.cuda.is_available():
+        pytest.skip("needs a GPU")
+    lib = _lib.lib()
+    rng = np.random.default_rng(4343)
+    lens = rng.integers(1, 601, 32).astype(np.int32)
+    lens[0] = 600
+    _case(lib, torch, rng, 32, 32, 8, 128, 600, lens)
+
+
 def test_noalloc_rejects_bad_arguments():
     torch = pytest.importorskip("torch")
     if not torch.cuda.is_available():
