@@ -149,6 +149,33 @@ def test_decode_longest_first_order_is_invisible(B):
     assert np.array_equal(lse_p, lse[perm])
 
 
+def test_decode_ragged_rows_by_ticket_over_repeated_steps():
+    """A ragged batch of one split per (sequence, kv head) takes its rows from a counter that the
+    launch's last taker resets: repeated steps, with steps of an equal-length batch (rows in grid
+    order, counter untouched) between them, give the same words every time, and the oracle's."""
+    rng = np.random.default_rng(611)
+    B, hq, hkv, d = 64, 32, 8, 128
+    lens = rng.integers(1, 600, size=B).astype(np.int32)
+    lens[[3, 40]] = 600
+    lens[7] = 0
+    with make_engine(B, hq, hkv, d, 640) as eng:
+        kc, vc = fill_cache(eng, rng, B, hkv, d, lens, lcap=640)
+        q = bf16_normal(rng, (B, hq, d))
+        out0, lse0 = eng.decode_step(q, lens, return_lse=True)
+        check_decode(out0, lse0, q, kc, vc, lens, None)
+        even = np.full(B, 500, np.int32)
+        even_out = None
+        for step in range(4):
+            out, lse = eng.decode_step(q, lens, return_lse=True)
+            assert np.array_equal(out, out0), f"ragged step {step}"
+            assert np.array_equal(lse.view(np.uint32), lse0.view(np.uint32))
+            out_e = eng.decode_step(q, even)
+            if even_out is None:
+                even_out = out_e
+                check_decode(out_e, None, q, kc, vc, even, None)
+            assert np.array_equal(out_e, even_out), f"equal-length step {step}"
+
+
 def test_decode_split_invariance():
     rng = np.random.default_rng(103)
     B, hq, hkv, d = 2, 32, 8, 128
