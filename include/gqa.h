@@ -334,7 +334,12 @@ int gqa_decode_append_noalloc(const gqa_config* cfg, void* k_cache, void* v_cach
  * gqa_layer_qkv_device does the same from device memory without a transaction: Q goes to
  * q_out ([H_q][n_tokens][D], 16-byte aligned, else GQA_ERR_RANGE), K/V to rows
  * [kv_row0, kv_row0 + n_tokens) of sequence b; it
- * allocates its workspace on first use.  gqa_layer_times returns the device time in us of
+ * allocates its workspace on first use.  The projection of a (token count, hidden) shape keeps
+ * hipBLASLt's up to 8 best-ranked algorithms; the first call of the shape outside a stream capture
+ * times them on the caller's operands (each run four times, the stream synchronised once per
+ * algorithm: a few ms, once) and later calls use the fastest, while calls under a capture use the
+ * best-ranked until such a call has run.  The context keeps the last 8 shapes.
+ * gqa_layer_times returns the device time in us of
  * the RMSNorm, projection and RoPE stages (n <= 3; synchronises) of the last gqa_submit_layer
  * call (GQA_ERR_NO_TRANSACTION when there is none); gqa_layer_qkv_device calls made while
  * GQA_OPT_PROFILE is on record their stages in the GQA_TIMER_NORM / _PROJECTION / _ROPE slots of
