@@ -317,11 +317,11 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
     // ranking.  Every wave of every work-group reaches the same answer from the same lengths.
     const bool ranked = a.longest_first && batch_is_ragged(a);
     if (a.ticket != nullptr && ranked) {
-        // One split per row: the work-group takes the next row in longest-first order as it starts,
-        // and the one that takes the last row resets the counter for the next launch (every
-        // work-group takes exactly one ticket, so no increment follows).  Rows are tickets modulo
-        // the row count: any run of that many tickets names every row once, so a row is in range
-        // whatever the counter held.
+        // One split per row: the work-group takes the next row in longest-first order as it starts.
+        // The counter is zero when a launch starts (cleared with the context, then reset by every
+        // launch): the launch's work-groups take one ticket each, 0 .. rows-1, and the one holding
+        // rows-1 made the last increment, so its store of zero races with none.  Taking the ticket
+        // modulo the row count keeps the row in range even if the counter held something else.
         __shared__ int s_row;
         if (threadIdx.x == 0) {
             const unsigned rows = gridDim.y;
