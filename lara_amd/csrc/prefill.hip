@@ -199,6 +199,37 @@ __device__ __forceinline__ int v_swz(int key) {
     return D == 128 ? 4 * (key & 3) : 4 * ((key >> 1) & 1);
 }
 
+// A wave's output block ([32 rows][D] bf16) goes to global memory through LDS: the lanes put their
+// O^T fragments (row `col`, dims mt*32 + 8*r4 + 4*half .. +3) into a stash of 16-byte chunks, chunk
+// c of row r at r*NCH + (c ^ (r % NCH)) (no bank conflicts either way), then store whole rows, 16
+// bytes per lane.  One store instruction then covers four 256-byte rows instead of 16 bytes of 32
+// rows, and the stores are nontemporal: the rows go to memory as they are written instead of sitting
+// dirty in L2 until the end-of-kernel write-back, which every work-group of a one-round launch would
+// otherwise reach at the same time.
+template <int D>
+__device__ __forceinline__ void stash_put(uint2* stash, int col, int half, int mt, int r4, uint2 w) {
+    constexpr int NCH = D / 8;
+    const int chunk = 4 * mt + r4;  // dims 8*chunk .. +7; this lane's four: + 4*half
+    stash[2 * (col * NCH + (chunk ^ (col & (NCH - 1)))) + half] = w;
+}
+
+// Stores rows row0 .. row0 + 31 (those below q_len) of the stash to out (row r at out + r*D).  The
+// stash was written by this wave; the wait orders its LDS writes before the reads.
+template <int D>
+__device__ __forceinline__ void stash_store_rows(const uint2* stash, uint16_t* out, int row0, int q_len, int lane) {
+    constexpr int NCH = D / 8;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    const uint4* s4 = reinterpret_cast<const uint4*>(stash);
+#pragma unroll
+    for (int it = 0; it < D / 16; ++it) {
+        const int qc = it * 64 + lane;  // chunk qc of the block: row r, chunk c
+        const int r = qc / NCH, c = qc % NCH;
+        if (row0 + r < q_len)
+            __builtin_nontemporal_store(__builtin_bit_cast(u32x4, s4[r * NCH + (c ^ (r & (NCH - 1)))]),
+                                        reinterpret_cast<u32x4*>(out + (size_t)(row0 + r) * D + 8 * c));
+    }
+}
+
 // V^T operand of one PV step (eight bf16: dims mt*32 + lane%32, keys kb + 4*half + 0..3 and
 // kb + 8 + 4*half + 0..3): ds_read_b64_tr_b16 hands lane i of each 16-lane group element (i % 4)
 // of the 8-byte piece that lane 4j + i/4 of the group addresses, for j = 0..3, so every lane
@@ -606,8 +637,7 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
                 uint2 w;
                 w.x = (uint32_t)f32_to_bf16_rne(o[mt][4 * r4 + 0] * inv) | ((uint32_t)f32_to_bf16_rne(o[mt][4 * r4 + 1] * inv) << 16);
                 w.y = (uint32_t)f32_to_bf16_rne(o[mt][4 * r4 + 2] * inv) | ((uint32_t)f32_to_bf16_rne(o[mt][4 * r4 + 3] * inv) << 16);
-                const int chunk = 4 * mt + r4;  // dims 8*chunk .. +7; this lane's four: + 4*half
-                stash[2 * (col * NCH + (chunk ^ (col & (NCH - 1)))) + half] = w;
+                stash_put<D>(stash, col, half, mt, r4, w);
             }
         cur_rb = rb;
         wave_hi = kv_limit(rb);
@@ -723,9 +753,12 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
             const float wa = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - M);
             const float wb = mlb.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mlb.x - M);
             const float l_sum = fmaf(l_row, wa, mlb.y * wb);
-            if (!row_ok) return;
+            // Every lane stages its row (rows past q_len too: the stores skip them), since the row
+            // stores below take each lane to other rows.
             const float inv = l_sum > 0.f ? 1.f / l_sum : 0.f;
-            uint16_t* orow = a.out + ((size_t)hq * a.q_len + row) * D;
+            // L's rows are staged in ring stage 3 (the partials and their (m, l) fill stages 0-2).
+            uint2* stash = reinterpret_cast<uint2*>(q4 < 2 ? &lds_k[NST - 1][0] : &lds_v[NST - 1][0]) +
+                           (q4 & 1) * (kRows * NCH * 2);
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -738,30 +771,24 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
                     uint2 w;
                     w.x = (uint32_t)f32_to_bf16_rne(v0) | ((uint32_t)f32_to_bf16_rne(v1) << 16);
                     w.y = (uint32_t)f32_to_bf16_rne(v2) | ((uint32_t)f32_to_bf16_rne(v3) << 16);
-                    *reinterpret_cast<uint2*>(orow + mt * 32 + 8 * r4 + 4 * half) = w;
+                    stash_put<D>(stash, col, half, mt, r4, w);
                 }
-            if (half == 0 && a.lse != nullptr)
+            stash_store_rows<D>(stash, a.out + (size_t)hq * a.q_len * D, rb * kRows, a.q_len, lane);
+            if (row_ok && half == 0 && a.lse != nullptr)
                 a.lse[(size_t)hq * a.q_len + row] = l_sum > 0.f ? (M + log2f(l_sum)) * kLn2 : -INFINITY;
         } else if (has_s) {
-            // S's output rows from the LDS stash, 16 bytes per lane and store.
-            const uint4* stash = reinterpret_cast<const uint4*>(&lds_q[q4][0][0]);
-#pragma unroll
-            for (int it = 0; it < KSTEPS; ++it) {
-                const int qc = it * 64 + lane;  // chunk qc of the [32][D] block: row r, chunk c
-                const int r = qc / NCH, c = qc % NCH;
-                const int srow = wx * kRows + r;
-                if (srow < a.q_len)
-                    *reinterpret_cast<uint4*>(a.out + ((size_t)hq * a.q_len + srow) * D + 8 * c) =
-                        stash[r * NCH + (c ^ (r & (NCH - 1)))];
-            }
+            // S's output rows from the stash leave_s filled.
+            stash_store_rows<D>(reinterpret_cast<const uint2*>(&lds_q[q4][0][0]), a.out + (size_t)hq * a.q_len * D,
+                                wx * kRows, a.q_len, lane);
             const int srow = wx * kRows + col;
             if (half == 0 && a.lse != nullptr && srow < a.q_len) a.lse[(size_t)hq * a.q_len + srow] = lse_s;
         }
         return;
     }
-    if (!row_ok) return;
+    if (!active) return;  // wave-uniform
     const float l_row = l_lane + half_swap(l_lane, half);
     if (a.n_segs > 1) {
+        if (!row_ok) return;
         // Rows this wave never reached in the segment are not read by the merge.
         if (seg_begin >= wave_hi) return;
         // The segment's unnormalised O in fp16, divided by the power of two 2^e just above the row's
@@ -790,8 +817,14 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
             *reinterpret_cast<float4*>(a.part_ml + prow * 4) = make_float4(m_run, l_row, (float)e, 0.f);
         return;
     }
+    // The rows are staged in the two ring stages no wave reads any more: block b sits in stage b % NST
+    // and only the last block's stage may still be read (every wave passed the last block's barrier
+    // after finishing the block before it, and no load is in flight after the last block's wait), so
+    // waves 0-3 take stage n_blocks % NST and waves 4-7 the next, two waves per K or V tile.  Every
+    // lane of the wave stages its row (rows past q_len too: the stores skip them).
+    const int f = (n_blocks + (wave >> 2)) % NST;
+    uint2* stash = reinterpret_cast<uint2*>((wave & 2) ? &lds_v[f][0] : &lds_k[f][0]) + (wave & 1) * (kRows * NCH * 2);
     const float inv = l_row > 0.f ? 1.f / l_row : 0.f;
-    uint16_t* orow = a.out + ((size_t)hq * a.q_len + row) * D;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -799,9 +832,10 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(PrefillArgs a) {
             uint2 w;
             w.x = (uint32_t)f32_to_bf16_rne(o[mt][4 * r4 + 0] * inv) | ((uint32_t)f32_to_bf16_rne(o[mt][4 * r4 + 1] * inv) << 16);
             w.y = (uint32_t)f32_to_bf16_rne(o[mt][4 * r4 + 2] * inv) | ((uint32_t)f32_to_bf16_rne(o[mt][4 * r4 + 3] * inv) << 16);
-            *reinterpret_cast<uint2*>(orow + mt * 32 + 8 * r4 + 4 * half) = w;
+            stash_put<D>(stash, col, half, mt, r4, w);
         }
-    if (half == 0 && a.lse != nullptr)
+    stash_store_rows<D>(stash, a.out + (size_t)hq * a.q_len * D, rb * kRows, a.q_len, lane);
+    if (row_ok && half == 0 && a.lse != nullptr)
         a.lse[(size_t)hq * a.q_len + row] = l_row > 0.f ? (m_run + log2f(l_row)) * kLn2 : -INFINITY;
 }
 
