@@ -202,10 +202,9 @@ __device__ __forceinline__ int v_swz(int key) {
 // A wave's output block ([32 rows][D] bf16) goes to global memory through LDS: the lanes put their
 // O^T fragments (row `col`, dims mt*32 + 8*r4 + 4*half .. +3) into a stash of 16-byte chunks, chunk
 // c of row r at r*NCH + (c ^ (r % NCH)) (no bank conflicts either way), then store whole rows, 16
-// bytes per lane.  One store instruction then covers four 256-byte rows instead of 16 bytes of 32
-// rows, and the stores are nontemporal: the rows go to memory as they are written instead of sitting
-// dirty in L2 until the end-of-kernel write-back, which every work-group of a one-round launch would
-// otherwise reach at the same time.
+// bytes per lane: one store instruction covers four 256-byte rows instead of 16 bytes of 32 rows.
+// Plain stores: nontemporal ones shortened these launches further but sent the rows past the
+// memory-side cache, so whatever reads the output next paid about as much again.
 template <int D>
 __device__ __forceinline__ void stash_put(uint2* stash, int col, int half, int mt, int r4, uint2 w) {
     constexpr int NCH = D / 8;
@@ -225,8 +224,7 @@ __device__ __forceinline__ void stash_store_rows(const uint2* stash, uint16_t* o
         const int qc = it * 64 + lane;  // chunk qc of the block: row r, chunk c
         const int r = qc / NCH, c = qc % NCH;
         if (row0 + r < q_len)
-            __builtin_nontemporal_store(__builtin_bit_cast(u32x4, s4[r * NCH + (c ^ (r & (NCH - 1)))]),
-                                        reinterpret_cast<u32x4*>(out + (size_t)(row0 + r) * D + 8 * c));
+            *reinterpret_cast<uint4*>(out + (size_t)(row0 + r) * D + 8 * c) = s4[r * NCH + (c ^ (r & (NCH - 1)))];
     }
 }
 
