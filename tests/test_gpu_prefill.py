@@ -148,6 +148,30 @@ def test_prefill_shapes_ragged(hq, hkv, d, causal, kernel):
     check_rows(out, lse, ref, ref_lse)
 
 
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (8, 8, 128), (16, 8, 128), (64, 8, 128), (64, 4, 128),
+                                      (8, 2, 64), (16, 16, 64), (32, 4, 64), (32, 2, 64)])
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_shared_one_segment_every_group(hq, hkv, d, causal):
+    """The GQA-shared kernel writing its rows itself (one KV segment: rows staged in the free ring
+    stages and stored whole) for every compiled (head_dim, group): ragged q_len (a partial last row
+    block), work-groups whose last waves have no task (group 1 and 2), position bases."""
+    rng = np.random.default_rng(hq * 11 + hkv * 5 + d + causal)
+    q_len, kv_len, qb, kb = 77, 333, 300, 40
+    print(f"[shared, one segment] hq={hq} hkv={hkv} d={d} causal={causal}", flush=True)
+    q = bf16_normal(rng, (hq, q_len, d))
+    k = bf16_normal(rng, (hkv, kv_len, d))
+    v = bf16_normal(rng, (hkv, kv_len, d))
+    with AttentionAccelerator(n_q_heads=hq, n_kv_heads=hkv, head_dim=d, max_seq_len=kv_len, max_q_len=q_len) as acc:
+        set_prefill_kernel(acc, "shared")
+        drv._lib.check(acc._lib.gqa_set_option(acc._ctx, drv._lib.GQA_OPT_PREFILL_WGS, 1), "wgs")
+        acc.load_kv(k, v)
+        out, lse = acc.prefill_chunk(q, q_pos_base=qb, kv_len=kv_len, kv_pos_base=kb, causal=causal,
+                                     return_lse=True)
+        assert acc.last_prefill_plan() == ("shared", 1)
+    ref, ref_lse = oracle_for(q, k, v, causal=causal, q_pos_base=qb, kv_pos_base=kb)
+    check_rows(out, lse, ref, ref_lse)
+
+
 @pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (16, 4, 64)])
 @pytest.mark.parametrize("q_len,kv_len,qb,kb", [(33, 33, 0, 0), (64, 64, 0, 0), (96, 96, 0, 0), (333, 333, 0, 0),
                                                 (200, 700, 500, 0), (257, 300, 43, 0), (160, 230, 100, 30),
