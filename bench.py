@@ -335,11 +335,11 @@ def residency(working_set: int, byte_rate: bool = True) -> dict:
     """Whether a workload's bytes fit the 256 MiB Infinity Cache: a step that does is served from it
     after warm-up, so a byte rate measured on it is not an HBM rate."""
     resident = working_set <= INFINITY_CACHE_BYTES
-    note = "cache-resident: the working set fits the 256 MiB Infinity Cache"
+    note = "fits the 256 MiB Infinity Cache"
     if resident and byte_rate:
-        note += ", so the GB/s figure is not an HBM rate (the step is latency-bound)"
+        note += ": GB/s is not an HBM rate (latency-bound)"
     return {"working_set_bytes": int(working_set), "cache_resident": resident,
-            "residency": note if resident else "HBM: the working set exceeds the 256 MiB Infinity Cache"}
+            "residency": note if resident else "HBM (exceeds the 256 MiB Infinity Cache)"}
 
 
 def measure(name: str, steps: int, warmup: int, chunk: int = 0, page_rows: int = PAGE_ROWS,
@@ -735,6 +735,22 @@ def _cpu_text(cpu) -> str:
     return " ".join(parts)
 
 
+def compact(obj, digits: int = 5):
+    """obj with every float rounded to `digits` significant digits (ints, strings and None unchanged),
+    so the one JSON line stays short enough for a log tail to hold all of it."""
+    if isinstance(obj, float):
+        if not math.isfinite(obj):
+            return obj
+        if obj.is_integer() and abs(obj) >= 10**digits:
+            return int(obj)  # byte counts keep every digit
+        return float(f"{obj:.{digits}g}")
+    if isinstance(obj, dict):
+        return {k: compact(v, digits) for k, v in obj.items()}
+    if isinstance(obj, (list, tuple)):
+        return [compact(v, digits) for v in obj]
+    return obj
+
+
 def summary_lines(main_name: str, main_r: dict, cpu, others: dict) -> list:
     """One short line per workload (GPU time per step, kernel time and rate, CPU baseline): the last
     lines the bench prints, so that a short tail of its output still holds every configuration."""
@@ -824,7 +840,8 @@ def read_ceiling(gib: int = 4, launches: int = 10) -> dict:
     log(f"read ceiling: {best['gbps']:.0f} GB/s ({best['unroll']} loads in flight per thread, "
         f"{best['work_groups']} work-groups)")
     return {"gbps": best["gbps"], "frac_of_spec": best["gbps"] / HBM_PEAK_GBPS, "spec_gbps": HBM_PEAK_GBPS,
-            "bytes": n, "best": best, "sweep": results,
+            "bytes": n, "best": best,
+            "sweep_gbps": {f"{r['unroll']}x{r['work_groups']}": round(r["gbps"]) for r in results},
             "method": f"gqa_stream_read_device over {gib} GiB: 16-byte nontemporal loads, 512-thread work-groups, "
                       f"{launches} launches back to back between two events per configuration"}
 
@@ -967,11 +984,10 @@ def cpu_decode_baseline(name: str, budget_s: float, threads: int = 1, pool=None)
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"{len(times)} timed repeats of {'whole steps' if whole else f'{len(sel)} of {len(units)} units'} "
-                   f"({len(units)} (sequence, kv head) units per step) after 1 warm-up, median"
-                   + ("" if whole else f", scaled to the step by attended keys (x{scale:.2f})")
-                   + f"; fp32 NumPy oracle (bf16 words in, stable softmax), {threads} thread(s) x 1 BLAS thread, "
-                   f"seeded inputs cycled from {n_pool} units' data; {sum(times):.1f} s timed"),
+        "sample": (f"median of {len(times)} "
+                   + ("whole steps" if whole else f"{len(sel)}/{len(units)}-unit samples x{scale:.2f} by keys")
+                   + f", fp32 NumPy oracle, {threads} thread(s) x 1 BLAS, inputs cycled from {n_pool} units, "
+                   f"{sum(times):.1f} s"),
         "us_per_step": step_s * 1e6,
         "us_per_step_p95": float(np.percentile(times, 95)) * scale * 1e6,
     }
@@ -1012,8 +1028,8 @@ def cpu_prefill_baseline(name: str, budget_s: float, threads: int = 1) -> dict:
         "unit": "TFLOP/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"{len(times)} whole prompts ({len(sched)} chunks each) after 1 warm-up, median; fp32 NumPy "
-                   f"oracle per KV group, {threads} BLAS thread(s); {sum(times):.1f} s timed"),
+        "sample": (f"median of {len(times)} whole prompts ({len(sched)} chunks), fp32 NumPy oracle per KV group, "
+                   f"{threads} BLAS thread(s), {sum(times):.1f} s"),
         "us_per_prompt": med * 1e6,
         "us_per_prompt_p95": float(np.percentile(times, 95)) * 1e6,
     }
@@ -1286,7 +1302,7 @@ def main() -> int:
     decode_keys = ("us_per_step", "gpu_us_per_step", "gated_gpu_us_per_step", "step_us", "step_gbps", "step_frac_of_peak", "decode_us",
                    "combine_us", "merges_per_step", "kernels_us_per_step", "decode_kernel_bytes",
                    "decode_kernel_gbps", "decode_kernel_frac_of_peak", "kernels_gbps", "tokens_per_s",
-                   "graph_us_per_step", "gate_held", "working_set_bytes", "cache_resident", "residency")
+                   "graph_us_per_step", "gate_held", "working_set_bytes", "cache_resident")
     for name in [x for x in args.others.split(",") if x and x != args.workload]:
         if name.removesuffix(PAGED_SUFFIX) in PREFILL_WORKLOADS:
             others[name] = measure_prefill(name, max(10, args.steps // 2), max(2, args.warmup // 2), args.prefill_wgs,
@@ -1375,10 +1391,12 @@ def main() -> int:
         "launch_floor": floor,
         "cpu_baseline": cpu,
         "environment": collect_environment(),
-        "other_workloads": others,
+        "other_workloads": {k: {f: v for f, v in r.items() if f != "residency"} for k, r in others.items()},
+        "residency_note": ("cache_resident: the workload's bytes fit the 256 MiB Infinity Cache, so after warm-up "
+                           "its steps are served from it and its GB/s are not HBM rates"),
     }
     line["summary"] = summary_lines(args.workload, main_r, cpu, others)
-    print(json.dumps(line), flush=True)
+    print(json.dumps(compact(line), separators=(",", ":")), flush=True)
     for text in line["summary"]:
         print(f"[summary] {text}", file=sys.stderr, flush=True)
     return 0
