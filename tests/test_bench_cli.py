@@ -109,3 +109,18 @@ def test_rolling_append_positions_form_a_ring():
     assert (pos >= 0).all() and (pos < lens[None, :]).all()
     for j, L in enumerate(lens):
         assert sorted(pos[:L, j].tolist()) == list(range(L))
+
+
+def test_compact_rounds_floats_and_keeps_counts_whole():
+    """The printed line rounds floats to 5 significant digits; whole byte counts stored as floats keep
+    every digit, and ints, strings, None and non-finite values pass through."""
+    import math
+
+    sys.path.insert(0, str(ROOT))
+    import bench
+
+    out = bench.compact({"v": 6934.080491501775, "f": 0.8676560901833921, "t": 2148915777.0, "n": 7,
+                         "s": "x", "z": None, "inf": math.inf, "l": [1.23456789, {"u": 309.56884765625}]})
+    assert out["v"] == 6934.1 and out["f"] == 0.86766 and out["l"] == [1.2346, {"u": 309.57}]
+    assert out["t"] == 2148915777 and isinstance(out["t"], int)
+    assert out["n"] == 7 and out["s"] == "x" and out["z"] is None and out["inf"] == math.inf
