@@ -256,6 +256,27 @@ def test_prefill_chunk_after_history_pairs_when_the_grid_fills_the_gpu(paged):
         check_rows(*outs[0], ref, ref_lse)
 
 
+def test_one_causal_8192_token_prompt_sampled_rows():
+    """One causal prefill launch over an 8192-token prompt already in the cache (32q/8kv, D 128: the
+    bench's one-shot shape, several dispatch rounds of the GQA-shared kernel): rows at the start, at
+    the middle and at the end of the prompt, every query head, against the float64 oracle over all
+    their keys; every output row finite."""
+    rng = np.random.default_rng(8192)
+    P = 8192
+    q = bf16_normal(rng, (32, P, 128))
+    k = bf16_normal(rng, (8, P, 128))
+    v = bf16_normal(rng, (8, P, 128))
+    with AttentionAccelerator(max_seq_len=P, max_q_len=P) as acc:
+        acc.load_kv(k, v)
+        print("[p8k] one causal launch over 8192 rows", flush=True)
+        out, lse = acc.prefill_chunk(q, q_pos_base=0, kv_len=P, causal=True, return_lse=True)
+        print(f"[p8k] plan {acc.last_prefill_plan()}", flush=True)
+    assert np.isfinite(orc.bf16_u16_to_fp32(out)).all() and np.isfinite(lse).all()
+    for r0 in (0, 4064, 8128):  # 64 rows each: the first blocks, a middle pair of blocks, the last
+        ref, ref_lse = oracle_for(q[:, r0:r0 + 64], k[:, :r0 + 64], v[:, :r0 + 64], causal=True, q_pos_base=r0)
+        check_rows(out[:, r0:r0 + 64], lse[:, r0:r0 + 64], ref, ref_lse)
+
+
 def test_prefill_rows_without_keys_are_zero():
     rng = np.random.default_rng(9)
     q_len, kv_len = 50, 120
