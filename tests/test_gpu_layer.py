@@ -216,3 +216,28 @@ def test_run_layer_rejects_bad_shapes():
             acc.run_layer(x, wq, wk, wv, rms_eps=float("nan"))
         out = acc.run_layer(x, wq, wk, wv, gamma, rope=False)
         assert out.shape == (8, 4096) and np.isfinite(out).all()
+
+
+def test_layer_at_2048_tokens_sampled_rows():
+    """The Llama-3-8B layer at 2048 tokens (hidden 4096, 32q/8kv, D 128): RMSNorm, the fused QKV
+    projection and RoPE over every row, then one causal prefill launch over them (paired row blocks);
+    rows at the start, middle and end of every head against the float64 chain rounded to bf16 at the
+    stage boundaries, within 3 bf16 ulp as for run_layer."""
+    rng = np.random.default_rng(2048)
+    L = 2048
+    x, wq, wk, wv, gamma = _layer_inputs(rng, L)
+    with AttentionAccelerator(max_seq_len=L, max_q_len=L) as acc:
+        print("[layer] 2048-token stage", flush=True)
+        q, k, v = stage(acc, x, wq, wk, wv, gamma, fused=True)
+        print("[layer] 2048-token causal attention", flush=True)
+        out = acc.prefill_chunk(q, q_pos_base=0, kv_len=L, causal=True)
+        assert acc.last_prefill_plan() == ("paired", 1)
+    y = orc.bf16_rne(lo.rms_norm_exact(x, gamma, 1e-5).astype(np.float32))
+    kc = lo.apply_rope(lo.reshape_to_heads(orc.bf16_rne(lo.project_exact(y, wk).astype(np.float32)), 8, 128), 0)
+    vc = lo.reshape_to_heads(orc.bf16_rne(lo.project_exact(y, wv).astype(np.float32)), 8, 128)
+    for r0 in (0, 992, 1984):  # 64 rows each
+        qc = lo.apply_rope(
+            lo.reshape_to_heads(orc.bf16_rne(lo.project_exact(y[r0:r0 + 64], wq).astype(np.float32)), 32, 128), r0)
+        chain, _ = orc.attention(orc.bf16_u16_to_fp32(qc), orc.bf16_u16_to_fp32(kc[:, :r0 + 64]),
+                                 orc.bf16_u16_to_fp32(vc[:, :r0 + 64]), causal=True, q_pos_base=r0)
+        assert float(orc.row_ulp_error(out[:, r0:r0 + 64], chain).max()) <= 3.0, r0
