@@ -223,13 +223,21 @@ def test_decode_constant_v_is_exact():
         assert np.array_equal(out[0], np.repeat(v0, hq // hkv, axis=0))
 
 
-def _full_size(name):
+def _full_size(name, page_size=0):
     from lara_amd.benchmark import WORKLOADS
     w = WORKLOADS[name]
     rng = np.random.default_rng(w.seed)
     lens = w.lengths()
+    paged = dict(page_size=page_size, n_pages=int(sum(-(-int(n) // page_size) for n in lens)) + 1) if page_size else {}
     with make_engine(w.batch, w.n_q_heads, w.n_kv_heads, w.head_dim, int(lens.max()), max_q_len=1,
-                     scale=w.scale) as eng:
+                     scale=w.scale, **paged) as eng:
+        if page_size:  # every sequence grows a page at a time, round robin: their pages interleave
+            grown = [0] * w.batch
+            while any(g < n for g, n in zip(grown, lens)):
+                for b, n in enumerate(lens):
+                    if grown[b] < n:
+                        grown[b] = min(int(n), grown[b] + page_size)
+                        eng.reserve(b, grown[b])
         kc, vc = fill_cache(eng, rng, w.batch, w.n_kv_heads, w.head_dim, lens, w.amplitude,
                             (w.outlier_fraction, w.outlier_scale))
         q = bf16_normal(rng, (w.batch, w.n_q_heads, w.head_dim), w.amplitude)
@@ -242,6 +250,12 @@ def _full_size(name):
 
 def test_decode_full_size_ns():
     _full_size("decode-b64-ctx8192")
+
+
+def test_decode_full_size_ns_on_scattered_pages():
+    """The north-star decode on a paged cache of 64-row pages, every sequence's pages interleaved
+    with the others' (the bench's NS-paged line), against the oracle at full size."""
+    _full_size("decode-b64-ctx8192", page_size=64)
 
 
 def test_decode_full_size_c3_ragged():
